@@ -1,0 +1,223 @@
+#!/usr/bin/env python3
+"""Benchmark of the MXFP8 grouped-GEMM path on one MI355X.
+
+Headline ("C2"): DeepSeek-V3 gate+up forward on one
+GPU's expert share — 32 experts, K=7168, N=4096, 65536 tokens routed by
+Multinomial(Dirichlet(1)) — MXFP8 e4m3 operands with E8M0 1x32 scales, bf16
+output, fp32 accumulation.  A step is one grouped-GEMM launch over the whole
+batch with operands already resident in HBM (quantised once before timing).
+value = 2 * tokens * N * K / step time, in TFLOPS.
+
+The same run also times, as secondary components: the C3 down-projection
+forward, the C4 weight gradient (fp32 dW), the bf16->MXFP8 casts, and the
+reference's CPU path (dequantise + per-group fp32 matmul with torch on the
+host cores) on a bounded sample of C2.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "mxfp8-grouped-gemm_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_MXFP8_TFLOPS = 5000.0  # MI355X dense fp8 / MXFP8 MFMA peak (published)
+PEAK_HBM_GBPS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_launches(fn, steps, warmup, torch):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms per launch
+
+
+def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, budget_s=12.0):
+    """The reference's CPU path on a bounded sample of the workload: whole
+    experts of C2, in order, until `budget_s` of CPU work has run."""
+    import torch
+    from oracle import oracle as O
+
+    done_tokens = 0
+    t_total = 0.0
+    experts = 0
+    b = 0
+    for g, e in enumerate(ends_np.tolist()):
+        if e > b:
+            a_q = xq[b:e].cpu().view(torch.uint8)
+            a_s = xs[b:e].cpu()
+            w_q = wq[g:g + 1].cpu().view(torch.uint8)
+            w_s = ws[g:g + 1].cpu()
+            t0 = time.perf_counter()
+            O.cpu_baseline_fwd(a_q, a_s, w_q, w_s, torch.tensor([e - b], dtype=torch.int32))
+            t_total += time.perf_counter() - t0
+            done_tokens += e - b
+            experts += 1
+        b = e
+        if t_total >= budget_s:
+            break
+    tflops = 2.0 * done_tokens * n * k / t_total / 1e12
+    return {
+        "value": round(tflops, 4),
+        "unit": "TFLOPS",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"C2 experts 0..{experts - 1} ({done_tokens} tokens x N={n} x K={k}): "
+                  f"dequantise e4m3*2^(b-127) to fp32, per-group fp32 matmul, {t_total:.1f} s",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["all", "fwd"], default="all",
+                    help="fwd: time only the headline forward (for profiler runs)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the MXFP8 grouped GEMM shards by expert and "
+              "this build runs a single GPU's expert share; --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import mxfp8gg
+    from mxfp8gg import workloads
+
+    dev = torch.device("cuda:0")
+    mxfp8gg.load_library()
+
+    # ---- headline: C2 forward ---------------------------------------------
+    log("C2: generating and quantising operands")
+    x, w, sizes = workloads.c2(dev)
+    ends_np = workloads.ends_of(sizes)
+    ends = torch.from_numpy(ends_np).to(dev)
+    xq, xs = mxfp8gg.to_mxfp8_dim0(x)
+    wq, ws = mxfp8gg.to_mxfp8_dim0(w)
+    M, K = x.shape
+    E, N, _ = w.shape
+    flops = workloads.gemm_flops(M, N, K)
+
+    quant_c2 = None
+    if args.only == "all":
+        # bf16 -> MXFP8 dim0 on X: algorithmic bytes = 2 (in) + 1 (payload) + 1/32 (scale) per element
+        ms_q = time_launches(lambda: mxfp8gg.to_mxfp8_dim0(x), 20, 3, torch)
+        qbytes = x.numel() * (2 + 1 + 1 / 32)
+        quant_c2 = {"ms": round(ms_q, 4), "GBps": round(qbytes / ms_q / 1e6, 1),
+                    "frac_of_8TBps": round(qbytes / ms_q / 1e6 / PEAK_HBM_GBPS, 4)}
+    del x, w
+
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        mxfp8gg.grouped_mm(xq, wq, ends, xs, ws, out=out)
+
+    log(f"C2: timing {args.steps} steps after {args.warmup} warm-up")
+    ms = time_launches(step, args.steps, args.warmup, torch)
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    components = {}
+    if args.only == "all":
+        components["quant_dim0_c2_x"] = quant_c2
+        # ---- C3 forward (down projection) --------------------------------
+        log("C3: down-projection forward")
+        h, w3, s3 = workloads.c3(dev)
+        e3 = torch.from_numpy(workloads.ends_of(s3)).to(dev)
+        hq, hs = mxfp8gg.to_mxfp8_dim0(h)
+        w3q, w3s = mxfp8gg.to_mxfp8_dim0(w3)
+        del h, w3
+        o3 = torch.empty((hq.shape[0], w3q.shape[1]), dtype=torch.bfloat16, device=dev)
+        ms3 = time_launches(lambda: mxfp8gg.grouped_mm(hq, w3q, e3, hs, w3s, out=o3), 20, 5,
+                            torch)
+        f3 = workloads.gemm_flops(hq.shape[0], w3q.shape[1], hq.shape[1])
+        components["fwd_c3"] = {"ms": round(ms3, 4), "tflops": round(f3 / ms3 / 1e9, 1),
+                                "frac_of_peak": round(f3 / ms3 / 1e9 / PEAK_MXFP8_TFLOPS, 4)}
+        del hq, hs, w3q, w3s, o3
+        # ---- C4 wgrad -------------------------------------------------------
+        log("C4: weight gradient")
+        dy, x4, s4 = workloads.c4(dev)
+        e4 = torch.from_numpy(workloads.ends_of(s4)).to(dev)
+        ms_d1 = time_launches(lambda: mxfp8gg.to_mxfp8_dim1(dy, e4), 10, 2, torch)
+        go, gos, pad = mxfp8gg.to_mxfp8_dim1(dy, e4)
+        ia, ias, _ = mxfp8gg.to_mxfp8_dim1(x4, e4)
+        d1bytes = dy.numel() * (2 + 1 + 1 / 32)
+        components["quant_dim1_c4_dy"] = {"ms": round(ms_d1, 4),
+                                          "GBps": round(d1bytes / ms_d1 / 1e6, 1)}
+        n4, k4 = dy.shape[1], x4.shape[1]
+        del dy, x4
+        dw = torch.empty((32, n4, k4), dtype=torch.float32, device=dev)
+        ms4 = time_launches(
+            lambda: mxfp8gg.grouped_wgrad(go, ia, pad, gos, ias, out_dtype=torch.float32, out=dw),
+            10, 3, torch)
+        f4 = workloads.gemm_flops(int(s4.sum()), n4, k4)
+        components["wgrad_c4"] = {"ms": round(ms4, 4), "tflops": round(f4 / ms4 / 1e9, 1),
+                                  "frac_of_peak": round(f4 / ms4 / 1e9 / PEAK_MXFP8_TFLOPS, 4),
+                                  "out": "fp32 [32, 4096, 7168]"}
+        del go, gos, ia, ias, dw
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_grouped_fwd_c2.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu and args.only == "all":
+        log("CPU baseline (reference CPU path on a bounded sample)")
+        cpu = cpu_baseline(xq, xs, wq, ws, ends_np, N, K)
+
+    line = {
+        "metric": "MXFP8 grouped-GEMM TFLOPS fwd & wgrad, DSv3 32-expert shape; % of MFMA peak",
+        "value": round(tflops, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp8_e4m3 (E8M0 1x32 scales, fp32 accumulate, bf16 out)",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2: DSv3 gate+up grouped forward, 32 local experts, K=7168, N=4096, "
+                        "65536 tokens, Dirichlet(1) routing, seed 0",
+            "experts": E, "tokens": M, "N": N, "K": K,
+            "group_sizes_min_max": [int(sizes.min()), int(sizes.max())],
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": PEAK_MXFP8_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_MXFP8_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel": "k_grouped_fwd<true,false> (one launch per step)",
+        },
+        "cpu_baseline": cpu,
+        "components": components,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

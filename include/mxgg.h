@@ -1,0 +1,148 @@
+/*
+ * mxgg.h — C ABI of libmxgg.so, the MI355X (gfx950) MXFP8 grouped-GEMM library.
+ *
+ * Every entry point is `extern "C"`, takes plain device pointers, element
+ * counts and leading dimensions, launches asynchronously on the caller's HIP
+ * stream (passed as `void*`, i.e. a `hipStream_t`), never allocates or frees
+ * device memory, never synchronises the host, and returns an `mxgg_status`.
+ * No C++ exception crosses the boundary.  On error a human readable reason is
+ * available from `mxgg_last_error()` (thread local).
+ *
+ * Data formats (OCP Microscaling v1.0):
+ *   payload  : float8 e4m3fn, one byte per element (torch.float8_e4m3fn)
+ *   scale    : E8M0, one byte b per block of 32 payload elements along the
+ *              contraction dimension, meaning 2^(b-127); 0xFF is NaN
+ *   bf16     : bfloat16, two bytes per element
+ * Leading dimensions (`ld*`) are in ELEMENTS of the array they describe.
+ * Groups ("experts") are described by `group_ends[num_groups]`, int32,
+ * cumulative end offsets (group g covers [group_ends[g-1], group_ends[g]),
+ * group 0 starts at 0) — the convention of torch._grouped_mm and of the
+ * reference's callers (e2e_bench.py:245, wgrad_fused.py:64).  Empty groups are
+ * allowed.  `group_ends` lives in device memory and is read only on the GPU.
+ */
+#ifndef MXGG_H
+#define MXGG_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXGG_ABI_VERSION 1
+
+typedef enum mxgg_status {
+  MXGG_OK = 0,
+  MXGG_ERR_INVALID_ARGUMENT = 1, /* null pointer, unknown enum value          */
+  MXGG_ERR_SHAPE = 2,            /* negative / inconsistent sizes, K % 32 != 0 */
+  MXGG_ERR_ALIGNMENT = 3,        /* pointer or leading dimension misaligned    */
+  MXGG_ERR_UNSUPPORTED = 4,      /* size outside the supported envelope        */
+  MXGG_ERR_DEVICE = 5,           /* no HIP device / not gfx950                 */
+  MXGG_ERR_LAUNCH = 6            /* kernel launch reported an error            */
+} mxgg_status;
+
+typedef enum mxgg_scale_mode {
+  MXGG_SCALE_RCEIL = 0, /* b = ceil(log2(amax/448)) + 127   (recipe "mxfp8_rceil") */
+  MXGG_SCALE_FLOOR = 1  /* b = floor(log2(amax)) - 8 + 127  (OCP MX v1.0 rule)      */
+} mxgg_scale_mode;
+
+typedef enum mxgg_out_dtype {
+  MXGG_OUT_BF16 = 0,
+  MXGG_OUT_F32 = 1
+} mxgg_out_dtype;
+
+/* ABI version of the loaded library (MXGG_ABI_VERSION at build time). */
+int mxgg_abi_version(void);
+
+/* Static string naming a status code. */
+const char* mxgg_status_string(int status);
+
+/* Detailed message for the last non-OK status returned on this thread. */
+const char* mxgg_last_error(void);
+
+/*
+ * Row-wise MXFP8 cast: 1x32 blocks along the last (contiguous) dimension.
+ *   x      : bf16 [rows, cols], row stride ldx
+ *   q      : e4m3 [rows, cols], row stride ldq
+ *   scales : E8M0 [rows, cols/32], row stride lds
+ * cols % 32 == 0.  Payload = RNE_e4m3(clamp(x * 2^(127-b), -448, 448)).
+ * Replaces torchao's triton_to_mxfp8_dim0 (called by the reference's trainer
+ * path, port_mxfp8.py:43-49) and the eager `.to(torch.float8_e4m3fn)` casts on
+ * the forward path (e2e_bench.py:238-243, fused_fwd.py:274-275).
+ */
+int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                    void* q, int64_t ldq, void* scales, int64_t lds,
+                    int scale_mode, void* stream);
+
+/*
+ * Token-axis (column-wise) MXFP8 cast with per-group block restart, written
+ * transposed: 1x32 blocks run along `rows` (tokens) and never straddle a group
+ * boundary; each group is zero-padded to a multiple of 32 tokens.
+ *   x              : bf16 [rows, cols], row stride ldx
+ *   group_ends     : int32 [num_groups] cumulative token ends (device), or NULL
+ *                    for a single group covering all rows
+ *   rows_pad_cap   : number of padded token columns the outputs can hold; must
+ *                    be >= round_up(rows + 31*num_groups, 32) (NULL groups: round_up(rows,32))
+ *   qt             : e4m3 [cols, rows_pad_cap], row stride ldqt
+ *   scales_t       : E8M0 [cols, rows_pad_cap/32], row stride ldst
+ *   group_ends_pad : int32 [num_groups] padded cumulative ends (device, written)
+ *                    or NULL when group_ends is NULL
+ * Columns past the padded total are written as zero payload / 0x7F scale.
+ * Replaces torchao's triton_to_mxfp8_dim1 (port_mxfp8.py:43) plus the
+ * transpose-and-stack copies of wgrad_fused.py:48-62 / e2e_bench.py:317-328.
+ */
+int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                    const int32_t* group_ends, int64_t num_groups,
+                    int64_t rows_pad_cap, void* qt, int64_t ldqt,
+                    void* scales_t, int64_t ldst, int32_t* group_ends_pad,
+                    int scale_mode, void* stream);
+
+/*
+ * Forward grouped GEMM  out[rows of g] = A[rows of g] . W[g]^T  (fp32 accumulate).
+ *   a        : e4m3 [M, K], row stride lda
+ *   a_scales : E8M0 [M, K/32], row stride ldas                (or NULL)
+ *   w        : e4m3 [E, N, K]: expert g at w + g*w_group_stride, row stride ldw
+ *   w_scales : E8M0 [E, N, K/32]: expert g at + g*ws_group_stride, row stride ldws (or NULL)
+ *   group_ends : int32 [num_groups] (device) or NULL for one group of M rows
+ *   out      : [M, N] bf16 or f32 (out_dtype), row stride ldo
+ * a_scales and w_scales are both given or both NULL (NULL = every scale 1.0,
+ * E8M0 byte 0x7F).  K % 32 == 0.  Rows past the last group end are untouched.
+ * Replaces fused_grouped_fwd (fused_fwd.py:172-229) + its kernel
+ * (fused_fwd.py:18-167), and fwd_ge (fwd_final.py:121-131) with num_groups=1.
+ */
+int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                     const void* w, int64_t w_group_stride, int64_t ldw,
+                     const void* w_scales, int64_t ws_group_stride, int64_t ldws,
+                     const int32_t* group_ends, int64_t num_groups,
+                     int64_t M, int64_t N, int64_t K,
+                     void* out, int64_t ldo, int out_dtype, void* stream);
+
+/*
+ * Weight-gradient grouped GEMM, contracting over the ragged token dimension:
+ *   dw[g] = sum over tokens t of group g of  go_t[:, t] (x) ia_t[:, t]
+ * i.e. dW_g = dY_g^T . X_g with both operands stored token-contiguous.
+ *   go_t        : e4m3 [N, M], row stride ldgo  (dY transposed)
+ *   go_scales_t : E8M0 [N, M/32], row stride ldgos        (or NULL)
+ *   ia_t        : e4m3 [K, M], row stride ldia  (X transposed)
+ *   ia_scales_t : E8M0 [K, M/32], row stride ldias        (or NULL)
+ *   group_ends  : int32 [num_groups] token ends (device); every end must be a
+ *                 multiple of 32 when scales are given (the padded layout that
+ *                 mxgg_quant_dim1 produces), so a scale block never straddles
+ *                 two groups
+ *   dw          : [num_groups, N, K] bf16 or f32, contiguous; empty groups are
+ *                 written with zeros
+ * Replaces wgrad_fused / wgrad_prepare + wgrad_kernel (wgrad_fused.py:34-112),
+ * which restack operands per group and call the forward kernel.
+ */
+int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, int64_t ldgos,
+                       const void* ia_t, int64_t ldia, const void* ia_scales_t, int64_t ldias,
+                       const int32_t* group_ends, int64_t num_groups,
+                       int64_t M, int64_t N, int64_t K,
+                       void* dw, int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXGG_H */

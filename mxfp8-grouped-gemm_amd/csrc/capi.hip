@@ -1,0 +1,272 @@
+// extern "C" entry points of libmxgg.so: argument validation, then launch.
+// No entry point allocates, frees or synchronises; all launches go to the
+// caller's stream.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "mxgg_internal.h"
+
+namespace mxgg {
+
+namespace {
+thread_local char g_last_error[512] = "";
+
+constexpr int64_t kMaxGroupsAbi = 1024;
+constexpr int64_t kMaxBufferBytes = 0x7FFFFFF0LL;  // one buffer resource per operand
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace
+
+int set_error(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int device_cu_count() {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)cache.size() <= dev) cache.resize(dev + 1, 0);
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return -1;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+static int check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    return set_error(MXGG_ERR_LAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return MXGG_OK;
+}
+
+}  // namespace mxgg
+
+using namespace mxgg;
+
+extern "C" {
+
+int mxgg_abi_version(void) { return MXGG_ABI_VERSION; }
+
+const char* mxgg_status_string(int status) {
+  switch (status) {
+    case MXGG_OK: return "ok";
+    case MXGG_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case MXGG_ERR_SHAPE: return "bad shape";
+    case MXGG_ERR_ALIGNMENT: return "misaligned pointer or leading dimension";
+    case MXGG_ERR_UNSUPPORTED: return "unsupported size";
+    case MXGG_ERR_DEVICE: return "device error";
+    case MXGG_ERR_LAUNCH: return "kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+const char* mxgg_last_error(void) { return g_last_error; }
+
+int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx, void* q, int64_t ldq,
+                    void* scales, int64_t lds, int scale_mode, void* stream) {
+  const int mode = scale_mode & 0xFF;
+  if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim0: unknown scale_mode %d", scale_mode);
+  if (rows < 0 || cols < 0)
+    return set_error(MXGG_ERR_SHAPE, "quant_dim0: negative size rows=%lld cols=%lld",
+                     (long long)rows, (long long)cols);
+  if (cols % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "quant_dim0: cols=%lld is not a multiple of 32",
+                     (long long)cols);
+  if (rows == 0 || cols == 0) return MXGG_OK;
+  if (!x || !q || !scales)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim0: null pointer");
+  if (ldx < cols || ldq < cols || lds < cols / 32)
+    return set_error(MXGG_ERR_SHAPE, "quant_dim0: leading dimension smaller than the row");
+  if (!aligned16(x) || !aligned16(q) || ldx % 8 != 0 || ldq % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(q) & 7u) != 0)
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "quant_dim0: x and q must be 16-byte aligned, ldx and ldq multiples of 8");
+  return check_launch(launch_quant_dim0(static_cast<const uint16_t*>(x), rows, cols, ldx,
+                                        static_cast<uint8_t*>(q), ldq,
+                                        static_cast<uint8_t*>(scales), lds, scale_mode,
+                                        static_cast<hipStream_t>(stream)),
+                      "quant_dim0");
+}
+
+int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                    const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap,
+                    void* qt, int64_t ldqt, void* scales_t, int64_t ldst,
+                    int32_t* group_ends_pad, int scale_mode, void* stream) {
+  const int mode = scale_mode & 0xFF;
+  if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim1: unknown scale_mode %d", scale_mode);
+  if (rows < 0 || cols < 0 || rows_pad_cap < 0)
+    return set_error(MXGG_ERR_SHAPE, "quant_dim1: negative size");
+  if (cols % 8 != 0)
+    return set_error(MXGG_ERR_SHAPE, "quant_dim1: cols=%lld is not a multiple of 8",
+                     (long long)cols);
+  if (rows_pad_cap % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "quant_dim1: rows_pad_cap=%lld is not a multiple of 32",
+                     (long long)rows_pad_cap);
+  if (group_ends) {
+    if (num_groups < 1 || num_groups > kMaxGroupsAbi)
+      return set_error(MXGG_ERR_UNSUPPORTED, "quant_dim1: num_groups=%lld outside [1, %lld]",
+                       (long long)num_groups, (long long)kMaxGroupsAbi);
+    if (!group_ends_pad)
+      return set_error(MXGG_ERR_INVALID_ARGUMENT,
+                       "quant_dim1: group_ends_pad is required with group_ends");
+  }
+  const int64_t groups = group_ends ? num_groups : 1;
+  const int64_t need = ((rows + 31 * (group_ends ? groups : 0) + 31) / 32) * 32;
+  if (rows_pad_cap < need)
+    return set_error(MXGG_ERR_SHAPE, "quant_dim1: rows_pad_cap=%lld < required %lld",
+                     (long long)rows_pad_cap, (long long)need);
+  if (cols == 0 || rows_pad_cap == 0) return MXGG_OK;
+  if (!x && rows > 0) return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim1: null x");
+  if (!qt || !scales_t) return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim1: null output");
+  if (ldx < cols || ldqt < rows_pad_cap || ldst < rows_pad_cap / 32)
+    return set_error(MXGG_ERR_SHAPE, "quant_dim1: leading dimension smaller than the row");
+  if ((x && !aligned16(x)) || !aligned16(qt) || ldx % 8 != 0 || ldqt % 16 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "quant_dim1: x and qt must be 16-byte aligned, ldx % 8 == 0, ldqt % 16 == 0");
+  if (rows > INT32_MAX || rows_pad_cap > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "quant_dim1: more than 2^31 rows");
+  return check_launch(
+      launch_quant_dim1(static_cast<const uint16_t*>(x), rows, cols, ldx, group_ends, groups,
+                        rows_pad_cap, static_cast<uint8_t*>(qt), ldqt,
+                        static_cast<uint8_t*>(scales_t), ldst, group_ends_pad, scale_mode,
+                        static_cast<hipStream_t>(stream)),
+      "quant_dim1");
+}
+
+int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                     const void* w, int64_t w_group_stride, int64_t ldw, const void* w_scales,
+                     int64_t ws_group_stride, int64_t ldws, const int32_t* group_ends,
+                     int64_t num_groups, int64_t M, int64_t N, int64_t K, void* out, int64_t ldo,
+                     int out_dtype, void* stream) {
+  if (out_dtype != MXGG_OUT_BF16 && out_dtype != MXGG_OUT_F32)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd: unknown out_dtype %d", out_dtype);
+  if (M < 0 || N < 0 || K < 0)
+    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: negative size");
+  if (K % 32 != 0 || K == 0)
+    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: K=%lld must be a positive multiple of 32",
+                     (long long)K);
+  const bool scaled = a_scales != nullptr;
+  if ((a_scales == nullptr) != (w_scales == nullptr))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT,
+                     "grouped_fwd: a_scales and w_scales must both be given or both be NULL");
+  const int64_t E = group_ends ? num_groups : 1;
+  if (E < 1 || E > kMaxGroupsAbi)
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_fwd: num_groups=%lld outside [1, %lld]",
+                     (long long)num_groups, (long long)kMaxGroupsAbi);
+  if (M == 0 || N == 0) return MXGG_OK;
+  if (!a || !w || !out) return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd: null pointer");
+  if (lda < K || ldw < K || ldo < N || (scaled && (ldas < K / 32 || ldws < K / 32)))
+    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: leading dimension smaller than the row");
+  if (E > 1 && w_group_stride < N * ldw)
+    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: w_group_stride smaller than one expert");
+  if (scaled && E > 1 && ws_group_stride < N * ldws)
+    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: ws_group_stride smaller than one expert");
+  if (!aligned16(a) || !aligned16(w) || lda % 16 != 0 || ldw % 16 != 0 ||
+      (E > 1 && w_group_stride % 16 != 0))
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "grouped_fwd: a and w must be 16-byte aligned with lda, ldw and the expert "
+                     "stride multiples of 16");
+  const int esz = out_dtype == MXGG_OUT_F32 ? 4 : 2;
+  if ((reinterpret_cast<uintptr_t>(out) % (4 * esz)) != 0 || ldo % 4 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "grouped_fwd: out must be aligned to 4 elements with ldo % 4 == 0");
+  if ((M - 1) * lda + K > kMaxBufferBytes || (N - 1) * ldw + K > kMaxBufferBytes)
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_fwd: operand larger than 2 GiB");
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_fwd: dimension above 2^31");
+  FwdArgs args;
+  args.a = static_cast<const uint8_t*>(a);
+  args.as = static_cast<const uint8_t*>(a_scales);
+  args.w = static_cast<const uint8_t*>(w);
+  args.ws = static_cast<const uint8_t*>(w_scales);
+  args.group_ends = group_ends;
+  args.out = out;
+  args.lda = lda;
+  args.ldas = scaled ? ldas : 0;
+  args.w_gstride = w_group_stride;
+  args.ldw = ldw;
+  args.ws_gstride = scaled ? ws_group_stride : 0;
+  args.ldws = scaled ? ldws : 0;
+  args.ldo = ldo;
+  args.M = (int32_t)M;
+  args.N = (int32_t)N;
+  args.K = (int32_t)K;
+  args.E = (int32_t)E;
+  args.out_f32 = out_dtype == MXGG_OUT_F32;
+  args.scaled = scaled;
+  return check_launch(launch_grouped_fwd(args, static_cast<hipStream_t>(stream)), "grouped_fwd");
+}
+
+int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, int64_t ldgos,
+                       const void* ia_t, int64_t ldia, const void* ia_scales_t, int64_t ldias,
+                       const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t N,
+                       int64_t K, void* dw, int out_dtype, void* stream) {
+  if (out_dtype != MXGG_OUT_BF16 && out_dtype != MXGG_OUT_F32)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: unknown out_dtype %d", out_dtype);
+  if (M < 0 || N < 0 || K < 0)
+    return set_error(MXGG_ERR_SHAPE, "grouped_wgrad: negative size");
+  if (num_groups < 1 || num_groups > kMaxGroupsAbi)
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_wgrad: num_groups=%lld outside [1, %lld]",
+                     (long long)num_groups, (long long)kMaxGroupsAbi);
+  if (!group_ends)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: group_ends is required");
+  const bool scaled = go_scales_t != nullptr;
+  if ((go_scales_t == nullptr) != (ia_scales_t == nullptr))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT,
+                     "grouped_wgrad: go_scales_t and ia_scales_t must both be given or both NULL");
+  if (M % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "grouped_wgrad: token count M=%lld not a multiple of 32",
+                     (long long)M);
+  if (N == 0 || K == 0) return MXGG_OK;
+  if (!dw) return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: null dw");
+  if (M > 0 && (!go_t || !ia_t))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: null operand");
+  if (ldgo < M || ldia < M || (scaled && (ldgos < M / 32 || ldias < M / 32)))
+    return set_error(MXGG_ERR_SHAPE, "grouped_wgrad: leading dimension smaller than the row");
+  if ((go_t && !aligned16(go_t)) || (ia_t && !aligned16(ia_t)) || ldgo % 16 != 0 ||
+      ldia % 16 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "grouped_wgrad: operands must be 16-byte aligned with ld % 16 == 0");
+  const int esz = out_dtype == MXGG_OUT_F32 ? 4 : 2;
+  if ((reinterpret_cast<uintptr_t>(dw) % (esz * 4)) != 0 || K % 4 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT, "grouped_wgrad: dw must be vector aligned, K % 4 == 0");
+  if ((N - 1) * ldgo + M > kMaxBufferBytes || (K - 1) * ldia + M > kMaxBufferBytes)
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_wgrad: operand larger than 2 GiB");
+  if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_wgrad: dimension above 2^31");
+  WgradArgs args;
+  args.go = static_cast<const uint8_t*>(go_t);
+  args.gos = static_cast<const uint8_t*>(go_scales_t);
+  args.ia = static_cast<const uint8_t*>(ia_t);
+  args.ias = static_cast<const uint8_t*>(ia_scales_t);
+  args.group_ends = group_ends;
+  args.dw = dw;
+  args.ldgo = ldgo;
+  args.ldgos = scaled ? ldgos : 0;
+  args.ldia = ldia;
+  args.ldias = scaled ? ldias : 0;
+  args.M = (int32_t)M;
+  args.N = (int32_t)N;
+  args.K = (int32_t)K;
+  args.E = (int32_t)num_groups;
+  args.out_f32 = out_dtype == MXGG_OUT_F32;
+  args.scaled = scaled;
+  return check_launch(launch_grouped_wgrad(args, static_cast<hipStream_t>(stream)),
+                      "grouped_wgrad");
+}
+
+}  // extern "C"

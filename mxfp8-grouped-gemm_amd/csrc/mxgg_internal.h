@@ -1,0 +1,70 @@
+// Internal declarations shared by the HIP translation units of libmxgg.so.
+// gfx950 (CDNA4) only: wave64, scaled MFMA (f8f6f4), 160 KB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mxgg.h"
+
+namespace mxgg {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Flag OR-ed into scale_mode: use the bit-level software e4m3 encoder instead
+// of v_cvt_pk_fp8_f32.  Both must give identical bytes; the flag exists so the
+// GPU tests can check the hardware convert against an independent encoder.
+constexpr int kCvtSoftwareFlag = 0x100;
+
+// Error reporting (capi.hip).
+int set_error(int status, const char* fmt, ...);
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+// ---------------------------------------------------------------------------
+// Launchers (implemented in quant.hip / gemm.hip).  Arguments are validated by
+// the C-ABI layer before these are called.
+// ---------------------------------------------------------------------------
+hipError_t launch_quant_dim0(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                             uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int mode,
+                             hipStream_t stream);
+
+hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                             const int32_t* group_ends, int64_t num_groups,
+                             int64_t rows_pad_cap, uint8_t* qt, int64_t ldqt, uint8_t* st,
+                             int64_t ldst, int32_t* group_ends_pad, int mode,
+                             hipStream_t stream);
+
+struct FwdArgs {
+  const uint8_t* a;
+  const uint8_t* as;
+  const uint8_t* w;
+  const uint8_t* ws;
+  const int32_t* group_ends;  // nullptr = one group of M rows
+  void* out;
+  int64_t lda, ldas, w_gstride, ldw, ws_gstride, ldws, ldo;
+  int32_t M, N, K, E;
+  int32_t out_f32;
+  int32_t scaled;
+};
+hipError_t launch_grouped_fwd(const FwdArgs& args, hipStream_t stream);
+
+struct WgradArgs {
+  const uint8_t* go;   // [N, M] token-contiguous
+  const uint8_t* gos;  // [N, M/32]
+  const uint8_t* ia;   // [K, M]
+  const uint8_t* ias;  // [K, M/32]
+  const int32_t* group_ends;
+  void* dw;            // [E, N, K]
+  int64_t ldgo, ldgos, ldia, ldias;
+  int32_t M, N, K, E;
+  int32_t out_f32;
+  int32_t scaled;
+};
+hipError_t launch_grouped_wgrad(const WgradArgs& args, hipStream_t stream);
+
+}  // namespace mxgg

@@ -1,0 +1,263 @@
+// bf16 -> MXFP8 (e4m3 payload + E8M0 1x32 block scale) casts for gfx950.
+//
+// Both kernels are HBM-bound streaming kernels: every input byte is read once
+// and every output byte written once, with 16-byte vector accesses.
+//   dim0 : blocks along the contiguous dimension (forward operands, K-blocks).
+//   dim1 : blocks along the row (token) dimension, restarting at every group
+//          boundary, written transposed and zero-padded per group to a
+//          multiple of 32 tokens (wgrad operands).
+#include "mx_device.h"
+#include "mxgg_internal.h"
+
+namespace mxgg {
+namespace {
+
+constexpr int kMaxGroups = 1024;
+
+// ---------------------------------------------------------------------------
+// dim0.  A wave covers 64 chunks of 8 bf16 (16 B) of one row; the four lanes
+// of a quad hold one 32-element block and combine their amax with two xor
+// shuffles.  Each wave handles 4 rows per trip, a block 16 rows.
+// ---------------------------------------------------------------------------
+template <int MODE, bool SW>
+__global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__ x, int64_t rows,
+                                                    int cols8, int64_t ldx,
+                                                    uint8_t* __restrict__ q, int64_t ldq,
+                                                    uint8_t* __restrict__ s, int64_t lds) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int cc = blockIdx.x * 64 + lane;  // chunk column
+  const bool col_ok = cc < cols8;         // whole quads share col_ok (cols8 % 4 == 0)
+  for (int64_t r0 = (int64_t)blockIdx.y * 16 + wave * 4; r0 < rows; r0 += (int64_t)gridDim.y * 16) {
+    uint4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t r = r0 + u;
+      if (col_ok && r < rows) {
+        v[u] = *reinterpret_cast<const uint4*>(x + r * ldx + (int64_t)cc * 8);
+      } else {
+        v[u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t r = r0 + u;
+      uint32_t am = amax16_of_word(v[u].x);
+      am = max(am, amax16_of_word(v[u].y));
+      am = max(am, amax16_of_word(v[u].z));
+      am = max(am, amax16_of_word(v[u].w));
+      am = max(am, (uint32_t)__shfl_xor((int)am, 1));
+      am = max(am, (uint32_t)__shfl_xor((int)am, 2));
+      const uint32_t b = e8m0_from_amax16<MODE>(am);
+      const int e = payload_exponent<MODE>(b);
+      float f[8];
+      bf16x2_to_scaled<MODE>(v[u].x, b, e, f[0], f[1]);
+      bf16x2_to_scaled<MODE>(v[u].y, b, e, f[2], f[3]);
+      bf16x2_to_scaled<MODE>(v[u].z, b, e, f[4], f[5]);
+      bf16x2_to_scaled<MODE>(v[u].w, b, e, f[6], f[7]);
+      uint2 o;
+      o.x = e4m3_pack4<SW>(f[0], f[1], f[2], f[3]);
+      o.y = e4m3_pack4<SW>(f[4], f[5], f[6], f[7]);
+      if (col_ok && r < rows) {
+        *reinterpret_cast<uint2*>(q + r * ldq + (int64_t)cc * 8) = o;
+        if ((lane & 3) == 0) s[r * lds + (cc >> 2)] = (uint8_t)b;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Block-wide prefix over group sizes, kept in LDS.
+//   ends_s[g]  : clamped end of group g (unpadded)
+//   pend_s[g]  : padded cumulative end (each group rounded up to 32 tokens)
+// ---------------------------------------------------------------------------
+__device__ void groups_to_lds(const int32_t* __restrict__ ends, int E, int64_t rows,
+                              int32_t* ends_s, int32_t* pend_s, int32_t* tmp /*256*/) {
+  const int t = threadIdx.x;
+  // Each thread owns up to 4 consecutive groups.
+  int32_t local_pad[4];
+  int32_t sum = 0;
+  const int g0 = t * 4;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int g = g0 + u;
+    int32_t pad = 0;
+    if (g < E) {
+      int64_t e = ends[g];
+      int64_t st = g > 0 ? (int64_t)ends[g - 1] : 0;
+      e = e < 0 ? 0 : (e > rows ? rows : e);
+      st = st < 0 ? 0 : (st > rows ? rows : st);
+      const int64_t sz = e > st ? e - st : 0;
+      ends_s[g] = (int32_t)e;
+      pad = (int32_t)((sz + 31) & ~(int64_t)31);
+    }
+    local_pad[u] = pad;
+    sum += pad;
+  }
+  tmp[t] = sum;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int32_t add = t >= off ? tmp[t - off] : 0;
+    __syncthreads();
+    tmp[t] += add;
+    __syncthreads();
+  }
+  int32_t run = t > 0 ? tmp[t - 1] : 0;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int g = g0 + u;
+    run += local_pad[u];
+    if (g < E) pend_s[g] = run;
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// dim1.  Block = 128 padded token columns x 64 features.  Load phase gathers
+// token rows (16 B per thread-chunk, coalesced along features) and stores them
+// transposed into LDS; compute phase gives each thread one feature and one
+// 32-token block, so four consecutive lanes write 128 contiguous output bytes.
+// ---------------------------------------------------------------------------
+template <int MODE, bool SW>
+__global__ __launch_bounds__(256) void k_quant_dim1(
+    const uint16_t* __restrict__ x, int64_t rows, int cols, int64_t ldx,
+    const int32_t* __restrict__ ends, int E, int64_t rows_pad_cap, uint8_t* __restrict__ qt,
+    int64_t ldqt, uint8_t* __restrict__ st, int64_t ldst, int32_t* __restrict__ ends_pad_out) {
+  __shared__ __align__(16) uint16_t tile[64][136];
+  __shared__ int32_t ends_s[kMaxGroups];
+  __shared__ int32_t pend_s[kMaxGroups];
+  __shared__ int32_t tmp[256];
+
+  const int t = threadIdx.x;
+  if (ends != nullptr) {
+    groups_to_lds(ends, E, rows, ends_s, pend_s, tmp);
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+      for (int g = t; g < E; g += 256) ends_pad_out[g] = pend_s[g];
+    }
+  }
+  const int64_t p0 = (int64_t)blockIdx.x * 128;
+  const int f0 = blockIdx.y * 64;
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int chunk = t + 256 * i;
+    const int r = chunk >> 3;
+    const int fc = chunk & 7;
+    const int64_t p = p0 + r;
+    int64_t tok = -1;
+    if (ends == nullptr) {
+      tok = p < rows ? p : -1;
+    } else {
+      // first group whose padded end is > p
+      int lo = 0, hi = E;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if ((int64_t)pend_s[mid] > p) hi = mid; else lo = mid + 1;
+      }
+      if (lo < E) {
+        const int64_t pstart = lo > 0 ? pend_s[lo - 1] : 0;
+        const int64_t gstart = lo > 0 ? ends_s[lo - 1] : 0;
+        const int64_t cand = gstart + (p - pstart);
+        tok = cand < (int64_t)ends_s[lo] ? cand : -1;
+        // a group whose clamped start exceeds its end holds no tokens
+        if (gstart > ends_s[lo]) tok = -1;
+      }
+    }
+    const int f = f0 + fc * 8;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (tok >= 0 && f < cols) v = *reinterpret_cast<const uint4*>(x + tok * ldx + f);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      tile[fc * 8 + 2 * u][r] = (uint16_t)(w[u] & 0xFFFFu);
+      tile[fc * 8 + 2 * u + 1][r] = (uint16_t)(w[u] >> 16);
+    }
+  }
+  __syncthreads();
+
+  const int f = t >> 2;
+  const int tb = t & 3;
+  const int64_t pc = p0 + tb * 32;
+  if (f0 + f < cols && pc < rows_pad_cap) {
+    const uint4* src = reinterpret_cast<const uint4*>(&tile[f][tb * 32]);
+    uint4 v[4] = {src[0], src[1], src[2], src[3]};
+    uint32_t am = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      am = max(am, amax16_of_word(v[u].x));
+      am = max(am, amax16_of_word(v[u].y));
+      am = max(am, amax16_of_word(v[u].z));
+      am = max(am, amax16_of_word(v[u].w));
+    }
+    const uint32_t b = e8m0_from_amax16<MODE>(am);
+    const int e = payload_exponent<MODE>(b);
+    uint32_t out[8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float f8[8];
+      bf16x2_to_scaled<MODE>(v[u].x, b, e, f8[0], f8[1]);
+      bf16x2_to_scaled<MODE>(v[u].y, b, e, f8[2], f8[3]);
+      bf16x2_to_scaled<MODE>(v[u].z, b, e, f8[4], f8[5]);
+      bf16x2_to_scaled<MODE>(v[u].w, b, e, f8[6], f8[7]);
+      out[2 * u] = e4m3_pack4<SW>(f8[0], f8[1], f8[2], f8[3]);
+      out[2 * u + 1] = e4m3_pack4<SW>(f8[4], f8[5], f8[6], f8[7]);
+    }
+    uint8_t* dst = qt + (int64_t)(f0 + f) * ldqt + pc;
+    reinterpret_cast<uint4*>(dst)[0] = make_uint4(out[0], out[1], out[2], out[3]);
+    reinterpret_cast<uint4*>(dst)[1] = make_uint4(out[4], out[5], out[6], out[7]);
+    st[(int64_t)(f0 + f) * ldst + (pc >> 5)] = (uint8_t)b;
+  }
+}
+
+template <int MODE, bool SW>
+hipError_t dim0_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx, uint8_t* q,
+                     int64_t ldq, uint8_t* s, int64_t lds, hipStream_t stream) {
+  const int cols8 = (int)(cols / 8);
+  dim3 grid((cols8 + 63) / 64, (unsigned)std::min<int64_t>((rows + 15) / 16, 65535));
+  hipLaunchKernelGGL((k_quant_dim0<MODE, SW>), grid, dim3(256), 0, stream, x, rows, cols8, ldx, q,
+                     ldq, s, lds);
+  return hipGetLastError();
+}
+
+template <int MODE, bool SW>
+hipError_t dim1_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                     const int32_t* ends, int64_t E, int64_t cap, uint8_t* qt, int64_t ldqt,
+                     uint8_t* st, int64_t ldst, int32_t* ends_pad, hipStream_t stream) {
+  dim3 grid((unsigned)((cap + 127) / 128), (unsigned)((cols + 63) / 64));
+  hipLaunchKernelGGL((k_quant_dim1<MODE, SW>), grid, dim3(256), 0, stream, x, rows, (int)cols, ldx,
+                     ends, (int)E, cap, qt, ldqt, st, ldst, ends_pad);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_quant_dim0(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                             uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int mode,
+                             hipStream_t stream) {
+  if (rows == 0 || cols == 0) return hipSuccess;
+  const bool sw = (mode & kCvtSoftwareFlag) != 0;
+  const int m = mode & 0xFF;
+  if (m == kModeRceil)
+    return sw ? dim0_impl<kModeRceil, true>(x, rows, cols, ldx, q, ldq, s, lds, stream)
+              : dim0_impl<kModeRceil, false>(x, rows, cols, ldx, q, ldq, s, lds, stream);
+  return sw ? dim0_impl<kModeFloor, true>(x, rows, cols, ldx, q, ldq, s, lds, stream)
+            : dim0_impl<kModeFloor, false>(x, rows, cols, ldx, q, ldq, s, lds, stream);
+}
+
+hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                             const int32_t* group_ends, int64_t num_groups,
+                             int64_t rows_pad_cap, uint8_t* qt, int64_t ldqt, uint8_t* st,
+                             int64_t ldst, int32_t* group_ends_pad, int mode,
+                             hipStream_t stream) {
+  if (cols == 0 || rows_pad_cap == 0) return hipSuccess;
+  const bool sw = (mode & kCvtSoftwareFlag) != 0;
+  const int m = mode & 0xFF;
+#define MXGG_DIM1(MODE, SWF)                                                                   \
+  dim1_impl<MODE, SWF>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, qt, ldqt, st, \
+                       ldst, group_ends_pad, stream)
+  if (m == kModeRceil) return sw ? MXGG_DIM1(kModeRceil, true) : MXGG_DIM1(kModeRceil, false);
+  return sw ? MXGG_DIM1(kModeFloor, true) : MXGG_DIM1(kModeFloor, false);
+#undef MXGG_DIM1
+}
+
+}  // namespace mxgg

@@ -1,0 +1,38 @@
+"""mxfp8gg — MXFP8 grouped GEMM for AMD MI355X (gfx950).
+
+bf16 -> MXFP8 casts, a forward grouped GEMM and a weight-gradient grouped GEMM
+over ragged expert groups, all as hand-written HIP kernels in libmxgg.so
+behind a C ABI (include/mxgg.h).  This package is the host side: it takes
+torch tensors, allocates outputs, and calls the library on the current stream.
+"""
+from ._lib import MxggError, load as load_library
+from .ops import (
+    _best_config,
+    fused_grouped_fwd,
+    fwd_ge,
+    grouped_mm,
+    grouped_wgrad,
+    padded_token_capacity,
+    to_mxfp8_dim0,
+    to_mxfp8_dim1,
+    wgrad_fused,
+    wgrad_kernel,
+    wgrad_prepare,
+)
+from .torchao_compat import (
+    apply,
+    triton_mxfp8_grouped_mm,
+    triton_mxfp8_wgrad,
+    triton_mxfp8_wgrad_v2,
+    triton_to_mxfp8_dim0,
+    triton_to_mxfp8_dim1,
+)
+
+__all__ = [
+    "MxggError", "load_library",
+    "to_mxfp8_dim0", "to_mxfp8_dim1", "padded_token_capacity",
+    "grouped_mm", "grouped_wgrad",
+    "fused_grouped_fwd", "fwd_ge", "wgrad_fused", "wgrad_prepare", "wgrad_kernel",
+    "triton_to_mxfp8_dim0", "triton_to_mxfp8_dim1",
+    "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",
+]

@@ -1,0 +1,385 @@
+"""Host side of the MXFP8 grouped-GEMM path: torch tensors in, libmxgg out.
+
+PyTorch only provides device memory and the current stream; every byte of
+arithmetic runs in the HIP kernels of libmxgg.so.  Outputs are allocated from
+torch's caching allocator and handed to the C ABI as raw pointers.  Nothing
+here synchronises with the host: group offsets stay on the device.
+
+Reference entry points mirrored here (all paths under the reference repo):
+  fused_grouped_fwd   fused_fwd.py:172-229
+  fwd_ge              fwd_final.py:121-131
+  wgrad_fused         wgrad_fused.py:34-71
+  wgrad_prepare       wgrad_fused.py:74-103
+  wgrad_kernel        wgrad_fused.py:106-112
+  _best_config        wgrad_fused.py:22-31
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_FP8 = torch.float8_e4m3fn
+_E8M0 = getattr(torch, "float8_e8m0fnu", None)
+
+_MODES = {"rceil": _lib.SCALE_RCEIL, "floor": _lib.SCALE_FLOOR}
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _stream_ptr(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need_gpu(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(
+            f"{name} is on {t.device}; the MXFP8 kernels run on a ROCm GPU only "
+            "(there is no CPU implementation)"
+        )
+
+
+def _mode(scaling_mode) -> int:
+    if isinstance(scaling_mode, int):
+        return scaling_mode
+    key = str(getattr(scaling_mode, "value", scaling_mode)).lower()
+    if key not in _MODES:
+        raise ValueError(f"scaling_mode must be one of {sorted(_MODES)}, got {scaling_mode!r}")
+    return _MODES[key]
+
+
+def _as_u8(t: torch.Tensor | None, name: str) -> torch.Tensor | None:
+    """Scale / payload tensors as raw bytes (uint8 view, no copy)."""
+    if t is None:
+        return None
+    if t.dtype == torch.uint8:
+        return t
+    if t.dtype == _FP8 or (_E8M0 is not None and t.dtype == _E8M0) or t.dtype == torch.int8:
+        return t.view(torch.uint8)
+    raise TypeError(f"{name}: expected uint8 / float8_e8m0fnu / float8_e4m3fn, got {t.dtype}")
+
+
+def _rowmajor(t: torch.Tensor) -> torch.Tensor:
+    """Last dimension contiguous (copy only if it is not)."""
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _group_ends(offs: torch.Tensor, num_groups: int, device) -> torch.Tensor:
+    """Accept [E] cumulative ends (torch._grouped_mm convention, used by every
+    caller of the reference) or [E+1] with a leading 0 (the form documented
+    at fused_fwd.py:7,181); return int32 [E] on the device."""
+    if not isinstance(offs, torch.Tensor):
+        offs = torch.as_tensor(offs, dtype=torch.int32)
+    if offs.dim() != 1:
+        raise ValueError(f"offs must be 1-D, got shape {tuple(offs.shape)}")
+    if offs.numel() == num_groups + 1:
+        offs = offs[1:]
+    elif offs.numel() != num_groups:
+        raise ValueError(
+            f"offs has {offs.numel()} entries; expected {num_groups} group ends "
+            f"(or {num_groups + 1} with a leading 0)"
+        )
+    if offs.device != device:
+        offs = offs.to(device, non_blocking=True)
+    if offs.dtype != torch.int32:
+        offs = offs.to(torch.int32)
+    return offs.contiguous()
+
+
+def _out_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return _lib.OUT_BF16
+    if dtype == torch.float32:
+        return _lib.OUT_F32
+    raise ValueError(f"out_dtype must be torch.bfloat16 or torch.float32, got {dtype}")
+
+
+# ---------------------------------------------------------------------------
+# bf16 -> MXFP8 casts
+# ---------------------------------------------------------------------------
+def to_mxfp8_dim0(x: torch.Tensor, scaling_mode="rceil"):
+    """Row-wise MXFP8: 1x32 blocks along the last dimension.
+
+    x: bf16 [..., K] (K % 32 == 0).  Returns (q float8_e4m3fn [..., K],
+    scales uint8 [..., K/32]) with E8M0 bytes (2^(b-127)).
+    """
+    _need_gpu(x, "x")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bfloat16, got {x.dtype}")
+    shape = x.shape
+    K = shape[-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    rows = x2.shape[0]
+    q = torch.empty((rows, K), dtype=_FP8, device=x.device)
+    s = torch.empty((rows, K // 32), dtype=torch.uint8, device=x.device)
+    lib = _lib.load()
+    _lib.check(
+        lib.mxgg_quant_dim0(x2.data_ptr(), rows, K, x2.stride(0), q.data_ptr(), q.stride(0),
+                            s.data_ptr(), s.stride(0), _mode(scaling_mode), _stream_ptr(x)),
+        "quant_dim0",
+    )
+    return q.reshape(shape), s.reshape(*shape[:-1], K // 32)
+
+
+def padded_token_capacity(num_tokens: int, num_groups: int | None) -> int:
+    """Columns of the dim1 output: every group padded to 32 tokens."""
+    extra = 31 * num_groups if num_groups else 0
+    return (num_tokens + extra + 31) // 32 * 32
+
+
+def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mode="rceil"):
+    """Token-axis MXFP8 for the wgrad operands, written transposed.
+
+    x: bf16 [M, C] (tokens x features).  Blocks of 32 run along M and restart
+    at each group boundary of `offs` (cumulative ends, int32, on the device);
+    each group is zero-padded to a multiple of 32 tokens.
+    Returns (qt float8_e4m3fn [C, M_pad], st uint8 [C, M_pad/32], offs_pad)
+    where offs_pad are the padded cumulative ends (int32 [E], None without
+    offs) and M_pad = padded_token_capacity(M, E) >= offs_pad[-1].
+    """
+    _need_gpu(x, "x")
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise TypeError("x must be a 2-D bfloat16 tensor")
+    M, C = x.shape
+    x2 = x if (x.stride(-1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0) else x.contiguous()
+    E = None
+    ends = None
+    ends_pad = None
+    if offs is not None:
+        E = offs.numel()
+        ends = _group_ends(offs, E, x.device)
+        ends_pad = torch.empty(E, dtype=torch.int32, device=x.device)
+    cap = padded_token_capacity(M, E)
+    qt = torch.empty((C, cap), dtype=_FP8, device=x.device)
+    st = torch.empty((C, cap // 32), dtype=torch.uint8, device=x.device)
+    lib = _lib.load()
+    _lib.check(
+        lib.mxgg_quant_dim1(
+            x2.data_ptr(), M, C, x2.stride(0),
+            ends.data_ptr() if ends is not None else None, E or 0, cap,
+            qt.data_ptr(), qt.stride(0), st.data_ptr(), st.stride(0),
+            ends_pad.data_ptr() if ends_pad is not None else None,
+            _mode(scaling_mode), _stream_ptr(x),
+        ),
+        "quant_dim1",
+    )
+    return qt, st, ends_pad
+
+
+# ---------------------------------------------------------------------------
+# forward grouped GEMM
+# ---------------------------------------------------------------------------
+def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
+               a_scales: torch.Tensor | None = None, w_scales: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.bfloat16, out: torch.Tensor | None = None):
+    """out[rows of g] = dequant(a[rows of g]) @ dequant(w[g])^T, fp32 accumulate.
+
+    a: e4m3 [M, K]; w: e4m3 [E, N, K]; offs: int32 group ends ([E] or [E+1]
+    with leading 0) or None for a single group; scales: E8M0 bytes
+    [M, K/32] and [E, N, K/32], both or neither (neither = scale 1.0).
+    Rows after the last group end are left untouched.
+    """
+    _need_gpu(a, "a")
+    _need_gpu(w, "w")
+    if a.dim() != 2 or w.dim() != 3:
+        raise ValueError(f"expected a [M, K] and w [E, N, K], got {tuple(a.shape)} and {tuple(w.shape)}")
+    M, K = a.shape
+    E, N, K2 = w.shape
+    assert K == K2, f"K mismatch: {K} vs {K2}"
+    a8 = _as_u8(_rowmajor(a), "a")
+    w8 = _as_u8(_rowmajor(w), "w")
+    if (a_scales is None) != (w_scales is None):
+        raise ValueError("a_scales and w_scales must both be given or both be None")
+    sa = sw = None
+    if a_scales is not None:
+        sa = _as_u8(_rowmajor(a_scales), "a_scales")
+        sw = _as_u8(_rowmajor(w_scales), "w_scales")
+        if tuple(sa.shape) != (M, K // 32):
+            raise ValueError(f"a_scales shape {tuple(sa.shape)} != {(M, K // 32)}")
+        if tuple(sw.shape) != (E, N, K // 32):
+            raise ValueError(f"w_scales shape {tuple(sw.shape)} != {(E, N, K // 32)}")
+        _need_gpu(sa, "a_scales")
+        _need_gpu(sw, "w_scales")
+    ends = None
+    if offs is not None:
+        ends = _group_ends(offs, E, a.device)
+    elif E != 1:
+        raise ValueError("offs is required when w holds more than one expert")
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    elif out.shape != (M, N) or out.dtype != out_dtype or out.stride(-1) != 1:
+        raise ValueError("out must be a row-major [M, N] tensor of out_dtype")
+    lib = _lib.load()
+    _lib.check(
+        lib.mxgg_grouped_fwd(
+            a8.data_ptr(), a8.stride(0),
+            sa.data_ptr() if sa is not None else None, sa.stride(0) if sa is not None else 0,
+            w8.data_ptr(), w8.stride(0), w8.stride(1),
+            sw.data_ptr() if sw is not None else None,
+            sw.stride(0) if sw is not None else 0, sw.stride(1) if sw is not None else 0,
+            ends.data_ptr() if ends is not None else None, E,
+            M, N, K, out.data_ptr(), out.stride(0), _out_code(out_dtype), _stream_ptr(a),
+        ),
+        "grouped_fwd",
+    )
+    return out
+
+
+def fused_grouped_fwd(a_fp8, w_fp8, offs, a_scales=None, w_scales=None,
+                      BLOCK_M=128, BLOCK_N=128, BLOCK_K=128,
+                      GROUP_SIZE_M=8, num_stages=None, num_warps=None, *,
+                      out_dtype=torch.bfloat16):
+    """Drop-in for fused_fwd.fused_grouped_fwd (fused_fwd.py:172-229).
+
+    a_fp8 [M, K] e4m3, w_fp8 [E, N, K] e4m3, offs group ends (honoured, also
+    when groups are unequal or empty), optional E8M0 scales [M, K/32] and
+    [E, N, K/32].  As in the reference, scales are used only when both are
+    given.  The tile keyword arguments are accepted for call-site
+    compatibility; the gfx950 kernel uses its own fixed 256x256x128 tiling.
+    Returns bf16 [M, N].
+    """
+    del BLOCK_M, BLOCK_N, BLOCK_K, GROUP_SIZE_M, num_stages, num_warps
+    use_scales = a_scales is not None and w_scales is not None
+    return grouped_mm(a_fp8, w_fp8, offs,
+                      a_scales if use_scales else None, w_scales if use_scales else None,
+                      out_dtype=out_dtype)
+
+
+def fwd_ge(x_fp8, w_fp8, BLOCK_M=256, BLOCK_N=256, BLOCK_K=128, NUM_WARPS=4, GROUP_M=4):
+    """Drop-in for fwd_final.fwd_ge (fwd_final.py:121-131): C[M,N] = X[M,K] @ W[K,N].
+
+    Unscaled (every E8M0 scale 1.0), bf16 out.  W [K, N] is consumed as its
+    transpose [N, K]; a W that is itself a transposed view of a row-major
+    [N, K] tensor (the layout the reference transposes away from,
+    fwd_final.py:189) is used without a copy.
+    """
+    del BLOCK_M, BLOCK_N, BLOCK_K, NUM_WARPS, GROUP_M
+    M, K = x_fp8.shape
+    K2, N = w_fp8.shape
+    assert K == K2
+    wt = w_fp8.t()
+    if wt.stride(-1) != 1:
+        wt = wt.contiguous()
+    return grouped_mm(x_fp8, wt.unsqueeze(0), None)
+
+
+# ---------------------------------------------------------------------------
+# wgrad grouped GEMM
+# ---------------------------------------------------------------------------
+def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
+                  go_scales: torch.Tensor | None = None, ia_scales: torch.Tensor | None = None,
+                  out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None):
+    """dW[g] = dequant(go[:, tok of g]) @ dequant(ia[:, tok of g])^T  -> [E, N, K].
+
+    go: e4m3 [N, M] (dY transposed, token-contiguous); ia: e4m3 [K, M]
+    (X transposed); offs: int32 [E] cumulative token ends; scales: E8M0
+    [N, M/32] / [K, M/32] along tokens, both or neither.  With scales every
+    group end must be a multiple of 32 (the layout to_mxfp8_dim1 produces).
+    Empty groups yield zeros.
+    """
+    _need_gpu(go, "go")
+    _need_gpu(ia, "ia")
+    if go.dim() != 2 or ia.dim() != 2:
+        raise ValueError("go and ia must be 2-D")
+    N, M = go.shape
+    K, M2 = ia.shape
+    assert M == M2, f"token count mismatch: {M} vs {M2}"
+    g8 = _as_u8(_rowmajor(go), "go")
+    i8 = _as_u8(_rowmajor(ia), "ia")
+    if (go_scales is None) != (ia_scales is None):
+        raise ValueError("go_scales and ia_scales must both be given or both be None")
+    sg = si = None
+    if go_scales is not None:
+        sg = _as_u8(_rowmajor(go_scales), "go_scales")
+        si = _as_u8(_rowmajor(ia_scales), "ia_scales")
+        if tuple(sg.shape) != (N, M // 32) or tuple(si.shape) != (K, M // 32):
+            raise ValueError(
+                f"scale shapes {tuple(sg.shape)}, {tuple(si.shape)} != {(N, M // 32)}, {(K, M // 32)}")
+    E = offs.numel()
+    ends = _group_ends(offs, E, go.device)
+    if out is None:
+        out = torch.empty((E, N, K), dtype=out_dtype, device=go.device)
+    elif out.shape != (E, N, K) or out.dtype != out_dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [E, N, K] tensor of out_dtype")
+    lib = _lib.load()
+    _lib.check(
+        lib.mxgg_grouped_wgrad(
+            g8.data_ptr(), g8.stride(0),
+            sg.data_ptr() if sg is not None else None, sg.stride(0) if sg is not None else 0,
+            i8.data_ptr(), i8.stride(0),
+            si.data_ptr() if si is not None else None, si.stride(0) if si is not None else 0,
+            ends.data_ptr(), E, M, N, K, out.data_ptr(), _out_code(out_dtype), _stream_ptr(go),
+        ),
+        "grouped_wgrad",
+    )
+    return out
+
+
+def _best_config(e, m):
+    """Reference tile heuristic (wgrad_fused.py:22-31).  Kept for call-site
+    compatibility; the gfx950 kernel ignores tile hints."""
+    if m >= 100000:
+        return dict(BLOCK_M=256, BLOCK_N=256, BLOCK_K=128, GROUP_SIZE_M=4,
+                    num_stages=None, num_warps=4)
+    return dict(BLOCK_M=128, BLOCK_N=128, BLOCK_K=128, GROUP_SIZE_M=1,
+                num_stages=2 if e <= 4 else None, num_warps=4)
+
+
+_TILE_KW = ("BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_SIZE_M", "num_stages", "num_warps")
+
+
+def _split_kw(kwargs):
+    out_dtype = kwargs.pop("out_dtype", torch.bfloat16)
+    for k in list(kwargs):
+        if k in _TILE_KW:
+            kwargs.pop(k)
+    if kwargs:
+        raise TypeError(f"unexpected keyword arguments: {sorted(kwargs)}")
+    return out_dtype
+
+
+def wgrad_fused(go, ia, offs, go_scales=None, ia_scales=None, **kwargs):
+    """Drop-in for wgrad_fused.wgrad_fused (wgrad_fused.py:34-71).
+
+    go (N, M) e4m3, ia (K, M) e4m3, offs (E,) int32 cumulative token ends,
+    optional E8M0 scales (N, M/32) and (K, M/32).  No restacking: the kernel
+    contracts each group's token range in place.  Returns (E, N, K), bf16 by
+    default like the reference; pass out_dtype=torch.float32 for fp32 grads.
+    Scales are used only when both are given, as in the reference.
+    """
+    out_dtype = _split_kw(dict(kwargs))
+    use_scales = go_scales is not None and ia_scales is not None
+    return grouped_wgrad(go, ia, offs, go_scales if use_scales else None,
+                         ia_scales if use_scales else None, out_dtype=out_dtype)
+
+
+def wgrad_prepare(go, ia, offs, go_scales=None, ia_scales=None):
+    """Drop-in for wgrad_fused.wgrad_prepare (wgrad_fused.py:74-103).
+
+    The reference restacks per group here; this kernel needs no restacking,
+    so the dict references the caller's tensors (same keys as the reference).
+    """
+    N, M = go.shape
+    K = ia.shape[0]
+    E = offs.shape[0]
+    use_scales = go_scales is not None and ia_scales is not None
+    return {
+        "A": go, "B": ia,
+        "offs": _group_ends(offs, E, go.device),
+        "As": go_scales if use_scales else None, "Bs": ia_scales if use_scales else None,
+        "E": E, "N": N, "K": K, "M": M,
+        "flops": 2 * M * N * K,
+    }
+
+
+def wgrad_kernel(data: dict, **kwargs):
+    """Drop-in for wgrad_fused.wgrad_kernel (wgrad_fused.py:106-112): run on a
+    wgrad_prepare() dict, return (E, N, K) (bf16 unless out_dtype is given)."""
+    out_dtype = _split_kw(dict(kwargs))
+    return grouped_wgrad(data["A"], data["B"], data["offs"], data["As"], data["Bs"],
+                         out_dtype=out_dtype)

@@ -1,0 +1,94 @@
+"""Host-side logic that runs without a GPU: reference-named modules import,
+argument handling fails loudly on CPU tensors (no CPU fallback), offs
+normalisation, and the torchao swap-in against a fake torchao module."""
+import sys
+import types
+
+import numpy as np
+import pytest
+import torch
+
+import fused_fwd
+import fwd_final
+import mxfp8gg
+import patch_kernels
+import wgrad_fused
+from mxfp8gg import ops, workloads
+
+
+def test_reference_module_names_resolve():
+    assert fused_fwd.fused_grouped_fwd is mxfp8gg.fused_grouped_fwd
+    assert fwd_final.fwd_ge is mxfp8gg.fwd_ge
+    assert wgrad_fused.wgrad_fused is mxfp8gg.wgrad_fused
+    assert wgrad_fused.wgrad_prepare is mxfp8gg.wgrad_prepare
+    assert wgrad_fused.wgrad_kernel is mxfp8gg.wgrad_kernel
+    assert callable(patch_kernels.apply)
+
+
+def test_best_config_matches_reference_heuristic():
+    # wgrad_fused.py:22-31
+    assert wgrad_fused._best_config(8, 128000)["BLOCK_M"] == 256
+    assert wgrad_fused._best_config(4, 32768)["num_stages"] == 2
+    assert wgrad_fused._best_config(8, 32768)["num_stages"] is None
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    a = torch.zeros(64, 256, dtype=torch.float8_e4m3fn)
+    w = torch.zeros(2, 32, 256, dtype=torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="ROCm GPU only"):
+        fused_fwd.fused_grouped_fwd(a, w, torch.tensor([32, 64], dtype=torch.int32))
+    with pytest.raises(ValueError, match="ROCm GPU only"):
+        mxfp8gg.to_mxfp8_dim0(torch.zeros(4, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="ROCm GPU only"):
+        mxfp8gg.wgrad_fused(torch.zeros(8, 64, dtype=torch.float8_e4m3fn),
+                            torch.zeros(8, 64, dtype=torch.float8_e4m3fn),
+                            torch.tensor([64], dtype=torch.int32))
+
+
+def test_offs_forms():
+    dev = torch.device("cpu")
+    ends = ops._group_ends(torch.tensor([0, 3, 7, 9], dtype=torch.int32), 3, dev)
+    assert ends.tolist() == [3, 7, 9]
+    ends = ops._group_ends(torch.tensor([3, 7, 9], dtype=torch.int64), 3, dev)
+    assert ends.dtype == torch.int32 and ends.tolist() == [3, 7, 9]
+    with pytest.raises(ValueError):
+        ops._group_ends(torch.tensor([1, 2]), 3, dev)
+
+
+def test_padded_capacity():
+    assert ops.padded_token_capacity(64, None) == 64
+    assert ops.padded_token_capacity(65, None) == 96
+    assert ops.padded_token_capacity(100, 4) == (100 + 124 + 31) // 32 * 32
+
+
+def test_workload_routing_shapes():
+    s2 = workloads.dirichlet_sizes(65536, 32, 0)
+    assert s2.sum() == 65536 and s2.shape == (32,)
+    s4 = workloads.zipf_sizes(65536, 32, 1.2, 0, empty=2)
+    assert s4.sum() == 65536 and (s4 == 0).sum() >= 2 and s4.max() > 16384
+    assert workloads.ends_of([1, 0, 2]).tolist() == [1, 1, 3]
+
+
+def test_apply_patches_a_fake_torchao(monkeypatch):
+    names = ["torchao", "torchao.prototype", "torchao.prototype.moe_training",
+             "torchao.prototype.moe_training.kernels",
+             "torchao.prototype.moe_training.kernels.mxfp8",
+             "torchao.prototype.moe_training.kernels.mxfp8.rocm_mxfp8_mm",
+             "torchao.prototype.moe_training.kernels.mxfp8.quant"]
+    for n in names:
+        monkeypatch.setitem(sys.modules, n, types.ModuleType(n))
+    target = sys.modules[names[5]]
+    target.triton_mxfp8_grouped_mm = object()
+    patch_kernels.apply()
+    assert target.triton_mxfp8_grouped_mm is mxfp8gg.triton_mxfp8_grouped_mm
+    assert target.triton_mxfp8_wgrad is mxfp8gg.triton_mxfp8_wgrad
+    assert target.triton_mxfp8_wgrad_v2 is mxfp8gg.triton_mxfp8_wgrad
+    assert sys.modules[names[4]].rocm_mxfp8_mm is target
+    assert sys.modules[names[6]].triton_to_mxfp8_dim0 is mxfp8gg.triton_to_mxfp8_dim0
+
+
+def test_apply_without_torchao_raises():
+    if "torchao" in sys.modules:
+        pytest.skip("torchao importable here")
+    with pytest.raises(ImportError):
+        patch_kernels.apply()

@@ -1,0 +1,143 @@
+"""C ABI of libmxgg.so without a GPU: it loads, exports every function that
+include/mxgg.h declares, and rejects bad arguments before touching the device.
+
+Every call below fails validation on the host (null pointers, bad shapes,
+misalignment, unknown enums), so no kernel is launched.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mxfp8gg import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mxgg.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mxgg_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_lists_the_bound_functions():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_status_strings(lib):
+    assert lib.mxgg_abi_version() == _lib.ABI_VERSION
+    for code in range(0, 7):
+        assert lib.mxgg_status_string(code)
+    assert lib.mxgg_status_string(99) == b"unknown status"
+
+
+FAKE = 0x10000  # 16-byte aligned, never dereferenced: validation fails first
+
+
+def _fwd(lib, **kw):
+    args = dict(a=FAKE, lda=256, a_s=None, ldas=0, w=FAKE, wg=512 * 256, ldw=256, w_s=None,
+                wsg=0, ldws=0, ends=None, E=1, M=64, N=512, K=256, out=FAKE, ldo=512,
+                dt=_lib.OUT_BF16)
+    args.update(kw)
+    return lib.mxgg_grouped_fwd(args["a"], args["lda"], args["a_s"], args["ldas"], args["w"],
+                                args["wg"], args["ldw"], args["w_s"], args["wsg"], args["ldws"],
+                                args["ends"], args["E"], args["M"], args["N"], args["K"],
+                                args["out"], args["ldo"], args["dt"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(K=100), _lib.ERR_SHAPE),                     # K % 32
+    (dict(K=0), _lib.ERR_SHAPE),
+    (dict(M=-1), _lib.ERR_SHAPE),
+    (dict(dt=7), _lib.ERR_INVALID_ARGUMENT),
+    (dict(a_s=FAKE, ldas=8), _lib.ERR_INVALID_ARGUMENT),  # only one of the scales
+    (dict(a=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(lda=128), _lib.ERR_SHAPE),                   # ld < K
+    (dict(a=FAKE + 8), _lib.ERR_ALIGNMENT),
+    (dict(lda=264), _lib.ERR_ALIGNMENT),               # not a multiple of 16
+    (dict(out=FAKE + 2), _lib.ERR_ALIGNMENT),
+    (dict(ends=FAKE, E=0), _lib.ERR_UNSUPPORTED),
+    (dict(ends=FAKE, E=2000), _lib.ERR_UNSUPPORTED),
+    (dict(ends=FAKE, E=4, wg=100), _lib.ERR_SHAPE),    # expert stride too small
+])
+def test_grouped_fwd_rejects(lib, kw, status):
+    assert _fwd(lib, **kw) == status
+    assert lib.mxgg_last_error()
+
+
+def test_grouped_fwd_empty_is_noop(lib):
+    assert _fwd(lib, M=0, a=None, w=None, out=None) == _lib.OK
+
+
+def _wg(lib, **kw):
+    args = dict(go=FAKE, ldgo=128, gs=None, ldgs=0, ia=FAKE, ldia=128, is_=None, ldis=0,
+                ends=FAKE, E=4, M=128, N=64, K=64, dw=FAKE, dt=_lib.OUT_F32)
+    args.update(kw)
+    return lib.mxgg_grouped_wgrad(args["go"], args["ldgo"], args["gs"], args["ldgs"], args["ia"],
+                                  args["ldia"], args["is_"], args["ldis"], args["ends"], args["E"],
+                                  args["M"], args["N"], args["K"], args["dw"], args["dt"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(M=100), _lib.ERR_SHAPE),                     # tokens % 32
+    (dict(ends=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(E=0), _lib.ERR_UNSUPPORTED),
+    (dict(gs=FAKE, ldgs=4), _lib.ERR_INVALID_ARGUMENT),
+    (dict(dw=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ldgo=64), _lib.ERR_SHAPE),
+    (dict(go=FAKE + 4), _lib.ERR_ALIGNMENT),
+    (dict(K=66), _lib.ERR_ALIGNMENT),
+    (dict(dt=3), _lib.ERR_INVALID_ARGUMENT),
+])
+def test_grouped_wgrad_rejects(lib, kw, status):
+    assert _wg(lib, **kw) == status
+
+
+@pytest.mark.parametrize("args,status", [
+    ((FAKE, 4, 100, 100, FAKE, 100, FAKE, 4, 0, None), _lib.ERR_SHAPE),      # cols % 32
+    ((FAKE, 4, 64, 64, FAKE, 64, FAKE, 2, 5, None), _lib.ERR_INVALID_ARGUMENT),  # mode
+    ((None, 4, 64, 64, FAKE, 64, FAKE, 2, 0, None), _lib.ERR_INVALID_ARGUMENT),
+    ((FAKE + 2, 4, 64, 64, FAKE, 64, FAKE, 2, 0, None), _lib.ERR_ALIGNMENT),
+    ((FAKE, 4, 64, 32, FAKE, 64, FAKE, 2, 0, None), _lib.ERR_SHAPE),       # ldx < cols
+])
+def test_quant_dim0_rejects(lib, args, status):
+    assert lib.mxgg_quant_dim0(*args) == status
+
+
+def test_quant_dim0_empty_is_noop(lib):
+    assert lib.mxgg_quant_dim0(None, 0, 64, 64, None, 64, None, 2, 0, None) == _lib.OK
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(cols=12), _lib.ERR_SHAPE),
+    (dict(cap=48), _lib.ERR_SHAPE),                    # not a multiple of 32
+    (dict(cap=32), _lib.ERR_SHAPE),                    # below rows + 31 * groups
+    (dict(E=0), _lib.ERR_UNSUPPORTED),
+    (dict(pad=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(mode=9), _lib.ERR_INVALID_ARGUMENT),
+    (dict(x=FAKE + 2), _lib.ERR_ALIGNMENT),
+])
+def test_quant_dim1_rejects(lib, kw, status):
+    a = dict(x=FAKE, rows=64, cols=64, ldx=64, ends=FAKE, E=2, cap=128, qt=FAKE, ldqt=128,
+             st=FAKE, ldst=4, pad=FAKE, mode=0)
+    a.update(kw)
+    assert lib.mxgg_quant_dim1(a["x"], a["rows"], a["cols"], a["ldx"], a["ends"], a["E"],
+                               a["cap"], a["qt"], a["ldqt"], a["st"], a["ldst"], a["pad"],
+                               a["mode"], None) == status
+
+
+def test_python_maps_errors_to_exceptions(lib):
+    with pytest.raises(ValueError, match="K=100"):
+        _lib.check(_fwd(lib, K=100), "grouped_fwd")

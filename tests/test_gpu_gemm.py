@@ -1,0 +1,281 @@
+"""GPU parity of the grouped GEMMs against the CPU oracle.
+
+Tolerance (see tests/_helpers.assert_close_to_oracle): every element within
+2^-7 |ref| + 2^-12 max|ref| of the float64 dequantise-then-matmul reference,
+and max|err| / max|ref| <= 1e-2.  Known-answer tests are exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+import fused_fwd
+import fwd_final
+import mxfp8gg
+import wgrad_fused
+from mxfp8gg import ops, workloads
+from oracle import oracle as O
+from tests._helpers import assert_close_to_oracle, bits, fp8_dev, u8
+
+pytestmark = pytest.mark.gpu
+
+
+def _ones(shape, gpu):
+    return torch.ones(shape, device=gpu, dtype=torch.bfloat16).to(torch.float8_e4m3fn)
+
+
+# ---------------------------------------------------------------------------
+# the reference's E8M0 known-answer tests (scale_correctness.py), called with
+# the reference's argument forms ([E+1] offs with leading 0, tile kwargs)
+# ---------------------------------------------------------------------------
+def test_kat_scale_bypass(gpu):
+    M, N, K, E = 64, 32, 64, 2
+    a_s = torch.full((M, K // 32), 127, dtype=torch.uint8, device=gpu)
+    a_s[:, 0] = 128
+    w_s = torch.full((E, N, K // 32), 127, dtype=torch.uint8, device=gpu)
+    offs = torch.tensor([0, M // 2, M], dtype=torch.int32, device=gpu)
+    c = fused_fwd.fused_grouped_fwd(_ones((M, K), gpu), _ones((E, N, K), gpu), offs,
+                                    a_scales=a_s, w_scales=w_s, BLOCK_M=64, BLOCK_N=32,
+                                    BLOCK_K=64, GROUP_SIZE_M=1)
+    assert c.dtype == torch.bfloat16 and torch.all(c.float() == 96.0)
+
+
+def test_kat_scale_application_order(gpu):
+    M, N, K = 64, 32, 64
+    a_s = torch.full((M, 2), 127, dtype=torch.uint8, device=gpu)
+    a_s[:, 0], a_s[:, 1] = 128, 126
+    w_s = torch.full((1, N, 2), 127, dtype=torch.uint8, device=gpu)
+    w_s[:, :, 0] = 129
+    offs = torch.tensor([0, M], dtype=torch.int32, device=gpu)
+    c = fused_fwd.fused_grouped_fwd(_ones((M, K), gpu), _ones((1, N, K), gpu), offs,
+                                    a_scales=a_s, w_scales=w_s)
+    assert torch.all(c.float() == 272.0)
+
+
+def test_kat_scale_layout_every_row(gpu):
+    M, N, K = 64, 32, 64
+    a_s = torch.full((M, 2), 127, dtype=torch.uint8, device=gpu)
+    a_s[:, 0] = torch.clamp(127 + torch.arange(M, device=gpu), max=254).to(torch.uint8)
+    w_s = torch.full((1, N, 2), 127, dtype=torch.uint8, device=gpu)
+    c = fused_fwd.fused_grouped_fwd(_ones((M, K), gpu), _ones((1, N, K), gpu),
+                                    torch.tensor([0, M], dtype=torch.int32, device=gpu),
+                                    a_scales=a_s, w_scales=w_s, out_dtype=torch.float32)
+    expect = 32.0 * torch.exp2(torch.arange(M, dtype=torch.float64)) + 32.0
+    got = c.double().cpu()
+    # exact while representable in fp32 (m < 20), then within fp32 rounding
+    assert torch.equal(got[:20], expect[:20, None].expand(20, N))
+    assert torch.allclose(got, expect[:, None].expand(M, N), rtol=2 ** -23, atol=0)
+
+
+def test_kat_per_column_and_per_block_scales(gpu):
+    # W-side layout: column n gets 2^(n%8) on block b=n%4 — catches a transposed
+    # or shifted B-scale lane mapping the reference's KATs leave open.
+    M, N, K = 32, 64, 128
+    w_s = torch.full((1, N, 4), 127, dtype=torch.uint8, device=gpu)
+    n = torch.arange(N, device=gpu)
+    w_s[0, n, n % 4] = (127 + n % 8).to(torch.uint8)
+    a_s = torch.full((M, 4), 127, dtype=torch.uint8, device=gpu)
+    c = ops.grouped_mm(_ones((M, K), gpu), _ones((1, N, K), gpu), None, a_s, w_s,
+                       out_dtype=torch.float32)
+    expect = 96.0 + 32.0 * torch.exp2((n % 8).double())
+    assert torch.equal(c.double(), expect[None, :].expand(M, N))
+
+
+# ---------------------------------------------------------------------------
+# random data against the oracle
+# ---------------------------------------------------------------------------
+def _rand_q(shape, gpu, seed, scale_lo=118, scale_hi=136):
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    codes = torch.randint(0, 0x7E, shape, generator=g, device=gpu, dtype=torch.int32)
+    sign = torch.randint(0, 2, shape, generator=g, device=gpu, dtype=torch.int32) << 7
+    q = (codes | sign).to(torch.uint8)
+    s_shape = shape[:-1] + (shape[-1] // 32,)
+    s = torch.randint(scale_lo, scale_hi, s_shape, generator=g, device=gpu,
+                      dtype=torch.int32).to(torch.uint8)
+    return q, s
+
+
+@pytest.mark.parametrize("sizes,N,K", [
+    ([64, 128, 32, 96], 512, 256),          # C1 geometry
+    ([0, 300, 1, 0, 212], 384, 320),        # empty groups, N and K tails (K % 128 = 64)
+    ([513], 256, 128),                      # one group, M tail
+    ([256, 256, 256], 256, 1024),           # aligned, several K stages
+    ([7, 0, 0], 96, 32),                    # tiny
+])
+@pytest.mark.parametrize("scaled", [True, False])
+def test_grouped_fwd_random_codes(gpu, sizes, N, K, scaled):
+    E, M = len(sizes), sum(sizes)
+    a_q, a_s = _rand_q((M, K), gpu, 21)
+    w_q, w_s = _rand_q((E, N, K), gpu, 22)
+    ends = workloads.ends_of(sizes)
+    y = ops.grouped_mm(a_q.view(torch.float8_e4m3fn), w_q.view(torch.float8_e4m3fn),
+                       torch.from_numpy(ends).to(gpu), a_s if scaled else None,
+                       w_s if scaled else None)
+    ref = O.grouped_fwd(u8(a_q), u8(a_s) if scaled else None, u8(w_q),
+                        u8(w_s) if scaled else None, ends)
+    assert_close_to_oracle(y, ref)
+
+
+def test_c1_end_to_end_quant_then_gemm(gpu):
+    x, w, sizes = workloads.c1(gpu)
+    xq, xs = mxfp8gg.to_mxfp8_dim0(x)
+    wq, ws = mxfp8gg.to_mxfp8_dim0(w)
+    ends = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    y = fused_fwd.fused_grouped_fwd(xq, wq, ends, xs, ws)
+    ref = O.grouped_fwd(u8(xq), u8(xs), u8(wq), u8(ws), workloads.ends_of(sizes))
+    assert_close_to_oracle(y, ref)
+    # and the dequant path matches the unquantised bf16 product to MXFP8 accuracy
+    bf = torch.cat([x[b:e].float() @ w[g].float().T
+                    for g, (b, e) in enumerate(O.group_bounds(workloads.ends_of(sizes), 320))])
+    assert (y.float() - bf).abs().max() / bf.abs().max() < 0.1
+
+
+def test_rows_outside_groups_untouched_and_each_row_written(gpu):
+    sizes = [100, 0, 37]
+    M, N, K = 200, 256, 128
+    a_q, a_s = _rand_q((M, K), gpu, 31)
+    w_q, w_s = _rand_q((3, N, K), gpu, 32)
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+    ops.grouped_mm(a_q.view(torch.float8_e4m3fn), w_q.view(torch.float8_e4m3fn),
+                   torch.tensor(np.cumsum(sizes), dtype=torch.int32, device=gpu), a_s, w_s,
+                   out=out)
+    assert not torch.isnan(out[:137]).any()
+    assert torch.isnan(out[137:]).all()
+
+
+def test_scale_bump_doubles_output_exactly(gpu):
+    x, w, sizes = workloads.c1(gpu)
+    xq, xs = mxfp8gg.to_mxfp8_dim0(x)
+    wq, ws = mxfp8gg.to_mxfp8_dim0(w)
+    ends = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    y = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.float32)
+    y2 = ops.grouped_mm(xq, wq, ends, xs + 1, ws, out_dtype=torch.float32)
+    assert torch.equal(y2, 2 * y)
+
+
+def test_fwd_ge_dense(gpu):
+    g = torch.Generator(device=gpu).manual_seed(41)
+    M, K, N = 300, 256, 320
+    x = torch.randn(M, K, generator=g, device=gpu).to(torch.float8_e4m3fn)
+    w_nk = torch.randn(N, K, generator=g, device=gpu).to(torch.float8_e4m3fn)
+    ref = O.grouped_fwd(u8(x), None, u8(w_nk)[None], None, None)
+    y1 = fwd_final.fwd_ge(x, w_nk.t().contiguous())     # [K, N] row-major
+    y2 = fwd_final.fwd_ge(x, w_nk.t())                   # transposed view, no copy
+    assert_close_to_oracle(y1, ref)
+    assert torch.equal(y1, y2)
+
+
+def test_torchao_named_forward(gpu):
+    x, w, sizes = workloads.c1(gpu)
+    xq, xs = mxfp8gg.triton_to_mxfp8_dim0(x, scaling_mode="rceil")
+    wq, ws = mxfp8gg.triton_to_mxfp8_dim0(w, scaling_mode="rceil")
+    ends = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    y1 = mxfp8gg.triton_mxfp8_grouped_mm(xq, wq, xs, ws, ends)
+    y2 = mxfp8gg.triton_mxfp8_grouped_mm(xq, wq.transpose(-2, -1), xs, ws, ends)
+    y3 = fused_fwd.fused_grouped_fwd(xq, wq, ends, xs, ws)
+    assert torch.equal(y1, y2) and torch.equal(y1, y3)
+
+
+@pytest.mark.parametrize("cfg", ["c2", "c3"])
+def test_full_size_forward_sampled_rows(gpu, cfg):
+    x, w, sizes = getattr(workloads, cfg)(gpu)
+    xq, xs = mxfp8gg.to_mxfp8_dim0(x)
+    wq, ws = mxfp8gg.to_mxfp8_dim0(w)
+    del x, w
+    ends_np = workloads.ends_of(sizes)
+    ends = torch.from_numpy(ends_np).to(gpu)
+    y = ops.grouped_mm(xq, wq, ends, xs, ws)
+    y_again = ops.grouped_mm(xq, wq, ends, xs, ws)
+    assert torch.equal(y, y_again)  # deterministic
+    # sampled rows from four experts (first rows, last rows, interior)
+    rows = []
+    for g in (0, 5, 17, 31):
+        b = 0 if g == 0 else int(ends_np[g - 1])
+        e = int(ends_np[g])
+        if e > b:
+            rows += sorted({b, (b + e) // 2, e - 1})
+    rows = np.array(sorted(set(rows)))
+    idx = torch.from_numpy(rows).to(gpu)
+    a_rows, as_rows = u8(xq[idx]), u8(xs[idx])
+    ref = np.empty((rows.size, wq.shape[1]))
+    for g in sorted({int(np.searchsorted(ends_np, r, side="right")) for r in rows}):
+        sel = np.nonzero(np.searchsorted(ends_np, rows, side="right") == g)[0]
+        wdq = O.dequant(u8(wq[g]), u8(ws[g]))
+        ref[sel] = O.dequant(a_rows[sel], as_rows[sel]) @ wdq.T
+    assert_close_to_oracle(y[idx], ref)
+
+
+# ---------------------------------------------------------------------------
+# wgrad
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("sizes,N,K", [
+    ([64, 0, 96, 32], 256, 256),            # empty expert, aligned
+    ([32, 160, 0, 0, 416], 320, 288),       # group starts not 128-aligned, N/K tails
+    ([1024], 128, 512),                     # one long group, several stages
+])
+@pytest.mark.parametrize("scaled", [True, False])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_wgrad_random_codes(gpu, sizes, N, K, scaled, out_dtype):
+    M = sum(sizes)
+    go_q, go_s = _rand_q((N, M), gpu, 51)
+    ia_q, ia_s = _rand_q((K, M), gpu, 52)
+    ends = workloads.ends_of(sizes)
+    dw = ops.grouped_wgrad(go_q.view(torch.float8_e4m3fn), ia_q.view(torch.float8_e4m3fn),
+                           torch.from_numpy(ends).to(gpu), go_s if scaled else None,
+                           ia_s if scaled else None, out_dtype=out_dtype)
+    ref = O.grouped_wgrad(u8(go_q), u8(go_s) if scaled else None, u8(ia_q),
+                          u8(ia_s) if scaled else None, ends)
+    for g in range(len(sizes)):
+        if sizes[g] == 0:
+            assert torch.all(dw[g] == 0)
+        else:
+            assert_close_to_oracle(dw[g], ref[g])
+
+
+def test_wgrad_reference_api_from_bf16(gpu):
+    g = torch.Generator(device=gpu).manual_seed(61)
+    sizes = [40, 0, 100, 7]
+    M = sum(sizes)
+    dy = (torch.randn(M, 192, generator=g, device=gpu) * 1e-3).to(torch.bfloat16)
+    x = torch.randn(M, 160, generator=g, device=gpu).to(torch.bfloat16)
+    offs = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    go, gos, pad = mxfp8gg.to_mxfp8_dim1(dy, offs)
+    ia, ias, pad2 = mxfp8gg.to_mxfp8_dim1(x, offs)
+    assert torch.equal(pad, pad2)
+    dw = wgrad_fused.wgrad_fused(go, ia, pad, gos, ias, out_dtype=torch.float32)
+    data = wgrad_fused.wgrad_prepare(go, ia, pad, gos, ias)
+    assert data["E"] == 4 and data["N"] == 192 and data["K"] == 160
+    dw2 = wgrad_fused.wgrad_kernel(data, out_dtype=torch.float32, BLOCK_M=128)
+    assert torch.equal(dw, dw2)
+    ref = O.grouped_wgrad(u8(go), u8(gos), u8(ia), u8(ias), pad.cpu().numpy())
+    for e in range(4):
+        if sizes[e]:
+            assert_close_to_oracle(dw[e], ref[e])
+        else:
+            assert torch.all(dw[e] == 0)
+    # bf16 default output, as in the reference
+    assert wgrad_fused.wgrad_fused(go, ia, pad, gos, ias).dtype == torch.bfloat16
+
+
+def test_wgrad_c4_sampled(gpu):
+    dy, x, sizes = workloads.c4(gpu)
+    offs = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    go, gos, pad = mxfp8gg.to_mxfp8_dim1(dy, offs)
+    ia, ias, _ = mxfp8gg.to_mxfp8_dim1(x, offs)
+    del dy, x
+    dw = ops.grouped_wgrad(go, ia, pad, gos, ias, out_dtype=torch.float32)
+    assert dw.shape == (32, 4096, 7168)
+    empty = np.nonzero(sizes == 0)[0]
+    assert len(empty) >= 2
+    for e in empty:
+        assert torch.all(dw[int(e)] == 0)
+    n_rows = np.array([0, 1, 2047, 4095])
+    k_rows = np.array([0, 5, 4000, 7167])
+    ni, ki = torch.from_numpy(n_rows).to(gpu), torch.from_numpy(k_rows).to(gpu)
+    ref = O.grouped_wgrad(u8(go[ni]), u8(gos[ni]), u8(ia[ki]), u8(ias[ki]), pad.cpu().numpy())
+    got = dw[:, ni][:, :, ki]
+    for e in range(32):
+        if sizes[e]:
+            assert_close_to_oracle(got[e], ref[e])
+    # linearity in the scales: one more on every dY scale doubles dW exactly
+    dw2 = ops.grouped_wgrad(go, ia, pad, gos + 1, ias, out_dtype=torch.float32)
+    assert torch.equal(dw2, 2 * dw)

@@ -1,0 +1,127 @@
+"""GPU parity of the bf16 -> MXFP8 casts against the CPU oracle: bit-exact
+payload and E8M0 bytes, both scale modes, both e4m3 encoders (hardware
+v_cvt_pk_fp8_f32 and the bit-level software encoder)."""
+import numpy as np
+import pytest
+import torch
+
+import mxfp8gg
+from mxfp8gg import _lib, ops, workloads
+from oracle import oracle as O
+from tests._helpers import bits, from_bits, u8
+
+pytestmark = pytest.mark.gpu
+
+MODES = [("rceil", O.RCEIL), ("floor", O.FLOOR)]
+ENCODERS = [0, _lib.CVT_SOFTWARE]
+
+
+def _dim0(x, mode_code):
+    return ops.to_mxfp8_dim0(x, mode_code)
+
+
+@pytest.mark.parametrize("name,mode", MODES)
+@pytest.mark.parametrize("enc", ENCODERS)
+def test_dim0_every_bf16_pattern(gpu, name, mode, enc):
+    # all 65536 bit patterns (incl. NaN, Inf, subnormals, -0), in order and shuffled
+    pats = np.arange(65536, dtype=np.uint16)
+    rng = np.random.default_rng(11)
+    x = np.concatenate([pats, rng.permutation(pats), rng.permutation(pats)]).reshape(-1, 256)
+    q, s = _dim0(from_bits(x, gpu), mode | enc)
+    rq, rs = O.quant_dim0(x, mode)
+    assert np.array_equal(u8(s), rs)
+    assert np.array_equal(u8(q), rq)
+
+
+@pytest.mark.parametrize("name,mode", MODES)
+def test_dim0_random_wide_dynamic_range(gpu, name, mode):
+    g = torch.Generator(device=gpu).manual_seed(12)
+    x = torch.randn(512, 1024, generator=g, device=gpu)
+    x = x * torch.exp2(torch.randint(-60, 60, (512, 32), generator=g, device=gpu).float()
+                       ).repeat_interleave(32, 1)
+    x = x.to(torch.bfloat16)
+    q, s = _dim0(x, mode)
+    rq, rs = O.quant_dim0(bits(x), mode)
+    assert np.array_equal(u8(s), rs) and np.array_equal(u8(q), rq)
+
+
+def test_dim0_strided_rows_and_3d(gpu):
+    g = torch.Generator(device=gpu).manual_seed(13)
+    base = torch.randn(64, 384, generator=g, device=gpu).to(torch.bfloat16)
+    x = base[:, :256]  # ldx = 384 > cols
+    q, s = ops.to_mxfp8_dim0(x)
+    rq, rs = O.quant_dim0(bits(x), O.RCEIL)
+    assert np.array_equal(u8(q), rq) and np.array_equal(u8(s), rs)
+    w = torch.randn(3, 40, 96, generator=g, device=gpu).to(torch.bfloat16)
+    q3, s3 = ops.to_mxfp8_dim0(w)
+    assert q3.shape == (3, 40, 96) and s3.shape == (3, 40, 3)
+    rq, rs = O.quant_dim0(bits(w.reshape(-1, 96)), O.RCEIL)
+    assert np.array_equal(u8(q3).reshape(-1, 96), rq)
+    assert np.array_equal(u8(s3).reshape(-1, 3), rs)
+
+
+def test_dim0_c2_activation_sampled_rows(gpu):
+    x, _, _ = workloads.c2(gpu)
+    q, s = ops.to_mxfp8_dim0(x)
+    rows = np.random.default_rng(14).choice(x.shape[0], 96, replace=False)
+    rows.sort()
+    rq, rs = O.quant_dim0(bits(x[torch.from_numpy(rows).to(gpu)]), O.RCEIL)
+    idx = torch.from_numpy(rows).to(gpu)
+    assert np.array_equal(u8(q[idx]), rq) and np.array_equal(u8(s[idx]), rs)
+    del x, q, s
+
+
+@pytest.mark.parametrize("name,mode", MODES)
+@pytest.mark.parametrize("enc", ENCODERS)
+@pytest.mark.parametrize("sizes", [[5, 0, 64, 33, 1, 40, 0], [128, 128], [300], [0, 0, 7]])
+def test_dim1_grouped_matches_oracle(gpu, name, mode, enc, sizes):
+    g = torch.Generator(device=gpu).manual_seed(15)
+    M = sum(sizes)
+    x = (torch.randn(M, 72, generator=g, device=gpu) * 3).to(torch.bfloat16)
+    ends = workloads.ends_of(sizes)
+    qt, st, pad = ops.to_mxfp8_dim1(x, torch.from_numpy(ends).to(gpu), mode | enc)
+    cap = qt.shape[1]
+    rq, rs, rpad = O.quant_dim1(bits(x), ends, cap, mode)
+    assert np.array_equal(pad.cpu().numpy(), rpad)
+    assert np.array_equal(u8(qt), rq)
+    assert np.array_equal(u8(st), rs)
+
+
+def test_dim1_ungrouped_and_torchao_layout(gpu):
+    g = torch.Generator(device=gpu).manual_seed(16)
+    x = torch.randn(96, 64, generator=g, device=gpu).to(torch.bfloat16)
+    qt, st, pad = ops.to_mxfp8_dim1(x)
+    assert pad is None and qt.shape == (64, 96)
+    rq, rs, _ = O.quant_dim1(bits(x), None, 96, O.RCEIL)
+    assert np.array_equal(u8(qt), rq) and np.array_equal(u8(st), rs)
+    d, sc = mxfp8gg.triton_to_mxfp8_dim1(x, scaling_mode="rceil")
+    assert d.shape == (96, 64) and d.stride() == (1, 96)   # column-major [M, K]
+    assert torch.equal(d.t().view(torch.uint8), qt.view(torch.uint8))
+    assert torch.equal(sc.view(torch.uint8), st)
+    d0, s0 = mxfp8gg.triton_to_mxfp8_dim0(x, scaling_mode="floor")
+    rq0, rs0 = O.quant_dim0(bits(x), O.FLOOR)
+    assert np.array_equal(u8(d0), rq0) and np.array_equal(u8(s0), rs0)
+
+
+def test_dim1_nan_inf_blocks(gpu):
+    x = torch.randn(64, 16, device=gpu).to(torch.bfloat16)
+    x[3, 2] = float("nan")
+    x[40, 5] = float("inf")
+    x[41, 6] = -float("inf")
+    ends = np.array([20, 64], dtype=np.int32)
+    for mode in (O.RCEIL, O.FLOOR):
+        qt, st, _ = ops.to_mxfp8_dim1(x, torch.from_numpy(ends).to(gpu), mode)
+        rq, rs, _ = O.quant_dim1(bits(x), ends, qt.shape[1], mode)
+        assert np.array_equal(u8(qt), rq) and np.array_equal(u8(st), rs)
+
+
+def test_dim1_c4_sampled_features(gpu):
+    dy, x, sizes = workloads.c4(gpu)
+    ends = workloads.ends_of(sizes)
+    feats = np.array([0, 1, 777, 4095])
+    qt, st, pad = ops.to_mxfp8_dim1(dy, torch.from_numpy(ends).to(gpu))
+    cap = qt.shape[1]
+    rq, rs, rpad = O.quant_dim1(bits(dy[:, torch.from_numpy(feats).to(gpu)]), ends, cap, O.RCEIL)
+    idx = torch.from_numpy(feats).to(gpu)
+    assert np.array_equal(pad.cpu().numpy(), rpad)
+    assert np.array_equal(u8(qt[idx]), rq) and np.array_equal(u8(st[idx]), rs)

@@ -1,0 +1,340 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the GPU checker.
+
+Each check is independent of the oracle's own formulas:
+  * e4m3: against torch's CPU float8_e4m3fn cast (an independent RNE
+    implementation) on every bf16 pattern, every tie point and random fp32;
+  * E8M0: against brute-force searches over candidate exponents written from
+    the rule's definition (smallest power covering amax/448; largest power
+    below amax);
+  * GEMM: against the reference's known answers (scale_correctness.py:228,
+    :310, :391), against pure-Python loops on tiny inputs, and the exact
+    power-of-two scaling invariant;
+  * dim1: against the transposed dim0 cast of each zero-padded group.
+"""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---------------------------------------------------------------------------
+# e4m3 payload encoding
+# ---------------------------------------------------------------------------
+def torch_e4m3(vals_f32: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(vals_f32.astype(np.float32)).to(torch.float8_e4m3fn).view(
+        torch.uint8).numpy()
+
+
+def test_e4m3_decode_matches_torch():
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    ref = codes.view(torch.float8_e4m3fn).float().double().numpy()
+    got = O.e4m3_table()
+    assert np.array_equal(np.isnan(ref), np.isnan(got))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(ref[ok], got[ok])
+
+
+def _enc(vals):
+    return np.array([O.e4m3_encode(v) for v in vals], dtype=np.uint8)
+
+
+def test_e4m3_encode_all_bf16_patterns():
+    bits = np.arange(65536, dtype=np.uint32) << 16
+    vals = bits.view(np.float32)
+    got = _enc(vals.astype(np.float64))
+    ref = torch_e4m3(vals)
+    assert np.array_equal(got, ref)
+
+
+def test_e4m3_encode_ties_and_neighbours():
+    table = O.e4m3_table()
+    pos = np.sort(table[:127])
+    mids = (pos[:-1] + pos[1:]) / 2.0  # exact tie points (representable in fp32)
+    vals = []
+    for m in mids.astype(np.float32):
+        vals += [np.nextafter(m, np.float32(-1)), m, np.nextafter(m, np.float32(1e9))]
+    vals = np.array(vals + [464.0, 464.0001, 479.99, 480.0, 1e30, -464.0, 2.0 ** -10,
+                            2.0 ** -10 * 1.0001, 2.0 ** -11], dtype=np.float32)
+    vals = np.concatenate([vals, -vals])
+    assert np.array_equal(_enc(vals.astype(np.float64)), torch_e4m3(vals))
+
+
+def test_e4m3_encode_random_fp32():
+    rng = np.random.default_rng(0)
+    vals = (rng.standard_normal(20000) * np.exp2(rng.integers(-14, 9, 20000))).astype(np.float32)
+    assert np.array_equal(_enc(vals.astype(np.float64)), torch_e4m3(vals))
+
+
+# ---------------------------------------------------------------------------
+# E8M0 scale rules
+# ---------------------------------------------------------------------------
+def _bf16_nonneg_finite():
+    bits = np.arange(0, 0x7F80, dtype=np.uint32) << 16
+    return bits.view(np.float32).astype(np.float64)
+
+
+def brute_rceil(amax: float) -> int:
+    """Smallest c in [-127, 127] with 448 * 2^c >= amax (c = -127 if amax is tiny)."""
+    for c in range(-127, 128):
+        if math.ldexp(448.0, c) >= amax:
+            return c + 127
+    return 254
+
+
+def brute_floor(amax: float) -> int:
+    """floor(log2 amax) by search, fp32-subnormal amax counted as exponent -127."""
+    if amax < 2.0 ** -126:
+        f = -127
+    else:
+        f = max(e for e in range(-126, 129) if 2.0 ** e <= amax)
+    return min(max(f - 8, -127), 128) + 127
+
+
+def test_e8m0_rceil_exhaustive_bf16():
+    vals = _bf16_nonneg_finite()
+    got = np.array([O.e8m0(v, O.RCEIL) for v in vals])
+    ref = np.array([0 if v == 0 else brute_rceil(v) for v in vals])
+    assert np.array_equal(got, ref)
+
+
+def test_e8m0_floor_exhaustive_bf16():
+    vals = _bf16_nonneg_finite()
+    got = np.array([O.e8m0(v, O.FLOOR) for v in vals])
+    ref = np.array([0 if v == 0 else brute_floor(v) for v in vals])
+    assert np.array_equal(got, ref)
+
+
+def test_e8m0_specials():
+    assert O.e8m0(float("nan"), O.RCEIL) == 255
+    assert O.e8m0(float("nan"), O.FLOOR) == 255
+    assert O.e8m0(float("inf"), O.RCEIL) == 254
+    assert O.e8m0(float("inf"), O.FLOOR) == 247
+    assert O.e8m0(448.0, O.RCEIL) == 127           # amax/448 = 1 exactly
+    assert O.e8m0(448.0 * 2 ** 5, O.RCEIL) == 132
+    assert O.e8m0(449.0, O.RCEIL) == 128
+    assert O.e8m0(1.0, O.FLOOR) == 119             # 2^0 / 2^8
+
+
+def test_rceil_payload_of_block_max_is_in_top_binade():
+    # RCEIL maps the block max into (224, 448]; FLOOR into [256, 512) before clamping.
+    rng = np.random.default_rng(1)
+    for v in np.abs(rng.standard_normal(2000)) * np.exp2(rng.integers(-40, 40, 2000)):
+        v = float(np.float32(v))
+        b = O.e8m0(v, O.RCEIL)
+        y = O.e4m3_table()[O.payload(v, b, O.RCEIL)]
+        assert 224.0 <= y <= 448.0
+
+
+# ---------------------------------------------------------------------------
+# dim0 cast: round-trip bound and known blocks
+# ---------------------------------------------------------------------------
+def _bf16_bits(x: torch.Tensor) -> np.ndarray:
+    return x.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("mode", [O.RCEIL, O.FLOOR])
+def test_dim0_round_trip_error_bound(mode):
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(64, 256, generator=g) * torch.exp2(torch.randint(-20, 20, (64, 1), generator=g).float())).to(torch.bfloat16)
+    q, s = O.quant_dim0(_bf16_bits(x), mode)
+    back = O.dequant(q, s)
+    xv = x.double().numpy()
+    step = np.repeat(np.ldexp(1.0, s.astype(np.int64) - 127 - 9), 32, axis=1)  # subnormal step
+    # RCEIL keeps the block max <= 448 (rounding only, 3 mantissa bits: 2^-4);
+    # FLOOR scales it into [256, 512) and clamps at 448 (up to 2^-3).
+    rel = 2.0 ** -4 if mode == O.RCEIL else 2.0 ** -3
+    assert np.all(np.abs(back - xv) <= np.abs(xv) * rel + step / 2)
+
+
+def test_dim0_constant_block_known_answer():
+    x = torch.ones(1, 32, dtype=torch.bfloat16)
+    q, s = O.quant_dim0(_bf16_bits(x), O.RCEIL)
+    assert s[0, 0] == 119 and np.all(q == 0x78)      # 1.0 * 2^8 = 256 -> 0x78
+    x = torch.full((1, 32), 448.0, dtype=torch.bfloat16)
+    q, s = O.quant_dim0(_bf16_bits(x), O.RCEIL)
+    assert s[0, 0] == 127 and np.all(q == 0x7E)
+    x = torch.zeros(1, 32, dtype=torch.bfloat16)
+    q, s = O.quant_dim0(_bf16_bits(x), O.RCEIL)
+    assert s[0, 0] == 0 and np.all(q == 0)
+
+
+# ---------------------------------------------------------------------------
+# dim1 cast: relation to dim0
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("mode", [O.RCEIL, O.FLOOR])
+def test_dim1_equals_transposed_dim0_per_group(mode):
+    g = torch.Generator().manual_seed(4)
+    sizes = [5, 0, 64, 33, 1, 40]
+    M = sum(sizes)
+    x = torch.randn(M, 16, generator=g).to(torch.bfloat16)
+    ends = np.cumsum(sizes).astype(np.int32)
+    cap = (M + 31 * len(sizes) + 31) // 32 * 32
+    qt, st, pad = O.quant_dim1(_bf16_bits(x), ends, cap, mode)
+    b = 0
+    p = 0
+    for sz, e in zip(sizes, ends):
+        padded = (sz + 31) // 32 * 32
+        blk = torch.zeros(padded, 16, dtype=torch.bfloat16)
+        blk[:sz] = x[b:e]
+        q0, s0 = O.quant_dim0(_bf16_bits(blk.t().contiguous()), mode)
+        assert np.array_equal(qt[:, p:p + padded], q0)
+        assert np.array_equal(st[:, p // 32:(p + padded) // 32], s0)
+        p += padded
+        b = e
+    assert list(pad) == list(np.cumsum([(s + 31) // 32 * 32 for s in sizes]))
+    assert np.all(qt[:, p:] == 0)
+
+
+# ---------------------------------------------------------------------------
+# GEMM references
+# ---------------------------------------------------------------------------
+def _kat(name):
+    return json.loads((GOLDEN / "scale_kats.json").read_text())[name]
+
+
+def _ones_fp8(*shape):
+    return np.full(shape, 0x38, dtype=np.uint8)  # e4m3 1.0
+
+
+def test_kat_scale_byte_interpretation():
+    k = _kat("scale_bypass")  # scale_correctness.py:181-251
+    M, N, K, E = k["M"], k["N"], k["K"], k["E"]
+    a_s = np.array(k["a_scale_row"], dtype=np.uint8)[None, :].repeat(M, 0)
+    w_s = np.full((E, N, K // 32), 127, np.uint8)
+    y = O.grouped_fwd(_ones_fp8(M, K), a_s, _ones_fp8(E, N, K), w_s, np.array(k["ends"]))
+    assert np.all(y == k["expected"])
+
+
+def test_kat_scale_application_order():
+    k = _kat("application_order")  # scale_correctness.py:258-337
+    M, N, K = k["M"], k["N"], k["K"]
+    a_s = np.array(k["a_scale_row"], dtype=np.uint8)[None, :].repeat(M, 0)
+    w_s = np.array(k["w_scale_row"], dtype=np.uint8)[None, None, :].repeat(N, 1)
+    y = O.grouped_fwd(_ones_fp8(M, K), a_s, _ones_fp8(1, N, K), w_s, np.array(k["ends"]))
+    assert np.all(y == k["expected"])
+
+
+def test_kat_scale_layout_per_row():
+    k = _kat("scale_layout")  # scale_correctness.py:344-401
+    M, N, K = k["M"], k["N"], k["K"]
+    a_s = np.full((M, K // 32), 127, np.uint8)
+    a_s[:, 0] = np.minimum(127 + np.arange(M), 254)
+    w_s = np.full((1, N, K // 32), 127, np.uint8)
+    y = O.grouped_fwd(_ones_fp8(M, K), a_s, _ones_fp8(1, N, K), w_s, np.array(k["ends"]))
+    expect = 32.0 * np.ldexp(1.0, a_s[:, 0].astype(int) - 127) + 32.0
+    # exact while 32*2^m + 32 fits in 53 bits; beyond, each of the 32 unit terms
+    # may round away (relative 32 * 2^-53)
+    assert np.allclose(y, np.repeat(expect[:, None], N, 1), rtol=2.0 ** -47, atol=0.0)
+    assert np.array_equal(y[:40], np.repeat(expect[:40, None], N, 1))
+
+
+def test_kat_known_scales_against_torch_dequant():
+    # scale_correctness.py:52-174: arange data, A scales alternating 2.0/1.0 per block.
+    M, N, K, E = 64, 96, 128, 2
+    # the reference's arange * 0.1 data, wrapped below 400 so it stays finite in e4m3
+    a_vals = ((torch.arange(M * K, dtype=torch.float32) % 4000).reshape(M, K) * 0.1).to(torch.bfloat16)
+    w_vals = ((torch.arange(E * N * K, dtype=torch.float32) % 4000).reshape(E, N, K) * 0.1).to(
+        torch.bfloat16)
+    a_s = np.full((M, K // 32), 127, np.uint8)
+    a_s[:, ::2] = 128
+    w_s = np.full((E, N, K // 32), 127, np.uint8)
+    sa = torch.from_numpy(np.ldexp(1.0, a_s.astype(np.int64) - 127)).repeat_interleave(32, 1)
+    sw = torch.from_numpy(np.ldexp(1.0, w_s.astype(np.int64) - 127)).repeat_interleave(32, 2)
+    a_q = (a_vals.double() / sa).float().to(torch.float8_e4m3fn)
+    w_q = (w_vals.double() / sw).float().to(torch.float8_e4m3fn)
+    # independent reference: torch's float8 decode, float64 matmul per group
+    ref = torch.empty(M, N, dtype=torch.float64)
+    ref[:32] = (a_q[:32].double() * sa[:32]) @ (w_q[0].double() * sw[0]).T
+    ref[32:] = (a_q[32:].double() * sa[32:]) @ (w_q[1].double() * sw[1]).T
+    y = O.grouped_fwd(a_q.view(torch.uint8).numpy(), a_s, w_q.view(torch.uint8).numpy(), w_s,
+                      np.array([32, 64]))
+    assert np.array_equal(y, ref.numpy())
+
+
+def test_grouped_fwd_brute_force_loops():
+    rng = np.random.default_rng(5)
+    M, N, K, E = 11, 5, 64, 4
+    ends = np.array([3, 3, 9, 11])  # group 1 empty
+    a_q = rng.integers(0, 0x7E, (M, K)).astype(np.uint8) | (rng.integers(0, 2, (M, K)) << 7).astype(np.uint8)
+    w_q = rng.integers(0, 0x7E, (E, N, K)).astype(np.uint8)
+    a_s = rng.integers(120, 134, (M, K // 32)).astype(np.uint8)
+    w_s = rng.integers(120, 134, (E, N, K // 32)).astype(np.uint8)
+    y = O.grouped_fwd(a_q, a_s, w_q, w_s, ends)
+    tdec = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).double()
+    dec = lambda c: float(tdec[int(c)])
+    beg = 0
+    for g, e in enumerate(ends):
+        for m in range(beg, e):
+            for n in range(N):
+                acc = 0.0
+                for k in range(K):
+                    acc += (dec(a_q[m, k]) * 2.0 ** (int(a_s[m, k // 32]) - 127)
+                            * dec(w_q[g, n, k]) * 2.0 ** (int(w_s[g, n, k // 32]) - 127))
+                assert y[m, n] == pytest.approx(acc, rel=1e-12, abs=1e-300)
+        beg = e
+
+
+def test_scale_bump_doubles_output_exactly():
+    rng = np.random.default_rng(6)
+    M, N, K, E = 40, 24, 96, 2
+    a_q = rng.integers(0, 0x7E, (M, K)).astype(np.uint8)
+    w_q = rng.integers(0, 0x7E, (E, N, K)).astype(np.uint8)
+    a_s = rng.integers(110, 140, (M, K // 32)).astype(np.uint8)
+    w_s = rng.integers(110, 140, (E, N, K // 32)).astype(np.uint8)
+    ends = np.array([17, 40])
+    y = O.grouped_fwd(a_q, a_s, w_q, w_s, ends)
+    y2 = O.grouped_fwd(a_q, a_s + 1, w_q, w_s, ends)
+    assert np.array_equal(y2, 2.0 * y)
+
+
+def test_wgrad_brute_force_loops():
+    rng = np.random.default_rng(7)
+    N, K, M = 3, 4, 96
+    ends = np.array([32, 32, 96])  # group 1 empty
+    go = rng.integers(0, 0x7E, (N, M)).astype(np.uint8)
+    ia = rng.integers(0, 0x7E, (K, M)).astype(np.uint8)
+    gs = rng.integers(120, 134, (N, M // 32)).astype(np.uint8)
+    is_ = rng.integers(120, 134, (K, M // 32)).astype(np.uint8)
+    dw = O.grouped_wgrad(go, gs, ia, is_, ends)
+    dec = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).double().numpy()
+    beg = 0
+    for g, e in enumerate(ends):
+        for n in range(N):
+            for k in range(K):
+                acc = sum(dec[go[n, t]] * 2.0 ** (int(gs[n, t // 32]) - 127) * dec[ia[k, t]]
+                          * 2.0 ** (int(is_[k, t // 32]) - 127) for t in range(beg, e))
+                assert dw[g, n, k] == pytest.approx(acc, rel=1e-12, abs=0.0)
+        beg = e
+    assert np.all(dw[1] == 0)
+
+
+# ---------------------------------------------------------------------------
+# golden fixture (config 1)
+# ---------------------------------------------------------------------------
+def test_c1_golden_fixture():
+    import hashlib
+    import sys
+
+    sys.path.insert(0, str(Path(__file__).resolve().parent.parent / "mxfp8-grouped-gemm_amd"))
+    from mxfp8gg import workloads
+
+    fx = json.loads((GOLDEN / "c1_golden.json").read_text())
+    x, w, sizes = workloads.c1("cpu")
+    xq, xs = O.quant_dim0(_bf16_bits(x), O.RCEIL)
+    wq, ws = O.quant_dim0(_bf16_bits(w.reshape(-1, 256)), O.RCEIL)
+    h = lambda a: hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+    assert h(_bf16_bits(x)) == fx["x_sha256"]
+    assert h(xq) == fx["xq_sha256"] and h(xs) == fx["xs_sha256"]
+    assert h(wq) == fx["wq_sha256"] and h(ws) == fx["ws_sha256"]
+    y = O.grouped_fwd(xq, xs, wq.reshape(4, 512, 256), ws.reshape(4, 512, 8),
+                      workloads.ends_of(sizes))
+    probe = np.array(fx["y_probe"])
+    idx = np.array(fx["y_probe_index"])
+    assert np.allclose(y[idx[:, 0], idx[:, 1]], probe, rtol=0, atol=1e-9)
