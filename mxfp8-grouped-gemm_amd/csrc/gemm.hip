@@ -211,10 +211,13 @@ __device__ __forceinline__ void drain_and_barrier() {
   __syncthreads();
 }
 
-__device__ __forceinline__ v8i lds_frag(const uint8_t* base, uint32_t row, uint32_t c0) {
+// MFMA operand of one lane: two 16-byte chunks (logical chunk indices clo and
+// chi of an LDS row).
+__device__ __forceinline__ v8i lds_frag(const uint8_t* base, uint32_t row, uint32_t clo,
+                                        uint32_t chi) {
   const uint32_t s = swz(row);
-  const uint4 lo = *reinterpret_cast<const uint4*>(base + row * kTileK + (((c0) ^ s) << 4));
-  const uint4 hi = *reinterpret_cast<const uint4*>(base + row * kTileK + (((c0 + 1u) ^ s) << 4));
+  const uint4 lo = *reinterpret_cast<const uint4*>(base + row * kTileK + ((clo ^ s) << 4));
+  const uint4 hi = *reinterpret_cast<const uint4*>(base + row * kTileK + ((chi ^ s) << 4));
   v8i f;
   f[0] = (int)lo.x; f[1] = (int)lo.y; f[2] = (int)lo.z; f[3] = (int)lo.w;
   f[4] = (int)hi.x; f[5] = (int)hi.y; f[6] = (int)hi.z; f[7] = (int)hi.w;
@@ -239,14 +242,21 @@ __device__ __forceinline__ void compute_stage(const Smem& sm, int buf, v16f (&ac
       sb[i] = kScaleOne;
     }
   }
+  // Operand layout of v_mfma_scale_f32_32x32x64_f8f6f4 (fp8): lane l serves
+  // row l%32; its bytes 0..15 belong to scale block 0 and bytes 16..31 to
+  // block 1 of the 64-deep step, both halves of the wave sharing each block,
+  // and the block-b scale of row r comes from lane r + 32b.  So for substep s
+  // (k-blocks 2s, 2s+1 of the stage) lane half h takes chunk 4s+h of block 2s
+  // and chunk 4s+2+h of block 2s+1, and its scale byte is byte 2s+h of the
+  // row's scale word: (word >> 8h) with op_sel 2s.
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     v8i fa[4], fb[4];
-    const uint32_t c0 = 4u * s + 2u * h;
+    const uint32_t clo = 4u * s + h, chi = 4u * s + 2u + h;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = lds_frag(sm.p[buf], wp * 128u + 32u * i + l32, c0);
+    for (int i = 0; i < 4; ++i) fa[i] = lds_frag(sm.p[buf], wp * 128u + 32u * i + l32, clo, chi);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) fb[j] = lds_frag(sm.q[buf], wq * 128u + 32u * j + l32, c0);
+    for (int j = 0; j < 4; ++j) fb[j] = lds_frag(sm.q[buf], wq * 128u + 32u * j + l32, clo, chi);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll

@@ -80,6 +80,29 @@ def test_kat_per_column_and_per_block_scales(gpu):
     assert torch.equal(c.double(), expect[None, :].expand(M, N))
 
 
+def test_kat_scale_pairs_with_its_own_32_elements(gpu):
+    # Row data: k-block 0 all 1.0, k-block 1 all 0; A scales 2^3 / 2^0.  Only a
+    # kernel that applies each scale to exactly its own 32 contiguous elements
+    # gives 32 * 8 = 256 (pairing half-blocks would give 16*8 + 16*1 = 144).
+    M, N, K = 32, 32, 64
+    a = torch.zeros((M, K), dtype=torch.bfloat16, device=gpu)
+    a[:, :32] = 1.0
+    a_s = torch.full((M, 2), 127, dtype=torch.uint8, device=gpu)
+    a_s[:, 0] = 130
+    w_s = torch.full((1, N, 2), 127, dtype=torch.uint8, device=gpu)
+    c = ops.grouped_mm(a.to(torch.float8_e4m3fn), _ones((1, N, K), gpu), None, a_s, w_s,
+                       out_dtype=torch.float32)
+    assert torch.all(c == 256.0)
+    # same on the W side, block 1 carrying the data
+    w = torch.zeros((1, N, K), dtype=torch.bfloat16, device=gpu)
+    w[:, :, 32:] = 1.0
+    w_s[:, :, 1] = 125
+    c = ops.grouped_mm(_ones((M, K), gpu), w.to(torch.float8_e4m3fn), None,
+                       torch.full((M, 2), 127, dtype=torch.uint8, device=gpu), w_s,
+                       out_dtype=torch.float32)
+    assert torch.all(c == 8.0)
+
+
 # ---------------------------------------------------------------------------
 # random data against the oracle
 # ---------------------------------------------------------------------------
