@@ -90,8 +90,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "fwd"], default="all",
-                    help="fwd: time only the headline forward (for profiler runs)")
+    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy"], default="all",
+                    help="fwd / wgrad: time only that GEMM (for profiler runs); copy: a plain "
+                         "1 GiB device-to-device copy, the reference for HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the MXFP8 grouped GEMM shards by expert and "
@@ -106,6 +107,31 @@ def main():
 
     dev = torch.device("cuda:0")
     mxfp8gg.load_library()
+
+    if args.only == "copy":
+        nbytes = 1 << 30
+        src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        ms = time_launches(lambda: dst.copy_(src), args.steps, args.warmup, torch)
+        print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
+                          "ms": round(ms, 4), "GBps": round(2 * nbytes / ms / 1e6, 1)}),
+              flush=True)
+        return
+    if args.only == "wgrad":
+        dy, x4, s4 = workloads.c4(dev)
+        e4 = torch.from_numpy(workloads.ends_of(s4)).to(dev)
+        go, gos, pad = mxfp8gg.to_mxfp8_dim1(dy, e4)
+        ia, ias, _ = mxfp8gg.to_mxfp8_dim1(x4, e4)
+        n4, k4 = dy.shape[1], x4.shape[1]
+        del dy, x4
+        dw = torch.empty((32, n4, k4), dtype=torch.float32, device=dev)
+        ms4 = time_launches(
+            lambda: mxfp8gg.grouped_wgrad(go, ia, pad, gos, ias, out_dtype=torch.float32, out=dw),
+            args.steps, args.warmup, torch)
+        f4 = workloads.gemm_flops(int(s4.sum()), n4, k4)
+        print(json.dumps({"wgrad_c4_ms": round(ms4, 4), "tflops": round(f4 / ms4 / 1e9, 1)}),
+              flush=True)
+        return
 
     # ---- headline: C2 forward ---------------------------------------------
     log("C2: generating and quantising operands")

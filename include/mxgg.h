@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 1
+#define MXGG_ABI_VERSION 2
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -52,6 +52,20 @@ typedef enum mxgg_out_dtype {
   MXGG_OUT_F32 = 1
 } mxgg_out_dtype;
 
+/*
+ * Memory layout of an E8M0 scale matrix that is logically [rows, nblk]
+ * (nblk = contraction length / 32):
+ *   ROW_MAJOR   : byte (r, b) at s[r * ld + b]   (the reference's [M, K//32]
+ *                 uint8 tensors, fused_fwd.py:182-183)
+ *   BLOCK_MAJOR : byte (r, b) at s[b * ld + r]   (one row of bytes per
+ *                 32-deep k-block; what the GEMM kernels consume, so a stage
+ *                 of 256 rows reads its scales as one contiguous run)
+ */
+typedef enum mxgg_scale_layout {
+  MXGG_SCALES_ROW_MAJOR = 0,
+  MXGG_SCALES_BLOCK_MAJOR = 1
+} mxgg_scale_layout;
+
 /* ABI version of the loaded library (MXGG_ABI_VERSION at build time). */
 int mxgg_abi_version(void);
 
@@ -65,14 +79,14 @@ const char* mxgg_last_error(void);
  * Row-wise MXFP8 cast: 1x32 blocks along the last (contiguous) dimension.
  *   x      : bf16 [rows, cols], row stride ldx
  *   q      : e4m3 [rows, cols], row stride ldq
- *   scales : E8M0 [rows, cols/32], row stride lds
+ *   scales : E8M0, logically [rows, cols/32], in `scale_layout` with stride lds
  * cols % 32 == 0.  Payload = RNE_e4m3(clamp(x * 2^(127-b), -448, 448)).
  * Replaces torchao's triton_to_mxfp8_dim0 (called by the reference's trainer
  * path, port_mxfp8.py:43-49) and the eager `.to(torch.float8_e4m3fn)` casts on
  * the forward path (e2e_bench.py:238-243, fused_fwd.py:274-275).
  */
 int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx,
-                    void* q, int64_t ldq, void* scales, int64_t lds,
+                    void* q, int64_t ldq, void* scales, int64_t lds, int scale_layout,
                     int scale_mode, void* stream);
 
 /*
@@ -85,25 +99,44 @@ int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx,
  *   rows_pad_cap   : number of padded token columns the outputs can hold; must
  *                    be >= round_up(rows + 31*num_groups, 32) (NULL groups: round_up(rows,32))
  *   qt             : e4m3 [cols, rows_pad_cap], row stride ldqt
- *   scales_t       : E8M0 [cols, rows_pad_cap/32], row stride ldst
+ *   scales_t       : E8M0, logically [cols, rows_pad_cap/32], in
+ *                    `scale_layout` with stride ldst
  *   group_ends_pad : int32 [num_groups] padded cumulative ends (device, written)
  *                    or NULL when group_ends is NULL
- * Columns past the padded total are written as zero payload / 0x7F scale.
+ * Columns past the padded total are written as zero payload with the scale of an
+ * all-zero block (byte 0).
  * Replaces torchao's triton_to_mxfp8_dim1 (port_mxfp8.py:43) plus the
  * transpose-and-stack copies of wgrad_fused.py:48-62 / e2e_bench.py:317-328.
  */
 int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
                     const int32_t* group_ends, int64_t num_groups,
                     int64_t rows_pad_cap, void* qt, int64_t ldqt,
-                    void* scales_t, int64_t ldst, int32_t* group_ends_pad,
-                    int scale_mode, void* stream);
+                    void* scales_t, int64_t ldst, int scale_layout,
+                    int32_t* group_ends_pad, int scale_mode, void* stream);
+
+/*
+ * Re-lay E8M0 scales from ROW_MAJOR to BLOCK_MAJOR, batched:
+ *   dst[b][k][r] = src[b][r][k]   for b < batch, r < rows, k < nblk
+ * src batch stride / row stride: src_bstride / lds; dst: dst_bstride / ldd.
+ * For callers holding the reference's row-major [M, K/32] / [E, N, K/32]
+ * uint8 scales; the library's own casts can emit BLOCK_MAJOR directly.
+ * (No reference counterpart: the reference's kernels read row-major scales
+ * inside the GEMM, fused_fwd.py:112-123.)
+ */
+int mxgg_scales_to_block_major(const void* src, int64_t batch, int64_t rows, int64_t nblk,
+                               int64_t src_bstride, int64_t lds, void* dst,
+                               int64_t dst_bstride, int64_t ldd, void* stream);
 
 /*
  * Forward grouped GEMM  out[rows of g] = A[rows of g] . W[g]^T  (fp32 accumulate).
  *   a        : e4m3 [M, K], row stride lda
- *   a_scales : E8M0 [M, K/32], row stride ldas                (or NULL)
+ *   a_scales : E8M0 BLOCK_MAJOR [K/32][ldas], ldas >= M       (or NULL)
  *   w        : e4m3 [E, N, K]: expert g at w + g*w_group_stride, row stride ldw
- *   w_scales : E8M0 [E, N, K/32]: expert g at + g*ws_group_stride, row stride ldws (or NULL)
+ *   w_scales : E8M0 BLOCK_MAJOR, expert g at + g*ws_group_stride: [K/32][ldws],
+ *              ldws >= N                                       (or NULL)
+ *   Scale strides and bases are multiples of 4 bytes, and a block-major array
+ *   of nblk block-rows holding `rows` rows must be readable for
+ *   (nblk-1)*ld + round_up(rows, 4) bytes from its base (per expert for w).
  *   group_ends : int32 [num_groups] (device) or NULL for one group of M rows
  *   out      : [M, N] bf16 or f32 (out_dtype), row stride ldo
  * a_scales and w_scales are both given or both NULL (NULL = every scale 1.0,
@@ -123,9 +156,11 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
  *   dw[g] = sum over tokens t of group g of  go_t[:, t] (x) ia_t[:, t]
  * i.e. dW_g = dY_g^T . X_g with both operands stored token-contiguous.
  *   go_t        : e4m3 [N, M], row stride ldgo  (dY transposed)
- *   go_scales_t : E8M0 [N, M/32], row stride ldgos        (or NULL)
+ *   go_scales_t : E8M0 BLOCK_MAJOR [M/32][ldgos], ldgos >= N   (or NULL)
  *   ia_t        : e4m3 [K, M], row stride ldia  (X transposed)
- *   ia_scales_t : E8M0 [K, M/32], row stride ldias        (or NULL)
+ *   ia_scales_t : E8M0 BLOCK_MAJOR [M/32][ldias], ldias >= K   (or NULL)
+ *                 (strides and bases multiples of 4; readable extent as for
+ *                 mxgg_grouped_fwd)
  *   group_ends  : int32 [num_groups] token ends (device); every end must be a
  *                 multiple of 32 when scales are given (the padded layout that
  *                 mxgg_quant_dim1 produces), so a scale block never straddles

@@ -74,11 +74,18 @@ const char* mxgg_status_string(int status) {
 
 const char* mxgg_last_error(void) { return g_last_error; }
 
+static bool valid_layout(int layout) {
+  return layout == MXGG_SCALES_ROW_MAJOR || layout == MXGG_SCALES_BLOCK_MAJOR;
+}
+
 int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx, void* q, int64_t ldq,
-                    void* scales, int64_t lds, int scale_mode, void* stream) {
+                    void* scales, int64_t lds, int scale_layout, int scale_mode, void* stream) {
   const int mode = scale_mode & 0xFF;
   if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim0: unknown scale_mode %d", scale_mode);
+  if (!valid_layout(scale_layout))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim0: unknown scale_layout %d",
+                     scale_layout);
   if (rows < 0 || cols < 0)
     return set_error(MXGG_ERR_SHAPE, "quant_dim0: negative size rows=%lld cols=%lld",
                      (long long)rows, (long long)cols);
@@ -88,7 +95,8 @@ int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx, void
   if (rows == 0 || cols == 0) return MXGG_OK;
   if (!x || !q || !scales)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim0: null pointer");
-  if (ldx < cols || ldq < cols || lds < cols / 32)
+  if (ldx < cols || ldq < cols ||
+      lds < (scale_layout == MXGG_SCALES_BLOCK_MAJOR ? rows : cols / 32))
     return set_error(MXGG_ERR_SHAPE, "quant_dim0: leading dimension smaller than the row");
   if (!aligned16(x) || !aligned16(q) || ldx % 8 != 0 || ldq % 8 != 0 ||
       (reinterpret_cast<uintptr_t>(q) & 7u) != 0)
@@ -96,18 +104,21 @@ int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx, void
                      "quant_dim0: x and q must be 16-byte aligned, ldx and ldq multiples of 8");
   return check_launch(launch_quant_dim0(static_cast<const uint16_t*>(x), rows, cols, ldx,
                                         static_cast<uint8_t*>(q), ldq,
-                                        static_cast<uint8_t*>(scales), lds, scale_mode,
-                                        static_cast<hipStream_t>(stream)),
+                                        static_cast<uint8_t*>(scales), lds, scale_layout,
+                                        scale_mode, static_cast<hipStream_t>(stream)),
                       "quant_dim0");
 }
 
 int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
                     const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap,
-                    void* qt, int64_t ldqt, void* scales_t, int64_t ldst,
+                    void* qt, int64_t ldqt, void* scales_t, int64_t ldst, int scale_layout,
                     int32_t* group_ends_pad, int scale_mode, void* stream) {
   const int mode = scale_mode & 0xFF;
   if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim1: unknown scale_mode %d", scale_mode);
+  if (!valid_layout(scale_layout))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim1: unknown scale_layout %d",
+                     scale_layout);
   if (rows < 0 || cols < 0 || rows_pad_cap < 0)
     return set_error(MXGG_ERR_SHAPE, "quant_dim1: negative size");
   if (cols % 8 != 0)
@@ -132,7 +143,8 @@ int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
   if (cols == 0 || rows_pad_cap == 0) return MXGG_OK;
   if (!x && rows > 0) return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim1: null x");
   if (!qt || !scales_t) return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim1: null output");
-  if (ldx < cols || ldqt < rows_pad_cap || ldst < rows_pad_cap / 32)
+  if (ldx < cols || ldqt < rows_pad_cap ||
+      ldst < (scale_layout == MXGG_SCALES_BLOCK_MAJOR ? cols : rows_pad_cap / 32))
     return set_error(MXGG_ERR_SHAPE, "quant_dim1: leading dimension smaller than the row");
   if ((x && !aligned16(x)) || !aligned16(qt) || ldx % 8 != 0 || ldqt % 16 != 0)
     return set_error(MXGG_ERR_ALIGNMENT,
@@ -142,9 +154,29 @@ int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
   return check_launch(
       launch_quant_dim1(static_cast<const uint16_t*>(x), rows, cols, ldx, group_ends, groups,
                         rows_pad_cap, static_cast<uint8_t*>(qt), ldqt,
-                        static_cast<uint8_t*>(scales_t), ldst, group_ends_pad, scale_mode,
-                        static_cast<hipStream_t>(stream)),
+                        static_cast<uint8_t*>(scales_t), ldst, scale_layout, group_ends_pad,
+                        scale_mode, static_cast<hipStream_t>(stream)),
       "quant_dim1");
+}
+
+int mxgg_scales_to_block_major(const void* src, int64_t batch, int64_t rows, int64_t nblk,
+                               int64_t src_bstride, int64_t lds, void* dst,
+                               int64_t dst_bstride, int64_t ldd, void* stream) {
+  if (batch < 0 || rows < 0 || nblk < 0)
+    return set_error(MXGG_ERR_SHAPE, "scales_to_block_major: negative size");
+  if (batch == 0 || rows == 0 || nblk == 0) return MXGG_OK;
+  if (!src || !dst)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "scales_to_block_major: null pointer");
+  if (lds < nblk || ldd < rows || (batch > 1 && (src_bstride < rows * lds ||
+                                                  dst_bstride < nblk * ldd)))
+    return set_error(MXGG_ERR_SHAPE, "scales_to_block_major: strides smaller than the data");
+  if (batch > 65535)
+    return set_error(MXGG_ERR_UNSUPPORTED, "scales_to_block_major: batch above 65535");
+  return check_launch(
+      launch_scales_to_block_major(static_cast<const uint8_t*>(src), batch, rows, nblk,
+                                   src_bstride, lds, static_cast<uint8_t*>(dst), dst_bstride,
+                                   ldd, static_cast<hipStream_t>(stream)),
+      "scales_to_block_major");
 }
 
 int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
@@ -169,12 +201,22 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
                      (long long)num_groups, (long long)kMaxGroupsAbi);
   if (M == 0 || N == 0) return MXGG_OK;
   if (!a || !w || !out) return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd: null pointer");
-  if (lda < K || ldw < K || ldo < N || (scaled && (ldas < K / 32 || ldws < K / 32)))
-    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: leading dimension smaller than the row");
+  if (lda < K || ldw < K || ldo < N || (scaled && (ldas < M || ldws < N)))
+    return set_error(MXGG_ERR_SHAPE,
+                     "grouped_fwd: leading dimension smaller than the row (block-major scales: "
+                     "ldas >= M, ldws >= N)");
   if (E > 1 && w_group_stride < N * ldw)
     return set_error(MXGG_ERR_SHAPE, "grouped_fwd: w_group_stride smaller than one expert");
-  if (scaled && E > 1 && ws_group_stride < N * ldws)
-    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: ws_group_stride smaller than one expert");
+  if (scaled && E > 1 && ws_group_stride < N)
+    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: ws_group_stride < N overlaps experts");
+  if (scaled && ((reinterpret_cast<uintptr_t>(a_scales) | reinterpret_cast<uintptr_t>(w_scales)) %
+                     4 != 0 ||
+                 ldas % 4 != 0 || ldws % 4 != 0 || (E > 1 && ws_group_stride % 4 != 0)))
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "grouped_fwd: scale bases, strides and expert stride must be multiples of 4");
+  if (scaled && ((K / 32) * ldas > kMaxBufferBytes || (K / 32) * ldws > kMaxBufferBytes ||
+                 (E - 1) * ws_group_stride + (K / 32) * ldws > INT64_C(1) << 40))
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_fwd: scale array larger than 2 GiB");
   if (!aligned16(a) || !aligned16(w) || lda % 16 != 0 || ldw % 16 != 0 ||
       (E > 1 && w_group_stride % 16 != 0))
     return set_error(MXGG_ERR_ALIGNMENT,
@@ -235,8 +277,17 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
   if (!dw) return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: null dw");
   if (M > 0 && (!go_t || !ia_t))
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: null operand");
-  if (ldgo < M || ldia < M || (scaled && (ldgos < M / 32 || ldias < M / 32)))
-    return set_error(MXGG_ERR_SHAPE, "grouped_wgrad: leading dimension smaller than the row");
+  if (ldgo < M || ldia < M || (scaled && (ldgos < N || ldias < K)))
+    return set_error(MXGG_ERR_SHAPE,
+                     "grouped_wgrad: leading dimension smaller than the row (block-major scales: "
+                     "ldgos >= N, ldias >= K)");
+  if (scaled && ((reinterpret_cast<uintptr_t>(go_scales_t) |
+                  reinterpret_cast<uintptr_t>(ia_scales_t)) % 4 != 0 ||
+                 ldgos % 4 != 0 || ldias % 4 != 0))
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "grouped_wgrad: scale bases and strides must be multiples of 4");
+  if (scaled && ((M / 32) * ldgos > kMaxBufferBytes || (M / 32) * ldias > kMaxBufferBytes))
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_wgrad: scale array larger than 2 GiB");
   if ((go_t && !aligned16(go_t)) || (ia_t && !aligned16(ia_t)) || ldgo % 16 != 0 ||
       ldia % 16 != 0)
     return set_error(MXGG_ERR_ALIGNMENT,

@@ -30,20 +30,24 @@ int device_cu_count();
 // the C-ABI layer before these are called.
 // ---------------------------------------------------------------------------
 hipError_t launch_quant_dim0(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
-                             uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int mode,
-                             hipStream_t stream);
+                             uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int layout,
+                             int mode, hipStream_t stream);
 
 hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
                              const int32_t* group_ends, int64_t num_groups,
                              int64_t rows_pad_cap, uint8_t* qt, int64_t ldqt, uint8_t* st,
-                             int64_t ldst, int32_t* group_ends_pad, int mode,
+                             int64_t ldst, int layout, int32_t* group_ends_pad, int mode,
                              hipStream_t stream);
+
+hipError_t launch_scales_to_block_major(const uint8_t* src, int64_t batch, int64_t rows,
+                                        int64_t nblk, int64_t sb, int64_t lds, uint8_t* dst,
+                                        int64_t db, int64_t ldd, hipStream_t stream);
 
 struct FwdArgs {
   const uint8_t* a;
-  const uint8_t* as;
+  const uint8_t* as;   // block-major [K/32][ldas]
   const uint8_t* w;
-  const uint8_t* ws;
+  const uint8_t* ws;   // per expert block-major [K/32][ldws]
   const int32_t* group_ends;  // nullptr = one group of M rows
   void* out;
   int64_t lda, ldas, w_gstride, ldw, ws_gstride, ldws, ldo;
@@ -55,9 +59,9 @@ hipError_t launch_grouped_fwd(const FwdArgs& args, hipStream_t stream);
 
 struct WgradArgs {
   const uint8_t* go;   // [N, M] token-contiguous
-  const uint8_t* gos;  // [N, M/32]
+  const uint8_t* gos;  // block-major [M/32][ldgos]
   const uint8_t* ia;   // [K, M]
-  const uint8_t* ias;  // [K, M/32]
+  const uint8_t* ias;  // block-major [M/32][ldias]
   const int32_t* group_ends;
   void* dw;            // [E, N, K]
   int64_t ldgo, ldgos, ldia, ldias;

@@ -23,7 +23,8 @@ template <int MODE, bool SW>
 __global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__ x, int64_t rows,
                                                     int cols8, int64_t ldx,
                                                     uint8_t* __restrict__ q, int64_t ldq,
-                                                    uint8_t* __restrict__ s, int64_t lds) {
+                                                    uint8_t* __restrict__ s, int64_t s_row,
+                                                    int64_t s_blk) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int cc = blockIdx.x * 64 + lane;  // chunk column
@@ -60,7 +61,7 @@ __global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__
       o.y = e4m3_pack4<SW>(f[4], f[5], f[6], f[7]);
       if (col_ok && r < rows) {
         *reinterpret_cast<uint2*>(q + r * ldq + (int64_t)cc * 8) = o;
-        if ((lane & 3) == 0) s[r * lds + (cc >> 2)] = (uint8_t)b;
+        if ((lane & 3) == 0) s[r * s_row + (int64_t)(cc >> 2) * s_blk] = (uint8_t)b;
       }
     }
   }
@@ -122,7 +123,8 @@ template <int MODE, bool SW>
 __global__ __launch_bounds__(256) void k_quant_dim1(
     const uint16_t* __restrict__ x, int64_t rows, int cols, int64_t ldx,
     const int32_t* __restrict__ ends, int E, int64_t rows_pad_cap, uint8_t* __restrict__ qt,
-    int64_t ldqt, uint8_t* __restrict__ st, int64_t ldst, int32_t* __restrict__ ends_pad_out) {
+    int64_t ldqt, uint8_t* __restrict__ st, int64_t st_row, int64_t st_blk,
+    int32_t* __restrict__ ends_pad_out) {
   __shared__ __align__(16) uint16_t tile[64][136];
   __shared__ int32_t ends_s[kMaxGroups];
   __shared__ int32_t pend_s[kMaxGroups];
@@ -205,59 +207,94 @@ __global__ __launch_bounds__(256) void k_quant_dim1(
     uint8_t* dst = qt + (int64_t)(f0 + f) * ldqt + pc;
     reinterpret_cast<uint4*>(dst)[0] = make_uint4(out[0], out[1], out[2], out[3]);
     reinterpret_cast<uint4*>(dst)[1] = make_uint4(out[4], out[5], out[6], out[7]);
-    st[(int64_t)(f0 + f) * ldst + (pc >> 5)] = (uint8_t)b;
+    st[(int64_t)(f0 + f) * st_row + (pc >> 5) * st_blk] = (uint8_t)b;
   }
 }
 
 template <int MODE, bool SW>
 hipError_t dim0_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx, uint8_t* q,
-                     int64_t ldq, uint8_t* s, int64_t lds, hipStream_t stream) {
+                     int64_t ldq, uint8_t* s, int64_t s_row, int64_t s_blk, hipStream_t stream) {
   const int cols8 = (int)(cols / 8);
   dim3 grid((cols8 + 63) / 64, (unsigned)std::min<int64_t>((rows + 15) / 16, 65535));
   hipLaunchKernelGGL((k_quant_dim0<MODE, SW>), grid, dim3(256), 0, stream, x, rows, cols8, ldx, q,
-                     ldq, s, lds);
+                     ldq, s, s_row, s_blk);
   return hipGetLastError();
 }
 
 template <int MODE, bool SW>
 hipError_t dim1_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
                      const int32_t* ends, int64_t E, int64_t cap, uint8_t* qt, int64_t ldqt,
-                     uint8_t* st, int64_t ldst, int32_t* ends_pad, hipStream_t stream) {
+                     uint8_t* st, int64_t st_row, int64_t st_blk, int32_t* ends_pad,
+                     hipStream_t stream) {
   dim3 grid((unsigned)((cap + 127) / 128), (unsigned)((cols + 63) / 64));
   hipLaunchKernelGGL((k_quant_dim1<MODE, SW>), grid, dim3(256), 0, stream, x, rows, (int)cols, ldx,
-                     ends, (int)E, cap, qt, ldqt, st, ldst, ends_pad);
+                     ends, (int)E, cap, qt, ldqt, st, st_row, st_blk, ends_pad);
   return hipGetLastError();
+}
+
+// Row-major [batch][rows][nblk] E8M0 -> block-major [batch][nblk][rows]
+// through a 64x64 LDS tile: coalesced reads along blocks, writes along rows.
+__global__ __launch_bounds__(256) void k_scales_to_block_major(
+    const uint8_t* __restrict__ src, int64_t rows, int64_t nblk, int64_t sb, int64_t lds,
+    uint8_t* __restrict__ dst, int64_t db, int64_t ldd) {
+  __shared__ uint8_t tile[64][65];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, k0 = (int64_t)blockIdx.y * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t r = r0 + i, k = k0 + tx;
+    if (r < rows && k < nblk) tile[i][tx] = src[b * sb + r * lds + k];
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t k = k0 + i, r = r0 + tx;
+    if (r < rows && k < nblk) dst[b * db + k * ldd + r] = tile[tx][i];
+  }
 }
 
 }  // namespace
 
 hipError_t launch_quant_dim0(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
-                             uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int mode,
-                             hipStream_t stream) {
+                             uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int layout,
+                             int mode, hipStream_t stream) {
   if (rows == 0 || cols == 0) return hipSuccess;
   const bool sw = (mode & kCvtSoftwareFlag) != 0;
   const int m = mode & 0xFF;
+  const int64_t s_row = layout == MXGG_SCALES_BLOCK_MAJOR ? 1 : lds;
+  const int64_t s_blk = layout == MXGG_SCALES_BLOCK_MAJOR ? lds : 1;
   if (m == kModeRceil)
-    return sw ? dim0_impl<kModeRceil, true>(x, rows, cols, ldx, q, ldq, s, lds, stream)
-              : dim0_impl<kModeRceil, false>(x, rows, cols, ldx, q, ldq, s, lds, stream);
-  return sw ? dim0_impl<kModeFloor, true>(x, rows, cols, ldx, q, ldq, s, lds, stream)
-            : dim0_impl<kModeFloor, false>(x, rows, cols, ldx, q, ldq, s, lds, stream);
+    return sw ? dim0_impl<kModeRceil, true>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk, stream)
+              : dim0_impl<kModeRceil, false>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk, stream);
+  return sw ? dim0_impl<kModeFloor, true>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk, stream)
+            : dim0_impl<kModeFloor, false>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk, stream);
 }
 
 hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
                              const int32_t* group_ends, int64_t num_groups,
                              int64_t rows_pad_cap, uint8_t* qt, int64_t ldqt, uint8_t* st,
-                             int64_t ldst, int32_t* group_ends_pad, int mode,
+                             int64_t ldst, int layout, int32_t* group_ends_pad, int mode,
                              hipStream_t stream) {
   if (cols == 0 || rows_pad_cap == 0) return hipSuccess;
   const bool sw = (mode & kCvtSoftwareFlag) != 0;
   const int m = mode & 0xFF;
+  const int64_t st_row = layout == MXGG_SCALES_BLOCK_MAJOR ? 1 : ldst;
+  const int64_t st_blk = layout == MXGG_SCALES_BLOCK_MAJOR ? ldst : 1;
 #define MXGG_DIM1(MODE, SWF)                                                                   \
   dim1_impl<MODE, SWF>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, qt, ldqt, st, \
-                       ldst, group_ends_pad, stream)
+                       st_row, st_blk, group_ends_pad, stream)
   if (m == kModeRceil) return sw ? MXGG_DIM1(kModeRceil, true) : MXGG_DIM1(kModeRceil, false);
   return sw ? MXGG_DIM1(kModeFloor, true) : MXGG_DIM1(kModeFloor, false);
 #undef MXGG_DIM1
+}
+
+hipError_t launch_scales_to_block_major(const uint8_t* src, int64_t batch, int64_t rows,
+                                        int64_t nblk, int64_t sb, int64_t lds, uint8_t* dst,
+                                        int64_t db, int64_t ldd, hipStream_t stream) {
+  if (batch == 0 || rows == 0 || nblk == 0) return hipSuccess;
+  dim3 grid((unsigned)((rows + 63) / 64), (unsigned)((nblk + 63) / 64), (unsigned)batch);
+  hipLaunchKernelGGL(k_scales_to_block_major, grid, dim3(256), 0, stream, src, rows, nblk, sb, lds,
+                     dst, db, ldd);
+  return hipGetLastError();
 }
 
 }  // namespace mxgg

@@ -28,7 +28,10 @@ CVT_SOFTWARE = 0x100  # verification-only: bit-level e4m3 encoder instead of v_c
 OUT_BF16 = 0
 OUT_F32 = 1
 
-ABI_VERSION = 1
+SCALES_ROW_MAJOR = 0
+SCALES_BLOCK_MAJOR = 1
+
+ABI_VERSION = 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -39,10 +42,13 @@ SIGNATURES = {
     "mxgg_abi_version": (_I, []),
     "mxgg_status_string": (ctypes.c_char_p, [_I]),
     "mxgg_last_error": (ctypes.c_char_p, []),
-    "mxgg_quant_dim0": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I, _P]),
+    "mxgg_quant_dim0": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _I, _I, _P]),
     "mxgg_quant_dim1": (
         _I,
-        [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I, _P],
+        [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I, _P, _I, _P],
+    ),
+    "mxgg_scales_to_block_major": (
+        _I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P],
     ),
     "mxgg_grouped_fwd": (
         _I,

@@ -89,6 +89,64 @@ def _group_ends(offs: torch.Tensor, num_groups: int, device) -> torch.Tensor:
     return offs.contiguous()
 
 
+def _ld16(n: int) -> int:
+    return max(16, (n + 15) // 16 * 16)
+
+
+def _block_major_buffer(rows: int, nblk: int, device) -> torch.Tensor:
+    """Storage for E8M0 scales laid out block-major: [nblk][round_up(rows, 16)]."""
+    return torch.empty((nblk, _ld16(rows)), dtype=torch.uint8, device=device)
+
+
+def _readable(t: torch.Tensor) -> int:
+    """Bytes of storage from t's first element to the end of its storage."""
+    return t.untyped_storage().nbytes() - t.storage_offset() * t.element_size()
+
+
+def _scales_2d(s: torch.Tensor, rows: int, nblk: int, name: str):
+    """Logical [rows, nblk] E8M0 scales -> (tensor, block-major stride) for the
+    GEMM kernels.  A block-major view (stride (1, ld), e.g. what this library's
+    casts return) is used in place; anything else is re-laid on the device."""
+    s = _as_u8(s, name)
+    _need_gpu(s, name)
+    if tuple(s.shape) != (rows, nblk):
+        raise ValueError(f"{name} shape {tuple(s.shape)} != {(rows, nblk)}")
+    if (s.stride(0) == 1 or rows == 1) and s.stride(1) >= rows and s.stride(1) % 4 == 0 \
+            and s.data_ptr() % 4 == 0 and nblk > 0 \
+            and _readable(s) >= (nblk - 1) * s.stride(1) + (rows + 3) // 4 * 4:
+        return s, s.stride(1)
+    src = s.contiguous()
+    dst = _block_major_buffer(rows, nblk, s.device)
+    lib = _lib.load()
+    _lib.check(lib.mxgg_scales_to_block_major(src.data_ptr(), 1, rows, nblk, 0, nblk,
+                                              dst.data_ptr(), 0, dst.stride(0),
+                                              _stream_ptr(s)), "scales_to_block_major")
+    return dst, dst.stride(0)
+
+
+def _scales_3d(s: torch.Tensor, E: int, rows: int, nblk: int, name: str):
+    """Logical [E, rows, nblk] scales -> (tensor, expert stride, block stride),
+    block-major within each expert (the expert stride may interleave experts
+    inside a block-row, as the cast of a flattened [E*rows, K] tensor does)."""
+    s = _as_u8(s, name)
+    _need_gpu(s, name)
+    if tuple(s.shape) != (E, rows, nblk):
+        raise ValueError(f"{name} shape {tuple(s.shape)} != {(E, rows, nblk)}")
+    st = s.stride()
+    if (st[1] == 1 or rows == 1) and st[2] % 4 == 0 and (E == 1 or st[0] % 4 == 0) \
+            and s.data_ptr() % 4 == 0 and st[2] >= rows and (E == 1 or st[0] >= rows) \
+            and _readable(s) >= (E - 1) * st[0] + (nblk - 1) * st[2] + (rows + 3) // 4 * 4:
+        return s, st[0], st[2]
+    src = s.contiguous()
+    ld = _ld16(rows)
+    dst = torch.empty((E, nblk, ld), dtype=torch.uint8, device=s.device)
+    lib = _lib.load()
+    _lib.check(lib.mxgg_scales_to_block_major(src.data_ptr(), E, rows, nblk, rows * nblk, nblk,
+                                              dst.data_ptr(), nblk * ld, ld, _stream_ptr(s)),
+               "scales_to_block_major")
+    return dst, nblk * ld, ld
+
+
 def _out_code(dtype: torch.dtype) -> int:
     if dtype == torch.bfloat16:
         return _lib.OUT_BF16
@@ -104,7 +162,9 @@ def to_mxfp8_dim0(x: torch.Tensor, scaling_mode="rceil"):
     """Row-wise MXFP8: 1x32 blocks along the last dimension.
 
     x: bf16 [..., K] (K % 32 == 0).  Returns (q float8_e4m3fn [..., K],
-    scales uint8 [..., K/32]) with E8M0 bytes (2^(b-127)).
+    scales uint8 [..., K/32]) with E8M0 bytes (2^(b-127)).  The scales are a
+    view of block-major storage ([K/32][rows], what the GEMM kernels read);
+    .contiguous() gives the row-major copy.
     """
     _need_gpu(x, "x")
     if x.dtype != torch.bfloat16:
@@ -115,15 +175,24 @@ def to_mxfp8_dim0(x: torch.Tensor, scaling_mode="rceil"):
     if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
         x2 = x2.contiguous()
     rows = x2.shape[0]
+    nblk = K // 32
     q = torch.empty((rows, K), dtype=_FP8, device=x.device)
-    s = torch.empty((rows, K // 32), dtype=torch.uint8, device=x.device)
+    buf = _block_major_buffer(rows, nblk, x.device)
     lib = _lib.load()
     _lib.check(
         lib.mxgg_quant_dim0(x2.data_ptr(), rows, K, x2.stride(0), q.data_ptr(), q.stride(0),
-                            s.data_ptr(), s.stride(0), _mode(scaling_mode), _stream_ptr(x)),
+                            buf.data_ptr(), buf.stride(0), _lib.SCALES_BLOCK_MAJOR,
+                            _mode(scaling_mode), _stream_ptr(x)),
         "quant_dim0",
     )
-    return q.reshape(shape), s.reshape(*shape[:-1], K // 32)
+    lead = tuple(shape[:-1])
+    lead_strides = []
+    acc = 1
+    for d in reversed(lead):
+        lead_strides.append(acc)
+        acc *= d
+    s = buf.as_strided(lead + (nblk,), tuple(reversed(lead_strides)) + (buf.stride(0),))
+    return q.reshape(shape), s
 
 
 def padded_token_capacity(num_tokens: int, num_groups: int | None) -> int:
@@ -140,7 +209,8 @@ def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mod
     each group is zero-padded to a multiple of 32 tokens.
     Returns (qt float8_e4m3fn [C, M_pad], st uint8 [C, M_pad/32], offs_pad)
     where offs_pad are the padded cumulative ends (int32 [E], None without
-    offs) and M_pad = padded_token_capacity(M, E) >= offs_pad[-1].
+    offs) and M_pad = padded_token_capacity(M, E) >= offs_pad[-1].  st is a
+    view of block-major storage ([M_pad/32][C]).
     """
     _need_gpu(x, "x")
     if x.dtype != torch.bfloat16 or x.dim() != 2:
@@ -156,18 +226,20 @@ def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mod
         ends_pad = torch.empty(E, dtype=torch.int32, device=x.device)
     cap = padded_token_capacity(M, E)
     qt = torch.empty((C, cap), dtype=_FP8, device=x.device)
-    st = torch.empty((C, cap // 32), dtype=torch.uint8, device=x.device)
+    buf = _block_major_buffer(C, cap // 32, x.device)
     lib = _lib.load()
     _lib.check(
         lib.mxgg_quant_dim1(
             x2.data_ptr(), M, C, x2.stride(0),
             ends.data_ptr() if ends is not None else None, E or 0, cap,
-            qt.data_ptr(), qt.stride(0), st.data_ptr(), st.stride(0),
+            qt.data_ptr(), qt.stride(0), buf.data_ptr(), buf.stride(0),
+            _lib.SCALES_BLOCK_MAJOR,
             ends_pad.data_ptr() if ends_pad is not None else None,
             _mode(scaling_mode), _stream_ptr(x),
         ),
         "quant_dim1",
     )
+    st = buf[:, :C].t()  # logical [C, cap/32], block-major storage
     return qt, st, ends_pad
 
 
@@ -196,15 +268,10 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
     if (a_scales is None) != (w_scales is None):
         raise ValueError("a_scales and w_scales must both be given or both be None")
     sa = sw = None
+    ldas = ldws = wsg = 0
     if a_scales is not None:
-        sa = _as_u8(_rowmajor(a_scales), "a_scales")
-        sw = _as_u8(_rowmajor(w_scales), "w_scales")
-        if tuple(sa.shape) != (M, K // 32):
-            raise ValueError(f"a_scales shape {tuple(sa.shape)} != {(M, K // 32)}")
-        if tuple(sw.shape) != (E, N, K // 32):
-            raise ValueError(f"w_scales shape {tuple(sw.shape)} != {(E, N, K // 32)}")
-        _need_gpu(sa, "a_scales")
-        _need_gpu(sw, "w_scales")
+        sa, ldas = _scales_2d(a_scales, M, K // 32, "a_scales")
+        sw, wsg, ldws = _scales_3d(w_scales, E, N, K // 32, "w_scales")
     ends = None
     if offs is not None:
         ends = _group_ends(offs, E, a.device)
@@ -218,10 +285,9 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
     _lib.check(
         lib.mxgg_grouped_fwd(
             a8.data_ptr(), a8.stride(0),
-            sa.data_ptr() if sa is not None else None, sa.stride(0) if sa is not None else 0,
+            sa.data_ptr() if sa is not None else None, ldas,
             w8.data_ptr(), w8.stride(0), w8.stride(1),
-            sw.data_ptr() if sw is not None else None,
-            sw.stride(0) if sw is not None else 0, sw.stride(1) if sw is not None else 0,
+            sw.data_ptr() if sw is not None else None, wsg, ldws,
             ends.data_ptr() if ends is not None else None, E,
             M, N, K, out.data_ptr(), out.stride(0), _out_code(out_dtype), _stream_ptr(a),
         ),
@@ -294,12 +360,10 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
     if (go_scales is None) != (ia_scales is None):
         raise ValueError("go_scales and ia_scales must both be given or both be None")
     sg = si = None
+    ldgs = ldis = 0
     if go_scales is not None:
-        sg = _as_u8(_rowmajor(go_scales), "go_scales")
-        si = _as_u8(_rowmajor(ia_scales), "ia_scales")
-        if tuple(sg.shape) != (N, M // 32) or tuple(si.shape) != (K, M // 32):
-            raise ValueError(
-                f"scale shapes {tuple(sg.shape)}, {tuple(si.shape)} != {(N, M // 32)}, {(K, M // 32)}")
+        sg, ldgs = _scales_2d(go_scales, N, M // 32, "go_scales")
+        si, ldis = _scales_2d(ia_scales, K, M // 32, "ia_scales")
     E = offs.numel()
     ends = _group_ends(offs, E, go.device)
     if out is None:
@@ -310,9 +374,9 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
     _lib.check(
         lib.mxgg_grouped_wgrad(
             g8.data_ptr(), g8.stride(0),
-            sg.data_ptr() if sg is not None else None, sg.stride(0) if sg is not None else 0,
+            sg.data_ptr() if sg is not None else None, ldgs,
             i8.data_ptr(), i8.stride(0),
-            si.data_ptr() if si is not None else None, si.stride(0) if si is not None else 0,
+            si.data_ptr() if si is not None else None, ldis,
             ends.data_ptr(), E, M, N, K, out.data_ptr(), _out_code(out_dtype), _stream_ptr(go),
         ),
         "grouped_wgrad",

@@ -71,6 +71,10 @@ def _fwd(lib, **kw):
     (dict(ends=FAKE, E=0), _lib.ERR_UNSUPPORTED),
     (dict(ends=FAKE, E=2000), _lib.ERR_UNSUPPORTED),
     (dict(ends=FAKE, E=4, wg=100), _lib.ERR_SHAPE),    # expert stride too small
+    (dict(a_s=FAKE, ldas=32, w_s=FAKE, ldws=512, wsg=512 * 8), _lib.ERR_SHAPE),  # ldas < M
+    (dict(a_s=FAKE, ldas=66, w_s=FAKE, ldws=512, wsg=512 * 8), _lib.ERR_ALIGNMENT),
+    (dict(a_s=FAKE + 2, ldas=64, w_s=FAKE, ldws=512, wsg=512 * 8), _lib.ERR_ALIGNMENT),
+    (dict(a_s=FAKE, ldas=64, w_s=FAKE, ldws=512, wsg=100, ends=FAKE, E=4), _lib.ERR_SHAPE),
 ])
 def test_grouped_fwd_rejects(lib, kw, status):
     assert _fwd(lib, **kw) == status
@@ -100,24 +104,47 @@ def _wg(lib, **kw):
     (dict(go=FAKE + 4), _lib.ERR_ALIGNMENT),
     (dict(K=66), _lib.ERR_ALIGNMENT),
     (dict(dt=3), _lib.ERR_INVALID_ARGUMENT),
+    (dict(gs=FAKE, ldgs=32, is_=FAKE, ldis=64), _lib.ERR_SHAPE),     # ldgos < N
+    (dict(gs=FAKE, ldgs=66, is_=FAKE, ldis=64), _lib.ERR_ALIGNMENT),
 ])
 def test_grouped_wgrad_rejects(lib, kw, status):
     assert _wg(lib, **kw) == status
 
 
+RM, BM = _lib.SCALES_ROW_MAJOR, _lib.SCALES_BLOCK_MAJOR
+
+
 @pytest.mark.parametrize("args,status", [
-    ((FAKE, 4, 100, 100, FAKE, 100, FAKE, 4, 0, None), _lib.ERR_SHAPE),      # cols % 32
-    ((FAKE, 4, 64, 64, FAKE, 64, FAKE, 2, 5, None), _lib.ERR_INVALID_ARGUMENT),  # mode
-    ((None, 4, 64, 64, FAKE, 64, FAKE, 2, 0, None), _lib.ERR_INVALID_ARGUMENT),
-    ((FAKE + 2, 4, 64, 64, FAKE, 64, FAKE, 2, 0, None), _lib.ERR_ALIGNMENT),
-    ((FAKE, 4, 64, 32, FAKE, 64, FAKE, 2, 0, None), _lib.ERR_SHAPE),       # ldx < cols
+    ((FAKE, 4, 100, 100, FAKE, 100, FAKE, 4, RM, 0, None), _lib.ERR_SHAPE),      # cols % 32
+    ((FAKE, 4, 64, 64, FAKE, 64, FAKE, 2, RM, 5, None), _lib.ERR_INVALID_ARGUMENT),  # mode
+    ((FAKE, 4, 64, 64, FAKE, 64, FAKE, 2, 7, 0, None), _lib.ERR_INVALID_ARGUMENT),  # layout
+    ((None, 4, 64, 64, FAKE, 64, FAKE, 2, RM, 0, None), _lib.ERR_INVALID_ARGUMENT),
+    ((FAKE + 2, 4, 64, 64, FAKE, 64, FAKE, 2, RM, 0, None), _lib.ERR_ALIGNMENT),
+    ((FAKE, 4, 64, 32, FAKE, 64, FAKE, 2, RM, 0, None), _lib.ERR_SHAPE),       # ldx < cols
+    ((FAKE, 40, 64, 64, FAKE, 64, FAKE, 32, BM, 0, None), _lib.ERR_SHAPE),     # block ld < rows
 ])
 def test_quant_dim0_rejects(lib, args, status):
     assert lib.mxgg_quant_dim0(*args) == status
 
 
 def test_quant_dim0_empty_is_noop(lib):
-    assert lib.mxgg_quant_dim0(None, 0, 64, 64, None, 64, None, 2, 0, None) == _lib.OK
+    assert lib.mxgg_quant_dim0(None, 0, 64, 64, None, 64, None, 2, RM, 0, None) == _lib.OK
+
+
+@pytest.mark.parametrize("args,status", [
+    ((FAKE, 1, -1, 4, 0, 4, FAKE, 0, 16), _lib.ERR_SHAPE),
+    ((None, 1, 8, 4, 0, 4, FAKE, 0, 16), _lib.ERR_INVALID_ARGUMENT),
+    ((FAKE, 1, 8, 4, 0, 2, FAKE, 0, 16), _lib.ERR_SHAPE),           # lds < nblk
+    ((FAKE, 1, 20, 4, 0, 4, FAKE, 0, 16), _lib.ERR_SHAPE),          # ldd < rows
+    ((FAKE, 2, 8, 4, 16, 4, FAKE, 64, 16), _lib.ERR_SHAPE),         # src batch stride
+    ((FAKE, 70000, 8, 4, 32, 4, FAKE, 64, 16), _lib.ERR_UNSUPPORTED),
+])
+def test_scales_to_block_major_rejects(lib, args, status):
+    assert lib.mxgg_scales_to_block_major(*args, None) == status
+
+
+def test_scales_to_block_major_empty_is_noop(lib):
+    assert lib.mxgg_scales_to_block_major(None, 0, 8, 4, 0, 4, None, 0, 16, None) == _lib.OK
 
 
 @pytest.mark.parametrize("kw,status", [
@@ -128,14 +155,16 @@ def test_quant_dim0_empty_is_noop(lib):
     (dict(pad=None), _lib.ERR_INVALID_ARGUMENT),
     (dict(mode=9), _lib.ERR_INVALID_ARGUMENT),
     (dict(x=FAKE + 2), _lib.ERR_ALIGNMENT),
+    (dict(layout=3), _lib.ERR_INVALID_ARGUMENT),
+    (dict(layout=BM, ldst=32), _lib.ERR_SHAPE),        # block ld < cols
 ])
 def test_quant_dim1_rejects(lib, kw, status):
     a = dict(x=FAKE, rows=64, cols=64, ldx=64, ends=FAKE, E=2, cap=128, qt=FAKE, ldqt=128,
-             st=FAKE, ldst=4, pad=FAKE, mode=0)
+             st=FAKE, ldst=4, layout=RM, pad=FAKE, mode=0)
     a.update(kw)
     assert lib.mxgg_quant_dim1(a["x"], a["rows"], a["cols"], a["ldx"], a["ends"], a["E"],
-                               a["cap"], a["qt"], a["ldqt"], a["st"], a["ldst"], a["pad"],
-                               a["mode"], None) == status
+                               a["cap"], a["qt"], a["ldqt"], a["st"], a["ldst"], a["layout"],
+                               a["pad"], a["mode"], None) == status
 
 
 def test_python_maps_errors_to_exceptions(lib):

@@ -123,6 +123,7 @@ def _rand_q(shape, gpu, seed, scale_lo=118, scale_hi=136):
     ([513], 256, 128),                      # one group, M tail
     ([256, 256, 256], 256, 1024),           # aligned, several K stages
     ([7, 0, 0], 96, 32),                    # tiny
+    ([3, 5, 9, 250], 320, 192),             # group starts not multiples of 4, odd stage count
 ])
 @pytest.mark.parametrize("scaled", [True, False])
 def test_grouped_fwd_random_codes(gpu, sizes, N, K, scaled):
@@ -136,6 +137,39 @@ def test_grouped_fwd_random_codes(gpu, sizes, N, K, scaled):
     ref = O.grouped_fwd(u8(a_q), u8(a_s) if scaled else None, u8(w_q),
                         u8(w_s) if scaled else None, ends)
     assert_close_to_oracle(y, ref)
+
+
+def test_scale_layouts_give_identical_results(gpu):
+    # block-major views (the cast's own output), row-major copies (re-laid by
+    # the converter kernel) and per-expert block-major buffers built by hand
+    x, w, sizes = workloads.c1(gpu)
+    xq, xs = mxfp8gg.to_mxfp8_dim0(x)
+    wq, ws = mxfp8gg.to_mxfp8_dim0(w)
+    ends = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    y_view = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.float32)
+    y_rm = ops.grouped_mm(xq, wq, ends, xs.contiguous(), ws.contiguous(), out_dtype=torch.float32)
+    ws_sep = torch.empty((4, 8, 528), dtype=torch.uint8, device=gpu)
+    ws_sep[:, :, :512] = ws.contiguous().transpose(1, 2)
+    y_sep = ops.grouped_mm(xq, wq, ends, xs, ws_sep[:, :, :512].transpose(1, 2),
+                           out_dtype=torch.float32)
+    assert torch.equal(y_view, y_rm) and torch.equal(y_view, y_sep)
+
+
+@pytest.mark.parametrize("batch,rows,nblk", [(1, 300, 7), (3, 64, 224), (2, 1, 1), (1, 4096, 2)])
+def test_scales_to_block_major_kernel(gpu, batch, rows, nblk):
+    from mxfp8gg import _lib
+
+    g = torch.Generator(device=gpu).manual_seed(71)
+    src = torch.randint(0, 256, (batch, rows, nblk), generator=g, device=gpu,
+                        dtype=torch.int32).to(torch.uint8)
+    ld = (rows + 15) // 16 * 16
+    dst = torch.zeros((batch, nblk, ld), dtype=torch.uint8, device=gpu)
+    lib = _lib.load()
+    _lib.check(lib.mxgg_scales_to_block_major(src.data_ptr(), batch, rows, nblk, rows * nblk,
+                                              nblk, dst.data_ptr(), nblk * ld, ld,
+                                              torch.cuda.current_stream().cuda_stream), "t")
+    assert torch.equal(dst[:, :, :rows], src.transpose(1, 2))
+    assert torch.all(dst[:, :, rows:] == 0)
 
 
 def test_c1_end_to_end_quant_then_gemm(gpu):

@@ -45,6 +45,23 @@ def test_dim0_random_wide_dynamic_range(gpu, name, mode):
     assert np.array_equal(u8(s), rs) and np.array_equal(u8(q), rq)
 
 
+@pytest.mark.parametrize("name,mode", MODES)
+def test_dim0_row_major_scale_layout(gpu, name, mode):
+    # the C ABI's ROW_MAJOR scale output (the reference's [M, K//32] layout)
+    g = torch.Generator(device=gpu).manual_seed(17)
+    x = (torch.randn(96, 512, generator=g, device=gpu) * 7).to(torch.bfloat16)
+    q = torch.empty((96, 512), dtype=torch.float8_e4m3fn, device=gpu)
+    s = torch.empty((96, 16), dtype=torch.uint8, device=gpu)
+    lib = _lib.load()
+    _lib.check(lib.mxgg_quant_dim0(x.data_ptr(), 96, 512, 512, q.data_ptr(), 512, s.data_ptr(), 16,
+                                   _lib.SCALES_ROW_MAJOR, mode,
+                                   torch.cuda.current_stream().cuda_stream), "dim0")
+    rq, rs = O.quant_dim0(bits(x), mode)
+    assert np.array_equal(u8(q), rq) and np.array_equal(u8(s), rs)
+    q2, s2 = ops.to_mxfp8_dim0(x, mode)
+    assert s2.stride() == (1, 96) and torch.equal(s2.contiguous(), s)
+
+
 def test_dim0_strided_rows_and_3d(gpu):
     g = torch.Generator(device=gpu).manual_seed(13)
     base = torch.randn(64, 384, generator=g, device=gpu).to(torch.bfloat16)
