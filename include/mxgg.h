@@ -141,6 +141,9 @@ int mxgg_scales_to_block_major(const void* src, int64_t batch, int64_t rows, int
  *   out      : [M, N] bf16 or f32 (out_dtype), row stride ldo
  * a_scales and w_scales are both given or both NULL (NULL = every scale 1.0,
  * E8M0 byte 0x7F).  K % 32 == 0.  Rows past the last group end are untouched.
+ * a and w are 16-byte aligned, lda and ldw multiples of 16 and at most 2^23,
+ * each operand spans less than 2 GiB; strides that are multiples of 128 let
+ * every load fetch whole cache lines (the fast case).
  * Replaces fused_grouped_fwd (fused_fwd.py:172-229) + its kernel
  * (fused_fwd.py:18-167), and fwd_ge (fwd_final.py:121-131) with num_groups=1.
  */
@@ -167,6 +170,9 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
  *                 two groups
  *   dw          : [num_groups, N, K] bf16 or f32, contiguous; empty groups are
  *                 written with zeros
+ * go_t and ia_t are 16-byte aligned, ldgo and ldia multiples of 16 and at most
+ * 2^23, each operand spans less than 2 GiB; strides that are multiples of 128
+ * let every load fetch whole cache lines (the fast case).
  * Replaces wgrad_fused / wgrad_prepare + wgrad_kernel (wgrad_fused.py:34-112),
  * which restack operands per group and call the forward kernel.
  */

@@ -17,6 +17,9 @@ thread_local char g_last_error[512] = "";
 
 constexpr int64_t kMaxGroupsAbi = 1024;
 constexpr int64_t kMaxBufferBytes = 0x7FFFFFF0LL;  // one buffer resource per operand
+// GEMM tiles run up to 255 rows past an operand's last row; those offsets must
+// stay below 2^32 (they read as zero through the buffer range check).
+constexpr int64_t kMaxRowStride = INT64_C(1) << 23;
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 }  // namespace
@@ -228,6 +231,8 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
                      "grouped_fwd: out must be aligned to 4 elements with ldo % 4 == 0");
   if ((M - 1) * lda + K > kMaxBufferBytes || (N - 1) * ldw + K > kMaxBufferBytes)
     return set_error(MXGG_ERR_UNSUPPORTED, "grouped_fwd: operand larger than 2 GiB");
+  if (lda > kMaxRowStride || ldw > kMaxRowStride)
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_fwd: row stride above 8 MiB");
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return set_error(MXGG_ERR_UNSUPPORTED, "grouped_fwd: dimension above 2^31");
   FwdArgs args;
@@ -297,6 +302,8 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
     return set_error(MXGG_ERR_ALIGNMENT, "grouped_wgrad: dw must be vector aligned, K % 4 == 0");
   if ((N - 1) * ldgo + M > kMaxBufferBytes || (K - 1) * ldia + M > kMaxBufferBytes)
     return set_error(MXGG_ERR_UNSUPPORTED, "grouped_wgrad: operand larger than 2 GiB");
+  if (ldgo > kMaxRowStride || ldia > kMaxRowStride)
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_wgrad: row stride above 8 MiB");
   if (M > INT32_MAX || N > INT32_MAX || K > INT32_MAX)
     return set_error(MXGG_ERR_UNSUPPORTED, "grouped_wgrad: dimension above 2^31");
   WgradArgs args;

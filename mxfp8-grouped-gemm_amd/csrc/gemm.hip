@@ -4,23 +4,31 @@
 //   D[p][q] = sum_k P[p][k] * 2^(sP[k/32][p]-127) * Q[q][k] * 2^(sQ[k/32][q]-127)
 // where P and Q are row-major e4m3 operands contiguous along the contraction
 // dimension k and the E8M0 scales are stored block-major (one row of bytes per
-// 32-deep k-block, indexed by operand row).  P feeds the MFMA "A" source (its
-// index lands on the 4 consecutive accumulator rows each lane holds), Q feeds
-// the "B" source (one index per lane), so the output's contiguous dimension is
-// the P index.
+// 32-deep k-block, indexed by operand row).  P feeds the MFMA "A" source and Q
+// the "B" source; each lane ends up holding runs of 4 consecutive P indices
+// (one from each of its 4 MFMA blocks along P) for one Q index, so the
+// output's contiguous dimension is the P index.
 //
 //   forward : P = W[g] (rows n), Q = X (rows m of group g), k = hidden  -> Y[m][n]
 //   wgrad   : P = X^T  (rows k), Q = dY^T (rows n),  k = tokens of g    -> dW[g][n][k]
 //
 // Tile 256(P) x 256(Q), 256 threads = 4 waves in a 2x2 arrangement, each wave
 // 128x128 = 4x4 MFMA 32x32 blocks (256 fp32 accumulators per lane in AGPRs).
-// The contraction streams through a ring of 4 LDS stages of 64 (two k-blocks):
-// each stage holds P and Q (256 rows x 64 B each, 16-byte chunks XOR-swizzled
-// per row) and their 4 scale rows, all written by LDS-DMA
-// (buffer_load ... lds) three stages ahead of the compute.  Each stage's MFMA
-// sequence is split around the barrier that publishes the next stage: the
-// last 8 MFMAs of stage s run while the waves synchronise and read stage s+1's
-// operands, so the matrix pipe does not drain at stage boundaries.
+// MFMA block i of a wave's 128 rows takes every 4th row (rows 4m+i), so the
+// four scale bytes a lane needs for one k-block are adjacent in the
+// block-major scale row and arrive with one 32-bit LDS read.
+//
+// The contraction streams through two LDS stages of 128 (four k-blocks, two
+// MFMA k-steps).  A stage holds P and Q (256 rows x 128 B each: every row is
+// one whole 128-byte cache line of the operand, 16-byte chunks XOR-swizzled)
+// and their 8 scale rows, all written by LDS-DMA (buffer_load ... lds).
+// Reading whole lines matters: with 64-byte stages every line crossed the
+// L2 -> L1 path twice and the L2 request rate, not the MFMA pipe, set the
+// speed.  Stage s+2 is requested right after the barrier that publishes
+// stage s+1 (which also retires all reads of stage s, whose slot it reuses), so
+// every load has a whole stage of compute to land.  The MFMA sequence is split
+// around that barrier: the last 8 MFMAs of stage s run while the waves
+// synchronise, issue the loads and read stage s+1's first operands.
 // Persistent grid (one workgroup per CU), tiles dealt round-robin with each XCD
 // taking a contiguous slice of every round.
 #include <algorithm>
@@ -32,21 +40,19 @@ namespace {
 
 constexpr int kTileP = 256;
 constexpr int kTileQ = 256;
-constexpr int kStageK = 64;     // contraction elements (bytes) per stage
-constexpr int kStages = 4;      // LDS ring depth
-constexpr int kAhead = 3;       // stages in flight ahead of the compute
+constexpr int kStageK = 128;    // contraction elements (bytes) per stage
 constexpr int kThreads = 256;
 constexpr int kMaxGroups = 1024;
-constexpr uint32_t kOpBytes = 256u * kStageK;          // one operand of one stage: 16 KB
+constexpr uint32_t kOpBytes = 256u * kStageK;          // one operand of one stage: 32 KB
 constexpr uint32_t kScaleOff = 2u * kOpBytes;          // scale rows after P and Q data
-constexpr uint32_t kStageBytes = 2u * kOpBytes + 1024u;  // + [2 operands][2 blocks][256]
-// DMA instructions per wave per stage: 4 P + 4 Q (+ 1 scale when scaled)
+constexpr uint32_t kStageBytes = kScaleOff + 4u * 512u;  // + [4 blocks][P, Q][256]
+// DMA instructions per wave per stage: 8 P + 8 Q (+ 1 P-scale + 1 Q-scale)
 template <bool SCALED>
-constexpr uint32_t dma_per_stage() { return SCALED ? 9u : 8u; }
+constexpr uint32_t dma_per_stage() { return SCALED ? 18u : 16u; }
 constexpr uint32_t kOobOffset = 0x80000000u;           // beyond every num_records we create
 
 struct __align__(16) Smem {
-  uint8_t ring[kStages][kStageBytes];
+  uint8_t ring[2][kStageBytes];
   int32_t sched[kMaxGroups + 1];
   int32_t order[kMaxGroups];
   int32_t scan_tmp[kThreads];
@@ -72,13 +78,16 @@ __device__ __forceinline__ uint32_t scale_extent(int64_t nblk, int64_t ld, int64
   return (uint32_t)((nblk - 1) * ld + ((rows + 3) & ~(int64_t)3));
 }
 
+// One operand of a tile.  Rows at or past `rows` are not clamped: their byte
+// offsets lie beyond the descriptor's num_records ((rows-1)*ld + K) and read
+// as zero.  The C ABI bounds (rows + 256) * ld below 2^32 so these offsets do
+// not wrap.
 struct Operand {
   desc_t data;    // [rows][ld] e4m3
   desc_t scale;   // [k-blocks][lds] E8M0, block-major
   uint32_t ld;    // bytes per data row
   uint32_t lds;   // bytes per scale block-row (multiple of 4)
   uint32_t row0;  // first operand row of this tile (multiple of 4)
-  uint32_t rows;  // rows that exist (data loads clamp to rows-1)
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -92,33 +101,34 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(uintptr_t)((const lds_void_t*)p);
 }
 
-// 16-byte chunk swizzle inside a 64-byte LDS row.  For 8 consecutive rows the
-// (row parity, chunk) pairs are distinct (conflict-free 8-lane service of a
-// 32-bank LDS) and for 16 consecutive rows the (row mod 4, chunk) pairs are
-// distinct (16-lane service of a 64-bank LDS).
-__device__ __forceinline__ uint32_t swz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3u; }
+// 16-byte chunk swizzle inside a 128-byte LDS slot.  gfx950 serves a
+// ds_read_b128 one half-wave (32 lanes, 512 B) at a time over 64 four-byte
+// banks; it runs at full rate when every bank holds at most two of the
+// half-wave's dwords.  A half-wave reads one chunk from each of 32 consecutive
+// slots; the bank quad of (slot s, chunk c) is 8*(s mod 2) + (c ^ swz(s)), and
+// with swz(s) = (s/2) mod 8 the 16 quads are each hit exactly twice.
+__device__ __forceinline__ uint32_t swz(uint32_t s) { return (s >> 1) & 7u; }
 
-// Publish a stage: this wave's DMA older than the 2 youngest stages (18
-// instructions scaled, 16 unscaled) has landed and all of its LDS reads have
-// returned, then the workgroup barrier.  Written as assembly so the
+// Tile row held by LDS slot s: slots [128w + 32i, +32) hold rows 128w + 4m + i
+// (m = 0..31), the rows of MFMA block i of wave row-half w.
+__device__ __forceinline__ uint32_t slot_row(uint32_t s) {
+  return (s & 128u) | ((s & 31u) << 2) | ((s >> 5) & 3u);
+}
+
+// Wait for this wave's DMA except the youngest `N` instructions and for all
+// of its LDS reads, then the workgroup barrier.  Written as assembly so the
 // compiler's waitcnt pass can neither relax nor move it (it does not see the
 // DMA, and would drop the lgkmcnt part for reads whose results are only used
 // after the barrier).
-template <bool SCALED>
-__device__ __forceinline__ void publish_barrier() {
-  static_assert((kAhead - 1) * dma_per_stage<SCALED>() == (SCALED ? 18u : 16u),
-                "wait counts below are written out for 2 stages in flight");
-  if (SCALED)
-    asm volatile("s_waitcnt vmcnt(18) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+template <int N>
+__device__ __forceinline__ void wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
-
 
 // LDS-DMA issued from inline assembly: M0 holds the wave's LDS destination,
 // each lane its byte offset into the buffer.  The compiler does not track
-// these loads, so it inserts no wait for them in front of LDS reads of other
-// stages; every consumer waits explicitly in publish_barrier().
+// these loads, so it inserts no wait for them in front of LDS reads of the
+// other stage; every consumer waits explicitly in wait_barrier().
 // M0 is reserved by the compiler, which warns about the clobber; on gfx950 it
 // only uses M0 for LDS-DMA, GWS and message instructions, none of which it
 // emits in these kernels (the generated code writes M0 only here).
@@ -143,89 +153,123 @@ __device__ __forceinline__ void dma_x1(const desc_t& d, uint32_t lds_addr, uint3
 #pragma clang diagnostic pop
 
 // Per-thread state of the global -> LDS stream for one tile.
-//  Data: wave w's i-th load (i = 0..3) fills LDS bytes [(4i+w)*1024, +1024) of
-//  an operand, lane l writing 16 B at +16*l: LDS row r = (4i+w)*16 + l/4 at
-//  physical chunk l%4, so the lane fetches logical chunk (l%4) ^ swz(r) of
-//  operand row r.  swz(r) does not depend on i, so one chunk column serves all
-//  four loads.  Chunks at or past kend are fetched from an out-of-range offset
-//  and land as zeros.
-//  Scales: wave w copies block (w&1) of operand (w>>1): 256 rows = 64 lanes x
-//  4 bytes, from block-row kb + (w&1).  A block at or past kend lands as zeros
-//  (scale 2^-127 on zero payload).
+//  Data: wave w's i-th load (i = 0..7) fills LDS bytes [4096i + 1024w, +1024)
+//  of an operand, lane l writing 16 B at +16l: slot s = 32i + 8w + l/8 at
+//  physical chunk l%8, so the lane fetches logical chunk (l%8) ^ swz(s) of
+//  tile row slot_row(s) = 128(i/4) + 4(8w + l/8) + i%4.  Eight lanes cover one
+//  128-byte line.  swz(s) = (4w + l/16) mod 8 does not depend on i, and the
+//  row moves by a lane-independent amount from load to load, so the lane keeps
+//  one base offset per operand and adds a uniform step.  Chunks outside
+//  [klo, kend) are fetched from an out-of-range offset and land as zeros.
+//  Scales: wave w copies block k0/32 + w of both operands: 256 rows = 64 lanes
+//  x 4 bytes in row order.  A block outside [klo, kend) lands as zeros (scale
+//  2^-127 on zero payload).
 template <bool SCALED>
 struct Stream {
-  uint32_t offp[4], offq[4];
-  uint32_t kcol;
-  uint32_t soff;   // this wave's scale source offset within a block-row
-  uint32_t slds;   // this wave's scale destination inside a stage
+  uint32_t vp, vq;   // lane offset of load 0 without k0
+  uint32_t kcol;     // lane's chunk column within a stage (bytes)
+  uint32_t sp, sq;   // lane offset of its scale dword within a block-row
+  uint32_t klo, kend;
 
-  __device__ __forceinline__ void init(const Operand& P, const Operand& Q) {
+  __device__ __forceinline__ void init(const Operand& P, const Operand& Q, uint32_t lo,
+                                       uint32_t hi) {
+    klo = lo;
+    kend = hi;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = wave_id();
-    const uint32_t c = (lane & 3u) ^ swz(wave * 16u + (lane >> 2));
-    kcol = 16u * c;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t r = (4u * i + wave) * 16u + (lane >> 2);
-      offp[i] = min(P.row0 + r, P.rows - 1u) * P.ld + kcol;
-      offq[i] = min(Q.row0 + r, Q.rows - 1u) * Q.ld + kcol;
-    }
+    kcol = 16u * ((lane & 7u) ^ ((4u * wave + (lane >> 4)) & 7u));
+    const uint32_t r = 4u * (8u * wave + (lane >> 3));
+    vp = (P.row0 + r) * P.ld + kcol;
+    vq = (Q.row0 + r) * Q.ld + kcol;
     if (SCALED) {
-      const Operand& X = (wave >> 1) ? Q : P;
-      soff = X.row0 + 4u * lane;
-      slds = kScaleOff + (wave >> 1) * 512u + (wave & 1u) * 256u;
+      sp = P.row0 + 4u * lane;
+      sq = Q.row0 + 4u * lane;
     }
   }
 
-  __device__ __forceinline__ void issue(uint8_t* stage, const Operand& P, const Operand& Q,
-                                        uint32_t k0, uint32_t kend) {
+  // Lane offsets of stage k0 (an out-of-range base when the chunk is outside
+  // [klo, kend); adding a step to it stays out of range).
+  __device__ __forceinline__ void stage_base(uint32_t k0, uint32_t& bp, uint32_t& bq) const {
+    const uint32_t k = k0 + kcol;
+    const bool ok = k >= klo && k < kend;
+    bp = ok ? vp + k0 : kOobOffset;
+    bq = ok ? vq + k0 : kOobOffset;
+  }
+
+  __device__ __forceinline__ static uint32_t step(uint32_t i, uint32_t ld) {
+    return (128u * (i >> 2) + (i & 3u)) * ld;
+  }
+
+  __device__ __forceinline__ void load_p(uint8_t* stage, const Operand& P, uint32_t bp,
+                                         uint32_t i) const {
+    dma_x4(P.data, lds_offset(stage) + 4096u * i + 1024u * wave_id(), bp + step(i, P.ld));
+  }
+  __device__ __forceinline__ void load_q(uint8_t* stage, const Operand& Q, uint32_t bq,
+                                         uint32_t i) const {
+    dma_x4(Q.data, lds_offset(stage) + kOpBytes + 4096u * i + 1024u * wave_id(),
+           bq + step(i, Q.ld));
+  }
+  __device__ __forceinline__ void load_scales(uint8_t* stage, const Operand& P, const Operand& Q,
+                                              uint32_t k0) const {
+    if (!SCALED) return;
     const uint32_t wave = wave_id();
-    const uint32_t base = lds_offset(stage) + wave * 1024u;
-    const bool ok = k0 + kcol < kend;
+    const uint32_t blk = (k0 >> 5) + wave;
+    const bool ok = blk >= (klo >> 5) && blk < (kend >> 5);
+    const uint32_t dst = lds_offset(stage) + kScaleOff + 512u * wave;
+    dma_x1(P.scale, dst, ok ? blk * P.lds + sp : kOobOffset);
+    dma_x1(Q.scale, dst + 256u, ok ? blk * Q.lds + sq : kOobOffset);
+  }
+
+  // All loads of one stage, back to back (prologue only).
+  __device__ __forceinline__ void issue(uint8_t* stage, const Operand& P, const Operand& Q,
+                                        uint32_t k0) const {
+    uint32_t bp, bq;
+    stage_base(k0, bp, bq);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma_x4(P.data, base + 4096u * i, ok ? offp[i] + k0 : kOobOffset);
+    for (uint32_t i = 0; i < 8; ++i) load_p(stage, P, bp, i);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma_x4(Q.data, base + kOpBytes + 4096u * i, ok ? offq[i] + k0 : kOobOffset);
-    if (SCALED) {
-      const uint32_t blk = (k0 >> 5) + (wave & 1u);
-      const Operand& X = (wave >> 1) ? Q : P;
-      const uint32_t off = (blk < (kend >> 5)) ? blk * X.lds + soff : kOobOffset;
-      dma_x1(X.scale, lds_offset(stage) + slds, off);
-    }
+    for (uint32_t i = 0; i < 8; ++i) load_q(stage, Q, bq, i);
+    load_scales(stage, P, Q, k0);
   }
 };
 
-// Operands of one stage in registers: 4 P fragments, 4 Q fragments, their scales.
+// Operands of one MFMA k-step in registers: 4 P fragments, 4 Q fragments, and
+// the scale bytes of the lane's block for fragments 0..3 (byte i for
+// fragment i).
 struct Frags {
   v8i a[4], b[4];
-  uint32_t sa[4], sb[4];
+  uint32_t sa, sb;
 };
 
-// Per-lane LDS byte offsets (relative to a stage) of fragment 0; fragment i
-// adds 32 rows = 2048 bytes, its scale 32 bytes.
+// Per-lane LDS byte offsets (relative to a stage) of fragment 0 for k-step
+// t = 0, 1; fragment i adds 32 slots = 4096 bytes.
 //   v_mfma_scale_f32_32x32x64_f8f6f4 (fp8) operand layout: lane l serves row
 //   l%32; its bytes 0..15 belong to scale block 0 and bytes 16..31 to block 1
 //   of the 64-deep step, both halves of the wave sharing each block, and the
-//   block-b scale of row r comes from lane r + 32b.  So lane half h takes
-//   chunk h (of block 0: chunks 0,1) and chunk 2+h (of block 1: chunks 2,3),
-//   and the scale byte of block h.
+//   block-b scale of row r comes from lane r + 32b.  So in k-step t lane half h
+//   takes chunk 4t+h (of block 2t: chunks 4t, 4t+1) and chunk 4t+2+h (of block
+//   2t+1), and the scales of block 2t+h: lane m of fragment i serves tile row
+//   128w + 4m + i, so its four scale bytes are the dword at 128w + 4m.
 struct FragAddr {
-  uint32_t plo, phi, qlo, qhi, ps, qs;
+  uint32_t plo[2], phi[2], qlo[2], qhi[2], ps, qs;
 
   __device__ __forceinline__ void init() {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t wp = wave & 1u, wq = wave >> 1;
     const uint32_t l32 = lane & 31u, h = lane >> 5;
-    const uint32_t rp = wp * 128u + l32, rq = wq * 128u + l32;
-    // swz(r + 32i) == swz(r): adding 32 rows changes neither (r>>1)&3 nor (r>>3)&3
-    plo = rp * kStageK + ((h ^ swz(rp)) << 4);
-    phi = rp * kStageK + (((2u + h) ^ swz(rp)) << 4);
-    qlo = kOpBytes + rq * kStageK + ((h ^ swz(rq)) << 4);
-    qhi = kOpBytes + rq * kStageK + (((2u + h) ^ swz(rq)) << 4);
-    ps = kScaleOff + h * 256u + rp;
-    qs = kScaleOff + 512u + h * 256u + rq;
+    // swz(128w + 32i + m) = swz(m) for every w, i
+    const uint32_t sw = swz(l32);
+    const uint32_t rp = (wp * 128u + l32) * kStageK, rq = kOpBytes + (wq * 128u + l32) * kStageK;
+#pragma unroll
+    for (uint32_t t = 0; t < 2; ++t) {
+      plo[t] = rp + (((4u * t + h) ^ sw) << 4);
+      phi[t] = rp + (((4u * t + 2u + h) ^ sw) << 4);
+      qlo[t] = rq + (((4u * t + h) ^ sw) << 4);
+      qhi[t] = rq + (((4u * t + 2u + h) ^ sw) << 4);
+    }
+    ps = kScaleOff + h * 512u + wp * 128u + 4u * l32;
+    qs = kScaleOff + 256u + h * 512u + wq * 128u + 4u * l32;
   }
 };
 
@@ -238,98 +282,134 @@ __device__ __forceinline__ v8i lds_v8i(const uint8_t* lo, const uint8_t* hi) {
   return f;
 }
 
-// Fragment reads are split so they spread over the MFMA stream:
-//   head : Q fragments 0..3, P fragments 0..1 and all scale bytes of a stage
+// Fragment reads of k-step T are split so they spread over the MFMA stream:
+//   head : Q fragments 0..3, P fragments 0..1 and the scales
 //   tail : P fragments 2..3
-template <bool SCALED>
+// Unscaled kernels use scale byte 127 (2^0) in every position.
+template <int T>
+__device__ __forceinline__ void read_q(const uint8_t* stage, const FragAddr& fa, Frags& f, int j) {
+  f.b[j] = lds_v8i(stage + fa.qlo[T] + 4096u * j, stage + fa.qhi[T] + 4096u * j);
+}
+template <int T>
+__device__ __forceinline__ void read_p(const uint8_t* stage, const FragAddr& fa, Frags& f, int i) {
+  f.a[i] = lds_v8i(stage + fa.plo[T] + 4096u * i, stage + fa.phi[T] + 4096u * i);
+}
+template <bool SCALED, int T>
+__device__ __forceinline__ void read_scales(const uint8_t* stage, const FragAddr& fa, Frags& f) {
+  f.sa = SCALED ? *reinterpret_cast<const uint32_t*>(stage + fa.ps + 1024u * T) : 0x7F7F7F7Fu;
+  f.sb = SCALED ? *reinterpret_cast<const uint32_t*>(stage + fa.qs + 1024u * T) : 0x7F7F7F7Fu;
+}
+template <bool SCALED, int T>
 __device__ __forceinline__ void read_head(const uint8_t* stage, const FragAddr& fa, Frags& f) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) f.b[j] = lds_v8i(stage + fa.qlo + 2048u * j, stage + fa.qhi + 2048u * j);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) f.a[i] = lds_v8i(stage + fa.plo + 2048u * i, stage + fa.phi + 2048u * i);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f.sa[i] = SCALED ? (uint32_t)stage[fa.ps + 32u * i] : 127u;
-    f.sb[i] = SCALED ? (uint32_t)stage[fa.qs + 32u * i] : 127u;
-  }
+  for (int j = 0; j < 4; ++j) read_q<T>(stage, fa, f, j);
+  read_p<T>(stage, fa, f, 0);
+  read_p<T>(stage, fa, f, 1);
+  read_scales<SCALED, T>(stage, fa, f);
 }
-
+template <int T>
 __device__ __forceinline__ void read_tail(const uint8_t* stage, const FragAddr& fa, Frags& f) {
-#pragma unroll
-  for (int i = 2; i < 4; ++i) f.a[i] = lds_v8i(stage + fa.plo + 2048u * i, stage + fa.phi + 2048u * i);
+  read_p<T>(stage, fa, f, 2);
+  read_p<T>(stage, fa, f, 3);
 }
 
-__device__ __forceinline__ void mfma_row(const Frags& f, int i, v16f (&acc)[4][4]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[i], f.b[j], acc[i][j], 0, 0, 0,
-                                                               (int)f.sa[i], 0, (int)f.sb[j]);
+// One MFMA: P fragment I against Q fragment J; op_sel picks scale byte I of
+// the P dword and byte J of the Q dword.
+template <int I, int J>
+__device__ __forceinline__ void mfma1(const Frags& f, v16f (&acc)[4][4]) {
+  acc[I][J] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[I], f.b[J], acc[I][J], 0, 0, I,
+                                                              (int)f.sa, J, (int)f.sb);
+}
+template <int I>
+__device__ __forceinline__ void mfma_row(const Frags& f, v16f (&acc)[4][4]) {
+  mfma1<I, 0>(f, acc);
+  mfma1<I, 1>(f, acc);
+  mfma1<I, 2>(f, acc);
+  mfma1<I, 3>(f, acc);
 }
 
-// One stage s: issue the DMA of stage s+kAhead, read P fragments 2..3 of
-// stage s, MFMA rows 0..1, wait for stage s+1's DMA (the two younger stages
-// stay in flight) and for this wave's LDS reads, barrier, read the head of
-// stage s+1 into `nxt`, then MFMA rows 2..3, which overlap the barrier and the
-// reads.  The step has no branches: the DMA of stages past the end is issued
-// anyway (it lands as zeros in a slot nobody reads again), so the wait count
-// is a constant, and after the last stage the head read fetches a stale slot
-// that is never used.
+#define MXGG_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+// After the barrier of stage s: MFMA rows 2..3 of `cur` (k-step 1 of stage s)
+// with the 18 loads of stage s+2 (into `fill`, stage s's slot) and the head
+// reads of stage s+1 (from `next`) woven between them, two loads and two
+// fragment reads per MFMA.
 template <bool SCALED>
-__device__ __forceinline__ void stage_step(Smem& sm, Stream<SCALED>& st, const Operand& P,
-                                           const Operand& Q, const FragAddr& fa, Frags& cur,
-                                           Frags& nxt, uint32_t s, uint32_t kbeg, uint32_t kend,
-                                           v16f (&acc)[4][4]) {
-  st.issue(sm.ring[(s + kAhead) % kStages], P, Q, kbeg + (s + kAhead) * kStageK, kend);
-  read_tail(sm.ring[s % kStages], fa, cur);
-  __builtin_amdgcn_sched_barrier(0);
-  mfma_row(cur, 0, acc);
-  mfma_row(cur, 1, acc);
-  __builtin_amdgcn_sched_barrier(0);
-  publish_barrier<SCALED>();
-  __builtin_amdgcn_sched_barrier(0);
-  read_head<SCALED>(sm.ring[(s + 1) % kStages], fa, nxt);
-  mfma_row(cur, 2, acc);
-  mfma_row(cur, 3, acc);
-  __builtin_amdgcn_sched_barrier(0);
+__device__ __forceinline__ void after_barrier(const Stream<SCALED>& st, const Operand& P,
+                                              const Operand& Q, uint8_t* fill, uint32_t k0,
+                                              const uint8_t* next,
+                                              const FragAddr& fa, const Frags& cur, Frags& nxt,
+                                              v16f (&acc)[4][4]) {
+  uint32_t bp, bq;
+  st.stage_base(k0, bp, bq);
+  mfma1<2, 0>(cur, acc); st.load_p(fill, P, bp, 0); st.load_p(fill, P, bp, 1); read_q<0>(next, fa, nxt, 0); MXGG_FENCE();
+  mfma1<2, 1>(cur, acc); st.load_p(fill, P, bp, 2); st.load_p(fill, P, bp, 3); read_q<0>(next, fa, nxt, 1); MXGG_FENCE();
+  mfma1<2, 2>(cur, acc); st.load_p(fill, P, bp, 4); st.load_p(fill, P, bp, 5); read_q<0>(next, fa, nxt, 2); MXGG_FENCE();
+  mfma1<2, 3>(cur, acc); st.load_p(fill, P, bp, 6); st.load_p(fill, P, bp, 7); read_q<0>(next, fa, nxt, 3); MXGG_FENCE();
+  mfma1<3, 0>(cur, acc); st.load_q(fill, Q, bq, 0); st.load_q(fill, Q, bq, 1); read_p<0>(next, fa, nxt, 0); MXGG_FENCE();
+  mfma1<3, 1>(cur, acc); st.load_q(fill, Q, bq, 2); st.load_q(fill, Q, bq, 3); read_p<0>(next, fa, nxt, 1); MXGG_FENCE();
+  mfma1<3, 2>(cur, acc); st.load_q(fill, Q, bq, 4); st.load_q(fill, Q, bq, 5); read_scales<SCALED, 0>(next, fa, nxt); MXGG_FENCE();
+  mfma1<3, 3>(cur, acc); st.load_q(fill, Q, bq, 6); st.load_q(fill, Q, bq, 7); st.load_scales(fill, P, Q, k0); MXGG_FENCE();
 }
 
+// Accumulate D over k in [klo, kend) (both multiples of 32).  The stages start
+// at klo rounded down to 128 so that every stage reads whole cache lines of
+// rows whose stride is a multiple of 128; chunks below klo load as zeros.
 template <bool SCALED>
 __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Operand& Q,
-                                         uint32_t kbeg, uint32_t kend, v16f (&acc)[4][4]) {
+                                         uint32_t klo, uint32_t kend, v16f (&acc)[4][4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  if (kend <= kbeg) return;
-  // The loop body computes two stages; an odd stage count gets one extra
-  // stage past kend, which the DMA fills with zero payload and zero scale
-  // bytes, adding exactly nothing.  (A conditional tail stage would make the
-  // accumulators live across a branch and spill.)
-  const uint32_t nsteps = ((kend - kbeg + 2 * kStageK - 1) / (2 * kStageK)) * 2;
+  if (kend <= klo) return;
+  const uint32_t kbeg = klo & ~(uint32_t)(kStageK - 1);
+  const uint32_t nst = (kend - kbeg + kStageK - 1) / kStageK;
   Stream<SCALED> st;
-  st.init(P, Q);
+  st.init(P, Q, klo, kend);
   FragAddr fa;
   fa.init();
-  // Prologue: stages 0 .. kAhead-1 in flight, then publish stage 0.
-#pragma unroll
-  for (uint32_t s = 0; s < (uint32_t)kAhead; ++s)
-    st.issue(sm.ring[s], P, Q, kbeg + s * kStageK, kend);
-  publish_barrier<SCALED>();
-  __builtin_amdgcn_sched_barrier(0);
+  // Prologue: stages 0 and 1 in flight, publish stage 0.
+  st.issue(sm.ring[0], P, Q, kbeg);
+  st.issue(sm.ring[1], P, Q, kbeg + kStageK);
+  wait_barrier<(int)dma_per_stage<SCALED>()>();
+  MXGG_FENCE();
   Frags f0, f1;
-  read_head<SCALED>(sm.ring[0], fa, f0);
-  // Stage s+kAhead goes into the ring slot of stage s-1, which every wave
-  // finished reading before the barrier inside step s-1.
-  for (uint32_t s = 0; s < nsteps; s += 2) {
-    stage_step<SCALED>(sm, st, P, Q, fa, f0, f1, s, kbeg, kend, acc);
-    stage_step<SCALED>(sm, st, P, Q, fa, f1, f0, s + 1, kbeg, kend, acc);
+  read_head<SCALED, 0>(sm.ring[0], fa, f0);
+  // Stage s lives in slot s%2.  Past the last stage the loads fetch zeros into
+  // a slot nobody reads again, and the final head read fetches a stale slot
+  // that is never used, so the loop body has no branches.
+  for (uint32_t s = 0; s < nst; ++s) {
+    uint8_t* cur = sm.ring[s & 1u];
+    uint8_t* nxt = sm.ring[(s & 1u) ^ 1u];
+    // k-step 0 (f0), head of k-step 1 into f1
+    read_tail<0>(cur, fa, f0);
+    MXGG_FENCE();
+    mfma_row<0>(f0, acc);
+    mfma_row<1>(f0, acc);
+    MXGG_FENCE();
+    read_head<SCALED, 1>(cur, fa, f1);
+    mfma_row<2>(f0, acc);
+    mfma_row<3>(f0, acc);
+    MXGG_FENCE();
+    // k-step 1 (f1)
+    read_tail<1>(cur, fa, f1);
+    MXGG_FENCE();
+    mfma_row<0>(f1, acc);
+    mfma_row<1>(f1, acc);
+    MXGG_FENCE();
+    // stage s+1 has landed and stage s is fully read: publish, refill slot s%2
+    wait_barrier<0>();
+    MXGG_FENCE();
+    after_barrier<SCALED>(st, P, Q, cur, kbeg + (s + 2) * kStageK, nxt, fa, f1, f0, acc);
   }
-  // Drain the DMA of the stages past the end before the next tile's prologue
-  // reuses the ring.
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  // Drain the loads past the end before the next tile's prologue reuses the slots.
+  wait_barrier<0>();
 }
+
+#undef MXGG_FENCE
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   const __bf16 ha = (__bf16)a, hb = (__bf16)b;
@@ -338,12 +418,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return (uint32_t)ua | ((uint32_t)ub << 16);
 }
 
-// Store the 4 consecutive outputs (P index p..p+3) of accumulator quad rg of
-// block (i, j) for this lane's Q index.  `rowp` points at element [q][0].
+// Store 4 consecutive outputs (P index p..p+3) of this lane's Q index.
+// `rowp` points at element [q][0].
 template <bool F32>
-__device__ __forceinline__ void store4(void* rowp, uint32_t p, uint32_t pend, const v16f& a,
-                                       int rg) {
-  const float v0 = a[4 * rg + 0], v1 = a[4 * rg + 1], v2 = a[4 * rg + 2], v3 = a[4 * rg + 3];
+__device__ __forceinline__ void store4(void* rowp, uint32_t p, uint32_t pend, float v0, float v1,
+                                       float v2, float v3) {
   if (F32) {
     float* d = reinterpret_cast<float*>(rowp) + p;
     if (p + 3 < pend) {
@@ -369,6 +448,10 @@ __device__ __forceinline__ void store4(void* rowp, uint32_t p, uint32_t pend, co
 }
 
 // Write the tile: output row = Q index in [qbeg, qend), column = P index < pend.
+// Accumulator register r of block (i, j) in lane (l32, h) is D[8(r/4) + 4h +
+// r%4][l32] of the 32x32 MFMA, i.e. P index 128wp + 4(8(r/4) + 4h + r%4) + i
+// and Q index 128wq + 4*l32 + j: the four blocks i = 0..3 hold four
+// consecutive P indices.
 template <bool F32>
 __device__ __forceinline__ void epilogue(const v16f (&acc)[4][4], char* out, int64_t ldo_bytes,
                                          uint32_t q0, uint32_t qbeg, uint32_t qend, uint32_t p0,
@@ -379,16 +462,13 @@ __device__ __forceinline__ void epilogue(const v16f (&acc)[4][4], char* out, int
   const uint32_t l32 = lane & 31u, h = lane >> 5;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t q = q0 + wq * 128u + 32u * j + l32;
+    const uint32_t q = q0 + wq * 128u + 4u * l32 + j;
     if (q < qbeg || q >= qend) continue;
     char* rowp = out + (int64_t)q * ldo_bytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int rg = 0; rg < 4; ++rg) {
-        const uint32_t p = p0 + wp * 128u + 32u * i + 8u * rg + 4u * h;
-        if (p < pend) store4<F32>(rowp, p, pend, acc[i][j], rg);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const uint32_t p = p0 + wp * 128u + 4u * (8u * (r >> 2) + 4u * h + (r & 3));
+      if (p < pend) store4<F32>(rowp, p, pend, acc[0][j][r], acc[1][j][r], acc[2][j][r], acc[3][j][r]);
     }
   }
 }
@@ -501,11 +581,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
     P.data = make_desc(wg, (uint32_t)((int64_t)(args.N - 1) * args.ldw + K));
     P.ld = (uint32_t)args.ldw;
     P.row0 = p0;
-    P.rows = (uint32_t)args.N;
     Q.data = make_desc(args.a, (uint32_t)((int64_t)(M - 1) * args.lda + K));
     Q.ld = (uint32_t)args.lda;
     Q.row0 = q0;
-    Q.rows = (uint32_t)M;
     if (SCALED) {
       const uint8_t* wsg = args.ws + (int64_t)g * args.ws_gstride;
       P.scale = make_desc(wsg, scale_extent(K / 32, args.ldws, args.N));
@@ -569,11 +647,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
     P.data = make_desc(args.ia, (uint32_t)((int64_t)(args.K - 1) * args.ldia + M));
     P.ld = (uint32_t)args.ldia;
     P.row0 = p0;
-    P.rows = (uint32_t)args.K;
     Q.data = make_desc(args.go, (uint32_t)((int64_t)(args.N - 1) * args.ldgo + M));
     Q.ld = (uint32_t)args.ldgo;
     Q.row0 = q0;
-    Q.rows = (uint32_t)args.N;
     if (SCALED) {
       P.scale = make_desc(args.ias, scale_extent(M / 32, args.ldias, args.K));
       P.lds = (uint32_t)args.ldias;

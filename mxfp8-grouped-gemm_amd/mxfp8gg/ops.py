@@ -196,9 +196,14 @@ def to_mxfp8_dim0(x: torch.Tensor, scaling_mode="rceil"):
 
 
 def padded_token_capacity(num_tokens: int, num_groups: int | None) -> int:
-    """Columns of the dim1 output: every group padded to 32 tokens."""
-    extra = 31 * num_groups if num_groups else 0
-    return (num_tokens + extra + 31) // 32 * 32
+    """Columns of the dim1 output.
+
+    Ungrouped: the tokens rounded up to 32.  Grouped: room for every group
+    padded to 32 tokens, rounded up to 128 so that each row starts on a
+    128-byte cache line (the wgrad GEMM streams whole lines)."""
+    if not num_groups:
+        return (num_tokens + 31) // 32 * 32
+    return (num_tokens + 31 * num_groups + 127) // 128 * 128
 
 
 def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mode="rceil"):

@@ -58,7 +58,8 @@ def test_offs_forms():
 def test_padded_capacity():
     assert ops.padded_token_capacity(64, None) == 64
     assert ops.padded_token_capacity(65, None) == 96
-    assert ops.padded_token_capacity(100, 4) == (100 + 124 + 31) // 32 * 32
+    assert ops.padded_token_capacity(100, 4) == 256   # 100 + 4*31 rounded up to 128
+    assert ops.padded_token_capacity(65536, 32) % 128 == 0
 
 
 def test_workload_routing_shapes():
