@@ -418,59 +418,73 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return (uint32_t)ua | ((uint32_t)ub << 16);
 }
 
-// Store 4 consecutive outputs (P index p..p+3) of this lane's Q index.
-// `rowp` points at element [q][0].
-template <bool F32>
-__device__ __forceinline__ void store4(void* rowp, uint32_t p, uint32_t pend, float v0, float v1,
-                                       float v2, float v3) {
-  if (F32) {
-    float* d = reinterpret_cast<float*>(rowp) + p;
-    if (p + 3 < pend) {
-      *reinterpret_cast<float4*>(d) = make_float4(v0, v1, v2, v3);
-    } else {
-      const float v[4] = {v0, v1, v2, v3};
-      for (int u = 0; u < 4; ++u)
-        if (p + u < pend) d[u] = v[u];
-    }
-  } else {
-    uint16_t* d = reinterpret_cast<uint16_t*>(rowp) + p;
-    if (p + 3 < pend) {
-      *reinterpret_cast<uint2*>(d) = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
-    } else {
-      const float v[4] = {v0, v1, v2, v3};
-      for (int u = 0; u < 4; ++u)
-        if (p + u < pend) {
-          const __bf16 hv = (__bf16)v[u];
-          d[u] = *reinterpret_cast<const uint16_t*>(&hv);
-        }
-    }
-  }
-}
-
 // Write the tile: output row = Q index in [qbeg, qend), column = P index < pend.
 // Accumulator register r of block (i, j) in lane (l32, h) is D[8(r/4) + 4h +
-// r%4][l32] of the 32x32 MFMA, i.e. P index 128wp + 4(8(r/4) + 4h + r%4) + i
-// and Q index 128wq + 4*l32 + j: the four blocks i = 0..3 hold four
-// consecutive P indices.
+// r%4][l32] of the 32x32 MFMA, i.e. P index 128wp + 4c + i with
+// c = 8(r/4) + 4h + r%4, and Q index 128wq + 4*l32 + j: the four blocks
+// i = 0..3 hold one 4-value chunk of consecutive P indices.
+// Stored directly, every store instruction would scatter 64 small pieces over
+// 32 rows.  Instead each wave stages its 128x128 fp32 sub-tile in its own
+// 32 KB of the idle LDS ring, in two passes of 64 rows (j = 0,1 then j = 2,3;
+// staged row s = 2*l32 + j%2, 512 B), and then stores whole rows: 32 lanes x
+// 4 values, converted to bf16 after the read for bf16 output.  The 16-byte
+// chunk k of staged row s sits at k ^ ((s/2) mod 16), so a half-wave writing
+// one chunk column of 32 rows, and one reading a whole row, touches each LDS
+// bank exactly twice.  The staging writes take the accumulators straight from
+// AGPRs.
 template <bool F32>
-__device__ __forceinline__ void epilogue(const v16f (&acc)[4][4], char* out, int64_t ldo_bytes,
-                                         uint32_t q0, uint32_t qbeg, uint32_t qend, uint32_t p0,
-                                         uint32_t pend) {
+__device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char* out,
+                                         int64_t ldo_bytes, uint32_t q0, uint32_t qbeg,
+                                         uint32_t qend, uint32_t p0, uint32_t pend) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t wp = wave & 1u, wq = wave >> 1;
   const uint32_t l32 = lane & 31u, h = lane >> 5;
+  uint8_t* stage = &sm.ring[0][0] + wave * 32768u;
+  const uint32_t p = p0 + wp * 128u + 4u * l32;  // this lane's 4 columns on the way out
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t q = q0 + wq * 128u + 4u * l32 + j;
-    if (q < qbeg || q >= qend) continue;
-    char* rowp = out + (int64_t)q * ldo_bytes;
+  for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint32_t p = p0 + wp * 128u + 4u * (8u * (r >> 2) + 4u * h + (r & 3));
-      if (p < pend) store4<F32>(rowp, p, pend, acc[0][j][r], acc[1][j][r], acc[2][j][r], acc[3][j][r]);
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * pass + jj;
+      uint8_t* row = stage + (2u * l32 + (uint32_t)jj) * 512u;
+      const uint32_t sw = l32 & 15u;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t c = 8u * (r >> 2) + 4u * h + (r & 3);
+        *reinterpret_cast<float4*>(row + ((c ^ sw) << 4)) =
+            make_float4(acc[0][j][r], acc[1][j][r], acc[2][j][r], acc[3][j][r]);
+      }
+    }
+    // This wave's LDS writes complete before its reads (in-order LDS queue).
+#pragma unroll 4
+    for (uint32_t t = 0; t < 32u; ++t) {
+      const uint32_t s = 2u * t + h;
+      const float4 v =
+          *reinterpret_cast<const float4*>(stage + s * 512u + ((l32 ^ (t & 15u)) << 4));
+      const uint32_t q = q0 + wq * 128u + 4u * t + 2u * (uint32_t)pass + h;
+      if (q < qbeg || q >= qend || p >= pend) continue;
+      char* dst = out + (int64_t)q * ldo_bytes + (int64_t)p * (F32 ? 4 : 2);
+      if (p + 4u <= pend) {
+        if (F32)
+          *reinterpret_cast<float4*>(dst) = v;
+        else
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+      } else {
+        const float w[4] = {v.x, v.y, v.z, v.w};
+        for (uint32_t u = 0; p + u < pend; ++u) {
+          if (F32) {
+            reinterpret_cast<float*>(dst)[u] = w[u];
+          } else {
+            const __bf16 b = (__bf16)w[u];
+            reinterpret_cast<uint16_t*>(dst)[u] = *reinterpret_cast<const uint16_t*>(&b);
+          }
+        }
+      }
     }
   }
+  // Every wave has read its staging area before the next tile's loads land in the ring.
+  __syncthreads();
 }
 
 // Decode a position in the tile order into (mt, nt): bands of `gm`
@@ -594,7 +608,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
     v16f acc[4][4];
     mainloop<SCALED>(sm, P, Q, 0u, K, acc);
     const int64_t ldo_bytes = args.ldo * (F32 ? 4 : 2);
-    epilogue<F32>(acc, reinterpret_cast<char*>(args.out), ldo_bytes, q0, (uint32_t)gb,
+    epilogue<F32>(sm, acc, reinterpret_cast<char*>(args.out), ldo_bytes, q0, (uint32_t)gb,
                   (uint32_t)ge, p0, (uint32_t)args.N);
   }
 }
@@ -671,7 +685,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
     }
     char* out = reinterpret_cast<char*>(args.dw) +
                 (int64_t)g * args.N * args.K * (F32 ? 4 : 2);
-    epilogue<F32>(acc, out, (int64_t)args.K * (F32 ? 4 : 2), q0, 0u, (uint32_t)args.N, p0,
+    epilogue<F32>(sm, acc, out, (int64_t)args.K * (F32 ? 4 : 2), q0, 0u, (uint32_t)args.N, p0,
                   (uint32_t)args.K);
   }
 }
