@@ -114,100 +114,127 @@ __device__ void groups_to_lds(const int32_t* __restrict__ ends, int E, int64_t r
 }
 
 // ---------------------------------------------------------------------------
-// dim1.  Block = 128 padded token columns x 64 features.  Load phase gathers
-// token rows (16 B per thread-chunk, coalesced along features) and stores them
-// transposed into LDS; compute phase gives each thread one feature and one
-// 32-token block, so four consecutive lanes write 128 contiguous output bytes.
+// Padded group ends for dim1 (one workgroup): ends_pad[g] = sum over groups
+// <= g of round_up(size, 32), sizes taken from the clamped ends.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_pad_ends(const int32_t* __restrict__ ends, int E,
+                                                  int64_t rows, int32_t* __restrict__ ends_pad) {
+  __shared__ int32_t ends_s[kMaxGroups];
+  __shared__ int32_t pend_s[kMaxGroups];
+  __shared__ int32_t tmp[256];
+  groups_to_lds(ends, E, rows, ends_s, pend_s, tmp);
+  for (int g = threadIdx.x; g < E; g += 256) ends_pad[g] = pend_s[g];
+}
+
+// One value of a block: x * 2^e clamped to +-448 (FLOOR NaN blocks divide by +inf).
+template <int MODE>
+__device__ __forceinline__ float scaled1(uint32_t bits16, uint32_t b, int e) {
+  const float x = bf16_bits_to_f32(bits16);
+  if (MODE == kModeFloor && b == 255u) return floor_nan_block_value(x);
+  return scale_and_clamp(x, e);
+}
+
+// ---------------------------------------------------------------------------
+// dim1.  A wave covers 128 padded token positions x 64 features; lane
+// (tg = lane % 8, fg = lane / 8) owns positions 16*tg .. +15 of the tile and
+// features 8*fg .. +7.  It loads its 16 token rows as 16-byte vectors (eight
+// lanes read one whole 128-byte line of a row), takes each feature's amax over
+// its 16 tokens, combines it with lane tg^1 (the other half of the 32-token
+// block), and writes 16 payload bytes per feature (eight lanes write one whole
+// 128-byte line of an output row).  No LDS transpose is needed.  Padded
+// positions map to tokens through the padded group ends; a run of 16 never
+// straddles two groups because every group starts on a multiple of 32.
+// A workgroup is 4 waves along the features (128 positions x 256 features).
 // ---------------------------------------------------------------------------
 template <int MODE, bool SW>
 __global__ __launch_bounds__(256) void k_quant_dim1(
     const uint16_t* __restrict__ x, int64_t rows, int cols, int64_t ldx,
-    const int32_t* __restrict__ ends, int E, int64_t rows_pad_cap, uint8_t* __restrict__ qt,
-    int64_t ldqt, uint8_t* __restrict__ st, int64_t st_row, int64_t st_blk,
-    int32_t* __restrict__ ends_pad_out) {
-  __shared__ __align__(16) uint16_t tile[64][136];
+    const int32_t* __restrict__ ends, const int32_t* __restrict__ ends_pad, int E,
+    int64_t rows_pad_cap, uint8_t* __restrict__ qt, int64_t ldqt, uint8_t* __restrict__ st,
+    int64_t st_row, int64_t st_blk) {
   __shared__ int32_t ends_s[kMaxGroups];
   __shared__ int32_t pend_s[kMaxGroups];
-  __shared__ int32_t tmp[256];
+  const int lane = threadIdx.x & 63;
+  const int tg = lane & 7, fg = lane >> 3;
+  const int64_t P = (int64_t)blockIdx.x * 128 + 16 * tg;
+  const int f = blockIdx.y * 256 + (threadIdx.x >> 6) * 64 + 8 * fg;
 
-  const int t = threadIdx.x;
+  int64_t tok0 = 0;
+  int ntok = 0;
   if (ends != nullptr) {
-    groups_to_lds(ends, E, rows, ends_s, pend_s, tmp);
-    if (blockIdx.x == 0 && blockIdx.y == 0) {
-      for (int g = t; g < E; g += 256) ends_pad_out[g] = pend_s[g];
+    for (int g = threadIdx.x; g < E; g += 256) {
+      const int32_t e = ends[g];
+      ends_s[g] = e < 0 ? 0 : (e > rows ? (int32_t)rows : e);
+      pend_s[g] = ends_pad[g];
     }
+    __syncthreads();
+    // first group whose padded end is > P
+    int lo = 0, hi = E;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if ((int64_t)pend_s[mid] > P) hi = mid; else lo = mid + 1;
+    }
+    if (lo < E) {
+      const int64_t pstart = lo > 0 ? pend_s[lo - 1] : 0;
+      const int64_t gstart = lo > 0 ? ends_s[lo - 1] : 0;
+      const int64_t gend = ends_s[lo];
+      tok0 = gstart + (P - pstart);
+      const int64_t n = gend - tok0;  // negative when the clamped start exceeds the end
+      ntok = n <= 0 ? 0 : (n >= 16 ? 16 : (int)n);
+    }
+  } else {
+    tok0 = P;
+    const int64_t n = rows - P;
+    ntok = n <= 0 ? 0 : (n >= 16 ? 16 : (int)n);
   }
-  const int64_t p0 = (int64_t)blockIdx.x * 128;
-  const int f0 = blockIdx.y * 64;
+  if (f >= cols) ntok = 0;
 
+  uint4 v[16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int chunk = t + 256 * i;
-    const int r = chunk >> 3;
-    const int fc = chunk & 7;
-    const int64_t p = p0 + r;
-    int64_t tok = -1;
-    if (ends == nullptr) {
-      tok = p < rows ? p : -1;
-    } else {
-      // first group whose padded end is > p
-      int lo = 0, hi = E;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if ((int64_t)pend_s[mid] > p) hi = mid; else lo = mid + 1;
-      }
-      if (lo < E) {
-        const int64_t pstart = lo > 0 ? pend_s[lo - 1] : 0;
-        const int64_t gstart = lo > 0 ? ends_s[lo - 1] : 0;
-        const int64_t cand = gstart + (p - pstart);
-        tok = cand < (int64_t)ends_s[lo] ? cand : -1;
-        // a group whose clamped start exceeds its end holds no tokens
-        if (gstart > ends_s[lo]) tok = -1;
-      }
-    }
-    const int f = f0 + fc * 8;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (tok >= 0 && f < cols) v = *reinterpret_cast<const uint4*>(x + tok * ldx + f);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      tile[fc * 8 + 2 * u][r] = (uint16_t)(w[u] & 0xFFFFu);
-      tile[fc * 8 + 2 * u + 1][r] = (uint16_t)(w[u] >> 16);
-    }
+  for (int i = 0; i < 16; ++i) {
+    v[i] = i < ntok ? *reinterpret_cast<const uint4*>(x + (tok0 + i) * ldx + f)
+                    : make_uint4(0, 0, 0, 0);
   }
-  __syncthreads();
-
-  const int f = t >> 2;
-  const int tb = t & 3;
-  const int64_t pc = p0 + tb * 32;
-  if (f0 + f < cols && pc < rows_pad_cap) {
-    const uint4* src = reinterpret_cast<const uint4*>(&tile[f][tb * 32]);
-    uint4 v[4] = {src[0], src[1], src[2], src[3]};
+  const bool out_ok = f < cols && P < rows_pad_cap;
+  uint32_t bytes[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int sh = 16 * (j & 1);
     uint32_t am = 0;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      am = max(am, amax16_of_word(v[u].x));
-      am = max(am, amax16_of_word(v[u].y));
-      am = max(am, amax16_of_word(v[u].z));
-      am = max(am, amax16_of_word(v[u].w));
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t w = (j >> 1) == 0 ? v[i].x : (j >> 1) == 1 ? v[i].y : (j >> 1) == 2 ? v[i].z : v[i].w;
+      am = max(am, (w >> sh) & 0x7FFFu);
     }
+    am = max(am, (uint32_t)__shfl_xor((int)am, 1));
     const uint32_t b = e8m0_from_amax16<MODE>(am);
     const int e = payload_exponent<MODE>(b);
-    uint32_t out[8];
+    bytes[j] = b;
+    uint32_t o[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      float f8[8];
-      bf16x2_to_scaled<MODE>(v[u].x, b, e, f8[0], f8[1]);
-      bf16x2_to_scaled<MODE>(v[u].y, b, e, f8[2], f8[3]);
-      bf16x2_to_scaled<MODE>(v[u].z, b, e, f8[4], f8[5]);
-      bf16x2_to_scaled<MODE>(v[u].w, b, e, f8[6], f8[7]);
-      out[2 * u] = e4m3_pack4<SW>(f8[0], f8[1], f8[2], f8[3]);
-      out[2 * u + 1] = e4m3_pack4<SW>(f8[4], f8[5], f8[6], f8[7]);
+    for (int k = 0; k < 4; ++k) {
+      float y[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = 4 * k + u;
+        const uint32_t w = (j >> 1) == 0 ? v[i].x : (j >> 1) == 1 ? v[i].y : (j >> 1) == 2 ? v[i].z : v[i].w;
+        y[u] = scaled1<MODE>((w >> sh) & 0xFFFFu, b, e);
+      }
+      o[k] = e4m3_pack4<SW>(y[0], y[1], y[2], y[3]);
     }
-    uint8_t* dst = qt + (int64_t)(f0 + f) * ldqt + pc;
-    reinterpret_cast<uint4*>(dst)[0] = make_uint4(out[0], out[1], out[2], out[3]);
-    reinterpret_cast<uint4*>(dst)[1] = make_uint4(out[4], out[5], out[6], out[7]);
-    st[(int64_t)(f0 + f) * st_row + (pc >> 5) * st_blk] = (uint8_t)b;
+    if (out_ok)
+      *reinterpret_cast<uint4*>(qt + (int64_t)(f + j) * ldqt + P) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+  if (out_ok && (tg & 1) == 0) {
+    uint8_t* sp = st + (int64_t)f * st_row + (P >> 5) * st_blk;
+    if (st_row == 1 && (reinterpret_cast<uintptr_t>(sp) & 7u) == 0) {
+      *reinterpret_cast<uint2*>(sp) = make_uint2(
+          bytes[0] | (bytes[1] << 8) | (bytes[2] << 16) | (bytes[3] << 24),
+          bytes[4] | (bytes[5] << 8) | (bytes[6] << 16) | (bytes[7] << 24));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sp[(int64_t)j * st_row] = (uint8_t)bytes[j];
+    }
   }
 }
 
@@ -226,9 +253,14 @@ hipError_t dim1_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
                      const int32_t* ends, int64_t E, int64_t cap, uint8_t* qt, int64_t ldqt,
                      uint8_t* st, int64_t st_row, int64_t st_blk, int32_t* ends_pad,
                      hipStream_t stream) {
-  dim3 grid((unsigned)((cap + 127) / 128), (unsigned)((cols + 63) / 64));
+  if (ends != nullptr) {
+    hipLaunchKernelGGL(k_pad_ends, dim3(1), dim3(256), 0, stream, ends, (int)E, rows, ends_pad);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  dim3 grid((unsigned)((cap + 127) / 128), (unsigned)((cols + 255) / 256));
   hipLaunchKernelGGL((k_quant_dim1<MODE, SW>), grid, dim3(256), 0, stream, x, rows, (int)cols, ldx,
-                     ends, (int)E, cap, qt, ldqt, st, st_row, st_blk, ends_pad);
+                     ends, ends_pad, (int)E, cap, qt, ldqt, st, st_row, st_blk);
   return hipGetLastError();
 }
 
