@@ -24,11 +24,10 @@
 // and their 8 scale rows, all written by LDS-DMA (buffer_load ... lds).
 // Reading whole lines matters: with 64-byte stages every line crossed the
 // L2 -> L1 path twice and the L2 request rate, not the MFMA pipe, set the
-// speed.  Stage s+2 is requested right after the barrier that publishes
-// stage s+1 (which also retires all reads of stage s, whose slot it reuses), so
-// every load has a whole stage of compute to land.  The MFMA sequence is split
-// around that barrier: the last 8 MFMAs of stage s run while the waves
-// synchronise, issue the loads and read stage s+1's first operands.
+// speed.  Each stage has a release barrier (every wave has read the stage into
+// registers, so its slot can be refilled with stage s+2) and a publish barrier
+// (stage s+1 has landed); the loads are spread one per MFMA, because a DMA
+// instruction stalls its wave's issue until the address unit accepts it.
 // Persistent grid (one workgroup per CU), tiles dealt round-robin with each XCD
 // taking a contiguous slice of every round.
 #include <algorithm>
@@ -46,9 +45,6 @@ constexpr int kMaxGroups = 1024;
 constexpr uint32_t kOpBytes = 256u * kStageK;          // one operand of one stage: 32 KB
 constexpr uint32_t kScaleOff = 2u * kOpBytes;          // scale rows after P and Q data
 constexpr uint32_t kStageBytes = kScaleOff + 4u * 512u;  // + [4 blocks][P, Q][256]
-// DMA instructions per wave per stage: 8 P + 8 Q (+ 1 P-scale + 1 Q-scale)
-template <bool SCALED>
-constexpr uint32_t dma_per_stage() { return SCALED ? 18u : 16u; }
 constexpr uint32_t kOobOffset = 0x80000000u;           // beyond every num_records we create
 
 struct __align__(16) Smem {
@@ -209,27 +205,26 @@ struct Stream {
     dma_x4(Q.data, lds_offset(stage) + kOpBytes + 4096u * i + 1024u * wave_id(),
            bq + step(i, Q.ld));
   }
-  __device__ __forceinline__ void load_scales(uint8_t* stage, const Operand& P, const Operand& Q,
-                                              uint32_t k0) const {
+  // Scale rows of k-block k0/32 + wave; operand X = P (OP 0) or Q (OP 1).
+  template <int OP>
+  __device__ __forceinline__ void load_scale(uint8_t* stage, const Operand& X, uint32_t k0) const {
     if (!SCALED) return;
     const uint32_t wave = wave_id();
     const uint32_t blk = (k0 >> 5) + wave;
     const bool ok = blk >= (klo >> 5) && blk < (kend >> 5);
-    const uint32_t dst = lds_offset(stage) + kScaleOff + 512u * wave;
-    dma_x1(P.scale, dst, ok ? blk * P.lds + sp : kOobOffset);
-    dma_x1(Q.scale, dst + 256u, ok ? blk * Q.lds + sq : kOobOffset);
+    dma_x1(X.scale, lds_offset(stage) + kScaleOff + 512u * wave + 256u * OP,
+           ok ? blk * X.lds + (OP ? sq : sp) : kOobOffset);
   }
 
-  // All loads of one stage, back to back (prologue only).
-  __device__ __forceinline__ void issue(uint8_t* stage, const Operand& P, const Operand& Q,
-                                        uint32_t k0) const {
+  // The 16 data loads of one stage, back to back (prologue only).
+  __device__ __forceinline__ void issue_data(uint8_t* stage, const Operand& P, const Operand& Q,
+                                             uint32_t k0) const {
     uint32_t bp, bq;
     stage_base(k0, bp, bq);
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) load_p(stage, P, bp, i);
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) load_q(stage, Q, bq, i);
-    load_scales(stage, P, Q, k0);
   }
 };
 
@@ -330,31 +325,31 @@ __device__ __forceinline__ void mfma_row(const Frags& f, v16f (&acc)[4][4]) {
 
 #define MXGG_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-// After the barrier of stage s: MFMA rows 2..3 of `cur` (k-step 1 of stage s)
-// with the 18 loads of stage s+2 (into `fill`, stage s's slot) and the head
-// reads of stage s+1 (from `next`) woven between them, two loads and two
-// fragment reads per MFMA.
-template <bool SCALED>
-__device__ __forceinline__ void after_barrier(const Stream<SCALED>& st, const Operand& P,
-                                              const Operand& Q, uint8_t* fill, uint32_t k0,
-                                              const uint8_t* next,
-                                              const FragAddr& fa, const Frags& cur, Frags& nxt,
-                                              v16f (&acc)[4][4]) {
-  uint32_t bp, bq;
-  st.stage_base(k0, bp, bq);
-  mfma1<2, 0>(cur, acc); st.load_p(fill, P, bp, 0); st.load_p(fill, P, bp, 1); read_q<0>(next, fa, nxt, 0); MXGG_FENCE();
-  mfma1<2, 1>(cur, acc); st.load_p(fill, P, bp, 2); st.load_p(fill, P, bp, 3); read_q<0>(next, fa, nxt, 1); MXGG_FENCE();
-  mfma1<2, 2>(cur, acc); st.load_p(fill, P, bp, 4); st.load_p(fill, P, bp, 5); read_q<0>(next, fa, nxt, 2); MXGG_FENCE();
-  mfma1<2, 3>(cur, acc); st.load_p(fill, P, bp, 6); st.load_p(fill, P, bp, 7); read_q<0>(next, fa, nxt, 3); MXGG_FENCE();
-  mfma1<3, 0>(cur, acc); st.load_q(fill, Q, bq, 0); st.load_q(fill, Q, bq, 1); read_p<0>(next, fa, nxt, 0); MXGG_FENCE();
-  mfma1<3, 1>(cur, acc); st.load_q(fill, Q, bq, 2); st.load_q(fill, Q, bq, 3); read_p<0>(next, fa, nxt, 1); MXGG_FENCE();
-  mfma1<3, 2>(cur, acc); st.load_q(fill, Q, bq, 4); st.load_q(fill, Q, bq, 5); read_scales<SCALED, 0>(next, fa, nxt); MXGG_FENCE();
-  mfma1<3, 3>(cur, acc); st.load_q(fill, Q, bq, 6); st.load_q(fill, Q, bq, 7); st.load_scales(fill, P, Q, k0); MXGG_FENCE();
+// Workgroup barrier after this wave's LDS reads have returned (no wait on
+// the DMA), as assembly for the same reason as wait_barrier().
+__device__ __forceinline__ void release_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // Accumulate D over k in [klo, kend) (both multiples of 32).  The stages start
 // at klo rounded down to 128 so that every stage reads whole cache lines of
 // rows whose stride is a multiple of 128; chunks below klo load as zeros.
+//
+// Stage s lives in slot s%2; f0 holds k-step 0 and f1 k-step 1 of a stage.
+// A DMA instruction holds up its wave's issue until the address unit takes
+// it, so the 18 loads of a stage are spread one per MFMA.  Per stage, with the
+// MFMA count reached at each point:
+//    0  read P tail of k-step 0; MFMA rows 0-1 of f0, the first two carrying
+//       the scale loads of stage s+1
+//    8  read all of k-step 1 into f1; MFMA rows 2-3 of f0
+//   16  release barrier: every wave has read all of slot s%2 -> MFMA rows 0-1
+//       of f1, each followed by one P load of stage s+2 into that slot
+//   24  publish barrier: everything older than those 8 loads, i.e. all of
+//       stage s+1, has landed -> MFMA rows 2-3 of f1, each followed by one Q
+//       load of stage s+2, with the head of stage s+1's k-step 0 read into f0
+// so a load has at least 22 MFMAs of compute to land in.  The vmcnt of both
+// waits is the same (16 in the prologue, 8 in the loop) with or without
+// scales, because the scale loads are always the oldest of their group.
 template <bool SCALED>
 __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Operand& Q,
                                          uint32_t klo, uint32_t kend, v16f (&acc)[4][4]) {
@@ -371,39 +366,58 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
   st.init(P, Q, klo, kend);
   FragAddr fa;
   fa.init();
-  // Prologue: stages 0 and 1 in flight, publish stage 0.
-  st.issue(sm.ring[0], P, Q, kbeg);
-  st.issue(sm.ring[1], P, Q, kbeg + kStageK);
-  wait_barrier<(int)dma_per_stage<SCALED>()>();
+  // Prologue: all of stage 0 and the data of stage 1 (its scales follow in
+  // the first stage), then publish stage 0.
+  st.issue_data(sm.ring[0], P, Q, kbeg);
+  st.template load_scale<0>(sm.ring[0], P, kbeg);
+  st.template load_scale<1>(sm.ring[0], Q, kbeg);
+  st.issue_data(sm.ring[1], P, Q, kbeg + kStageK);
+  wait_barrier<16>();
   MXGG_FENCE();
   Frags f0, f1;
   read_head<SCALED, 0>(sm.ring[0], fa, f0);
-  // Stage s lives in slot s%2.  Past the last stage the loads fetch zeros into
-  // a slot nobody reads again, and the final head read fetches a stale slot
-  // that is never used, so the loop body has no branches.
+  // Past the last stage the loads fetch zeros into a slot nobody reads again,
+  // and the final head read fetches a stale slot that is never used, so the
+  // loop body has no branches.
   for (uint32_t s = 0; s < nst; ++s) {
     uint8_t* cur = sm.ring[s & 1u];
     uint8_t* nxt = sm.ring[(s & 1u) ^ 1u];
-    // k-step 0 (f0), head of k-step 1 into f1
+    const uint32_t knext = kbeg + (s + 1) * kStageK;
+    uint32_t bp, bq;
+    st.stage_base(kbeg + (s + 2) * kStageK, bp, bq);
     read_tail<0>(cur, fa, f0);
     MXGG_FENCE();
-    mfma_row<0>(f0, acc);
+    mfma1<0, 0>(f0, acc); st.template load_scale<0>(nxt, P, knext); MXGG_FENCE();
+    mfma1<0, 1>(f0, acc); st.template load_scale<1>(nxt, Q, knext); MXGG_FENCE();
+    mfma1<0, 2>(f0, acc);
+    mfma1<0, 3>(f0, acc);
     mfma_row<1>(f0, acc);
     MXGG_FENCE();
     read_head<SCALED, 1>(cur, fa, f1);
+    read_tail<1>(cur, fa, f1);
     mfma_row<2>(f0, acc);
     mfma_row<3>(f0, acc);
     MXGG_FENCE();
-    // k-step 1 (f1)
-    read_tail<1>(cur, fa, f1);
+    release_barrier();
     MXGG_FENCE();
-    mfma_row<0>(f1, acc);
-    mfma_row<1>(f1, acc);
+    mfma1<0, 0>(f1, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
+    mfma1<0, 1>(f1, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
+    mfma1<0, 2>(f1, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
+    mfma1<0, 3>(f1, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
+    mfma1<1, 0>(f1, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
+    mfma1<1, 1>(f1, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
+    mfma1<1, 2>(f1, acc); st.load_p(cur, P, bp, 6); MXGG_FENCE();
+    mfma1<1, 3>(f1, acc); st.load_p(cur, P, bp, 7); MXGG_FENCE();
+    wait_barrier<8>();
     MXGG_FENCE();
-    // stage s+1 has landed and stage s is fully read: publish, refill slot s%2
-    wait_barrier<0>();
-    MXGG_FENCE();
-    after_barrier<SCALED>(st, P, Q, cur, kbeg + (s + 2) * kStageK, nxt, fa, f1, f0, acc);
+    mfma1<2, 0>(f1, acc); st.load_q(cur, Q, bq, 0); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
+    mfma1<2, 1>(f1, acc); st.load_q(cur, Q, bq, 1); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
+    mfma1<2, 2>(f1, acc); st.load_q(cur, Q, bq, 2); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
+    mfma1<2, 3>(f1, acc); st.load_q(cur, Q, bq, 3); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
+    mfma1<3, 0>(f1, acc); st.load_q(cur, Q, bq, 4); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
+    mfma1<3, 1>(f1, acc); st.load_q(cur, Q, bq, 5); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
+    mfma1<3, 2>(f1, acc); st.load_q(cur, Q, bq, 6); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
+    mfma1<3, 3>(f1, acc); st.load_q(cur, Q, bq, 7); MXGG_FENCE();
   }
   // Drain the loads past the end before the next tile's prologue reuses the slots.
   wait_barrier<0>();
