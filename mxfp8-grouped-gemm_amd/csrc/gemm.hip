@@ -339,17 +339,18 @@ __device__ __forceinline__ void release_barrier() {
 // A DMA instruction holds up its wave's issue until the address unit takes
 // it, so the 18 loads of a stage are spread one per MFMA.  Per stage, with the
 // MFMA count reached at each point:
-//    0  read P tail of k-step 0; MFMA rows 0-1 of f0, the first two carrying
-//       the scale loads of stage s+1
-//    8  read all of k-step 1 into f1; MFMA rows 2-3 of f0
-//   16  release barrier: every wave has read all of slot s%2 -> MFMA rows 0-1
-//       of f1, each followed by one P load of stage s+2 into that slot
-//   24  publish barrier: everything older than those 8 loads, i.e. all of
-//       stage s+1, has landed -> MFMA rows 2-3 of f1, each followed by one Q
-//       load of stage s+2, with the head of stage s+1's k-step 0 read into f0
-// so a load has at least 22 MFMAs of compute to land in.  The vmcnt of both
-// waits is the same (16 in the prologue, 8 in the loop) with or without
-// scales, because the scale loads are always the oldest of their group.
+//    0  MFMA rows 0-1 of f0 while the rest of stage s is read: the P tail of
+//       k-step 0 and all of k-step 1 into f1
+//    8  release barrier: every wave has read all of slot s%2 -> MFMA rows 2-3
+//       of f0 and rows 0-1 of f1, each followed by one data load of stage s+2
+//       into that slot (8 P, then 8 Q)
+//   24  publish barrier: everything older than those 16 loads, i.e. all of
+//       stage s+1, has landed -> MFMA rows 2-3 of f1 with the two scale loads
+//       of stage s+2 and the head of stage s+1's k-step 0 read into f0
+// so every load has at least 31 MFMAs of compute to land in.  The wait counts
+// do not depend on whether scales are loaded: the scale loads of a stage come
+// after its data loads, and the publish wait keeps exactly the 16 newest
+// (data) loads in flight.
 template <bool SCALED>
 __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Operand& Q,
                                          uint32_t klo, uint32_t kend, v16f (&acc)[4][4]) {
@@ -368,11 +369,13 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
   fa.init();
   // Prologue: all of stage 0 and the data of stage 1 (its scales follow in
   // the first stage), then publish stage 0.
-  st.issue_data(sm.ring[0], P, Q, kbeg);
   st.template load_scale<0>(sm.ring[0], P, kbeg);
   st.template load_scale<1>(sm.ring[0], Q, kbeg);
+  st.issue_data(sm.ring[0], P, Q, kbeg);
   st.issue_data(sm.ring[1], P, Q, kbeg + kStageK);
-  wait_barrier<16>();
+  st.template load_scale<0>(sm.ring[1], P, kbeg + kStageK);
+  st.template load_scale<1>(sm.ring[1], Q, kbeg + kStageK);
+  wait_barrier<SCALED ? 18 : 16>();
   MXGG_FENCE();
   Frags f0, f1;
   read_head<SCALED, 0>(sm.ring[0], fa, f0);
@@ -382,42 +385,50 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
   for (uint32_t s = 0; s < nst; ++s) {
     uint8_t* cur = sm.ring[s & 1u];
     uint8_t* nxt = sm.ring[(s & 1u) ^ 1u];
-    const uint32_t knext = kbeg + (s + 1) * kStageK;
     uint32_t bp, bq;
     st.stage_base(kbeg + (s + 2) * kStageK, bp, bq);
+    // MFMA 0-7: rows 0-1 of f0 while the rest of stage s is read (f0 tail, all of f1)
     read_tail<0>(cur, fa, f0);
     MXGG_FENCE();
-    mfma1<0, 0>(f0, acc); st.template load_scale<0>(nxt, P, knext); MXGG_FENCE();
-    mfma1<0, 1>(f0, acc); st.template load_scale<1>(nxt, Q, knext); MXGG_FENCE();
-    mfma1<0, 2>(f0, acc);
-    mfma1<0, 3>(f0, acc);
-    mfma_row<1>(f0, acc);
-    MXGG_FENCE();
-    read_head<SCALED, 1>(cur, fa, f1);
-    read_tail<1>(cur, fa, f1);
-    mfma_row<2>(f0, acc);
-    mfma_row<3>(f0, acc);
-    MXGG_FENCE();
+    mfma1<0, 0>(f0, acc); read_q<1>(cur, fa, f1, 0); MXGG_FENCE();
+    mfma1<0, 1>(f0, acc); read_q<1>(cur, fa, f1, 1); MXGG_FENCE();
+    mfma1<0, 2>(f0, acc); read_q<1>(cur, fa, f1, 2); MXGG_FENCE();
+    mfma1<0, 3>(f0, acc); read_q<1>(cur, fa, f1, 3); MXGG_FENCE();
+    mfma1<1, 0>(f0, acc); read_p<1>(cur, fa, f1, 0); MXGG_FENCE();
+    mfma1<1, 1>(f0, acc); read_p<1>(cur, fa, f1, 1); MXGG_FENCE();
+    mfma1<1, 2>(f0, acc); read_p<1>(cur, fa, f1, 2); MXGG_FENCE();
+    mfma1<1, 3>(f0, acc); read_p<1>(cur, fa, f1, 3); read_scales<SCALED, 1>(cur, fa, f1); MXGG_FENCE();
     release_barrier();
     MXGG_FENCE();
-    mfma1<0, 0>(f1, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
-    mfma1<0, 1>(f1, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
-    mfma1<0, 2>(f1, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
-    mfma1<0, 3>(f1, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
-    mfma1<1, 0>(f1, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
-    mfma1<1, 1>(f1, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
-    mfma1<1, 2>(f1, acc); st.load_p(cur, P, bp, 6); MXGG_FENCE();
-    mfma1<1, 3>(f1, acc); st.load_p(cur, P, bp, 7); MXGG_FENCE();
-    wait_barrier<8>();
+    // MFMA 8-23: rows 2-3 of f0 and 0-1 of f1, each followed by one load of stage s+2
+    mfma1<2, 0>(f0, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
+    mfma1<2, 1>(f0, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
+    mfma1<2, 2>(f0, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
+    mfma1<2, 3>(f0, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
+    mfma1<3, 0>(f0, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
+    mfma1<3, 1>(f0, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
+    mfma1<3, 2>(f0, acc); st.load_p(cur, P, bp, 6); MXGG_FENCE();
+    mfma1<3, 3>(f0, acc); st.load_p(cur, P, bp, 7); MXGG_FENCE();
+    mfma1<0, 0>(f1, acc); st.load_q(cur, Q, bq, 0); MXGG_FENCE();
+    mfma1<0, 1>(f1, acc); st.load_q(cur, Q, bq, 1); MXGG_FENCE();
+    mfma1<0, 2>(f1, acc); st.load_q(cur, Q, bq, 2); MXGG_FENCE();
+    mfma1<0, 3>(f1, acc); st.load_q(cur, Q, bq, 3); MXGG_FENCE();
+    mfma1<1, 0>(f1, acc); st.load_q(cur, Q, bq, 4); MXGG_FENCE();
+    mfma1<1, 1>(f1, acc); st.load_q(cur, Q, bq, 5); MXGG_FENCE();
+    mfma1<1, 2>(f1, acc); st.load_q(cur, Q, bq, 6); MXGG_FENCE();
+    mfma1<1, 3>(f1, acc); st.load_q(cur, Q, bq, 7); MXGG_FENCE();
+    // MFMA 24-31: stage s+1 published (all but the 16 newest loads have landed);
+    // rows 2-3 of f1, the scale loads of stage s+2, the head of stage s+1 into f0
+    wait_barrier<16>();
     MXGG_FENCE();
-    mfma1<2, 0>(f1, acc); st.load_q(cur, Q, bq, 0); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
-    mfma1<2, 1>(f1, acc); st.load_q(cur, Q, bq, 1); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
-    mfma1<2, 2>(f1, acc); st.load_q(cur, Q, bq, 2); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
-    mfma1<2, 3>(f1, acc); st.load_q(cur, Q, bq, 3); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
-    mfma1<3, 0>(f1, acc); st.load_q(cur, Q, bq, 4); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
-    mfma1<3, 1>(f1, acc); st.load_q(cur, Q, bq, 5); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
-    mfma1<3, 2>(f1, acc); st.load_q(cur, Q, bq, 6); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
-    mfma1<3, 3>(f1, acc); st.load_q(cur, Q, bq, 7); MXGG_FENCE();
+    mfma1<2, 0>(f1, acc); st.template load_scale<0>(cur, P, kbeg + (s + 2) * kStageK); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
+    mfma1<2, 1>(f1, acc); st.template load_scale<1>(cur, Q, kbeg + (s + 2) * kStageK); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
+    mfma1<2, 2>(f1, acc); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
+    mfma1<2, 3>(f1, acc); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
+    mfma1<3, 0>(f1, acc); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
+    mfma1<3, 1>(f1, acc); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
+    mfma1<3, 2>(f1, acc); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
+    mfma1<3, 3>(f1, acc); MXGG_FENCE();
   }
   // Drain the loads past the end before the next tile's prologue reuses the slots.
   wait_barrier<0>();
