@@ -482,27 +482,40 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
       }
     }
     // This wave's LDS writes complete before its reads (in-order LDS queue).
-#pragma unroll 4
-    for (uint32_t t = 0; t < 32u; ++t) {
-      const uint32_t s = 2u * t + h;
-      const float4 v =
-          *reinterpret_cast<const float4*>(stage + s * 512u + ((l32 ^ (t & 15u)) << 4));
-      const uint32_t q = q0 + wq * 128u + 4u * t + 2u * (uint32_t)pass + h;
-      if (q < qbeg || q >= qend || p >= pend) continue;
-      char* dst = out + (int64_t)q * ldo_bytes + (int64_t)p * (F32 ? 4 : 2);
-      if (p + 4u <= pend) {
-        if (F32)
-          *reinterpret_cast<float4*>(dst) = v;
-        else
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
-      } else {
-        const float w[4] = {v.x, v.y, v.z, v.w};
-        for (uint32_t u = 0; p + u < pend; ++u) {
-          if (F32) {
-            reinterpret_cast<float*>(dst)[u] = w[u];
-          } else {
-            const __bf16 b = (__bf16)w[u];
-            reinterpret_cast<uint16_t*>(dst)[u] = *reinterpret_cast<const uint16_t*>(&b);
+    // Reads go out eight at a time, unconditionally (they are always in
+    // bounds), so their latency overlaps; only the global stores are guarded.
+#pragma unroll
+    for (uint32_t t0 = 0; t0 < 32u; t0 += 8u) {
+      v4f v[8];
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) {
+        const uint32_t t = t0 + u;
+        v[u] = *reinterpret_cast<const v4f*>(stage + (2u * t + h) * 512u +
+                                             ((l32 ^ (t & 15u)) << 4));
+      }
+      // keep the reads here instead of letting them sink into the guarded stores
+      asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                   "+v"(v[6]), "+v"(v[7]));
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u) {
+        const uint32_t q = q0 + wq * 128u + 4u * (t0 + u) + 2u * (uint32_t)pass + h;
+        if (q < qbeg || q >= qend || p >= pend) continue;
+        char* dst = out + (int64_t)q * ldo_bytes + (int64_t)p * (F32 ? 4 : 2);
+        if (p + 4u <= pend) {
+          if (F32)
+            *reinterpret_cast<v4f*>(dst) = v[u];
+          else
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(pack_bf16x2(v[u][0], v[u][1]), pack_bf16x2(v[u][2], v[u][3]));
+        } else {
+          const float w[4] = {v[u][0], v[u][1], v[u][2], v[u][3]};
+          for (uint32_t k = 0; p + k < pend; ++k) {
+            if (F32) {
+              reinterpret_cast<float*>(dst)[k] = w[k];
+            } else {
+              const __bf16 b = (__bf16)w[k];
+              reinterpret_cast<uint16_t*>(dst)[k] = *reinterpret_cast<const uint16_t*>(&b);
+            }
           }
         }
       }
