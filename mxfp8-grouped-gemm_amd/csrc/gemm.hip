@@ -400,34 +400,36 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
     mfma1<1, 3>(f0, acc); read_p<1>(cur, fa, f1, 3); read_scales<SCALED, 1>(cur, fa, f1); MXGG_FENCE();
     release_barrier();
     MXGG_FENCE();
-    // MFMA 8-23: rows 2-3 of f0 and 0-1 of f1, each followed by one load of stage s+2
+    // MFMA 8-31: the 18 loads of stage s+2, three on every four MFMAs
     mfma1<2, 0>(f0, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
     mfma1<2, 1>(f0, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
     mfma1<2, 2>(f0, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
-    mfma1<2, 3>(f0, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
-    mfma1<3, 0>(f0, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
-    mfma1<3, 1>(f0, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
-    mfma1<3, 2>(f0, acc); st.load_p(cur, P, bp, 6); MXGG_FENCE();
-    mfma1<3, 3>(f0, acc); st.load_p(cur, P, bp, 7); MXGG_FENCE();
-    mfma1<0, 0>(f1, acc); st.load_q(cur, Q, bq, 0); MXGG_FENCE();
-    mfma1<0, 1>(f1, acc); st.load_q(cur, Q, bq, 1); MXGG_FENCE();
-    mfma1<0, 2>(f1, acc); st.load_q(cur, Q, bq, 2); MXGG_FENCE();
-    mfma1<0, 3>(f1, acc); st.load_q(cur, Q, bq, 3); MXGG_FENCE();
-    mfma1<1, 0>(f1, acc); st.load_q(cur, Q, bq, 4); MXGG_FENCE();
-    mfma1<1, 1>(f1, acc); st.load_q(cur, Q, bq, 5); MXGG_FENCE();
-    mfma1<1, 2>(f1, acc); st.load_q(cur, Q, bq, 6); MXGG_FENCE();
-    mfma1<1, 3>(f1, acc); st.load_q(cur, Q, bq, 7); MXGG_FENCE();
-    // MFMA 24-31: stage s+1 published (all but the 16 newest loads have landed);
-    // rows 2-3 of f1, the scale loads of stage s+2, the head of stage s+1 into f0
-    wait_barrier<16>();
+    mfma1<2, 3>(f0, acc); MXGG_FENCE();
+    mfma1<3, 0>(f0, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
+    mfma1<3, 1>(f0, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
+    mfma1<3, 2>(f0, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
+    mfma1<3, 3>(f0, acc); MXGG_FENCE();
+    mfma1<0, 0>(f1, acc); st.load_p(cur, P, bp, 6); MXGG_FENCE();
+    mfma1<0, 1>(f1, acc); st.load_p(cur, P, bp, 7); MXGG_FENCE();
+    mfma1<0, 2>(f1, acc); st.load_q(cur, Q, bq, 0); MXGG_FENCE();
+    mfma1<0, 3>(f1, acc); MXGG_FENCE();
+    mfma1<1, 0>(f1, acc); st.load_q(cur, Q, bq, 1); MXGG_FENCE();
+    mfma1<1, 1>(f1, acc); st.load_q(cur, Q, bq, 2); MXGG_FENCE();
+    mfma1<1, 2>(f1, acc); st.load_q(cur, Q, bq, 3); MXGG_FENCE();
+    mfma1<1, 3>(f1, acc); MXGG_FENCE();
+    // MFMA 24-31: stage s+1 published (all but the 12 loads above have
+    // landed); the remaining 6 loads of stage s+2 and the head of stage s+1's
+    // k-step 0 into f0
+    wait_barrier<12>();
     MXGG_FENCE();
-    mfma1<2, 0>(f1, acc); st.template load_scale<0>(cur, P, kbeg + (s + 2) * kStageK); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
-    mfma1<2, 1>(f1, acc); st.template load_scale<1>(cur, Q, kbeg + (s + 2) * kStageK); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
-    mfma1<2, 2>(f1, acc); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
+    const uint32_t k2 = kbeg + (s + 2) * kStageK;
+    mfma1<2, 0>(f1, acc); st.load_q(cur, Q, bq, 4); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
+    mfma1<2, 1>(f1, acc); st.load_q(cur, Q, bq, 5); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
+    mfma1<2, 2>(f1, acc); st.load_q(cur, Q, bq, 6); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
     mfma1<2, 3>(f1, acc); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
-    mfma1<3, 0>(f1, acc); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
-    mfma1<3, 1>(f1, acc); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
-    mfma1<3, 2>(f1, acc); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
+    mfma1<3, 0>(f1, acc); st.load_q(cur, Q, bq, 7); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
+    mfma1<3, 1>(f1, acc); st.template load_scale<0>(cur, P, k2); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
+    mfma1<3, 2>(f1, acc); st.template load_scale<1>(cur, Q, k2); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
     mfma1<3, 3>(f1, acc); MXGG_FENCE();
   }
   // Drain the loads past the end before the next tile's prologue reuses the slots.
