@@ -13,7 +13,7 @@ forward, the C4 weight gradient (fp32 dW), the bf16->MXFP8 casts, and the
 reference's CPU path (dequantise + per-group fp32 matmul with torch on the
 host cores) on a bounded sample of C2.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|wgrad|copy|ref8]
 """
 import argparse
 import json
@@ -47,6 +47,43 @@ def time_launches(fn, steps, warmup, torch):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps  # ms per launch
+
+
+# The reference's published forward numbers on MI355X are geometric means over
+# these 8 equal-group DeepSeek-V3 shapes (fused_fwd.py:323-333): 1501 TFLOPS
+# with E8M0 scales, 1864 without.
+REF_GEOMEAN_SCALED = 1501.0
+REF_GEOMEAN_UNSCALED = 1864.0
+
+
+def ref_equal_shapes(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
+    """Scaled and unscaled forward TFLOPS on the reference's 8 equal-group shapes."""
+    import math
+    rows = []
+    gen = torch.Generator(device=dev).manual_seed(0)
+    for E, M, N, K in workloads.DSV3_EQUAL_SHAPES:
+        x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+        w = (torch.randn((E, N, K), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+        xq, xs = mxfp8gg.to_mxfp8_dim0(x)
+        wq, ws = mxfp8gg.to_mxfp8_dim0(w)
+        del x, w
+        ends = torch.arange(1, E + 1, dtype=torch.int32, device=dev) * (M // E)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        fl = 2 * M * N * K
+        ms_s = time_launches(lambda: mxfp8gg.grouped_mm(xq, wq, ends, xs, ws, out=out),
+                             steps, warmup, torch)
+        ms_u = time_launches(lambda: mxfp8gg.grouped_mm(xq, wq, ends, out=out), steps, warmup, torch)
+        rows.append({"E": E, "M": M, "N": N, "K": K, "scaled_tflops": round(fl / ms_s / 1e9, 1),
+                     "unscaled_tflops": round(fl / ms_u / 1e9, 1)})
+        del xq, xs, wq, ws, out
+    gs = math.exp(sum(math.log(r["scaled_tflops"]) for r in rows) / len(rows))
+    gu = math.exp(sum(math.log(r["unscaled_tflops"]) for r in rows) / len(rows))
+    return {"shapes": rows, "geomean_scaled_tflops": round(gs, 1),
+            "geomean_unscaled_tflops": round(gu, 1),
+            "reference_geomean_scaled": REF_GEOMEAN_SCALED,
+            "reference_geomean_unscaled": REF_GEOMEAN_UNSCALED,
+            "vs_reference_scaled": round(gs / REF_GEOMEAN_SCALED, 3),
+            "vs_reference_unscaled": round(gu / REF_GEOMEAN_UNSCALED, 3)}
 
 
 def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, budget_s=12.0):
@@ -90,9 +127,10 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8"], default="all",
                     help="fwd / wgrad: time only that GEMM (for profiler runs); copy: a plain "
-                         "1 GiB device-to-device copy, the reference for HBM byte counters")
+                         "1 GiB device-to-device copy, the reference for HBM byte counters; "
+                         "ref8: the reference's 8 equal-group shapes only")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the MXFP8 grouped GEMM shards by expert and "
@@ -108,6 +146,9 @@ def main():
     dev = torch.device("cuda:0")
     mxfp8gg.load_library()
 
+    if args.only == "ref8":
+        print(json.dumps(ref_equal_shapes(torch, mxfp8gg, workloads, dev)), flush=True)
+        return
     if args.only == "copy":
         nbytes = 1 << 30
         src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
@@ -200,6 +241,8 @@ def main():
                                   "frac_of_peak": round(f4 / ms4 / 1e9 / PEAK_MXFP8_TFLOPS, 4),
                                   "out": "fp32 [32, 4096, 7168]"}
         del go, gos, ia, ias, dw
+        log("reference's 8 equal-group shapes")
+        components["ref_equal_shapes"] = ref_equal_shapes(torch, mxfp8gg, workloads, dev)
 
     traffic = None
     tfile = ROOT / "profiles" / "traffic_grouped_fwd_c2.json"
