@@ -132,6 +132,8 @@ int mxgg_scales_to_block_major(const void* src, int64_t batch, int64_t rows, int
  *   a        : e4m3 [M, K], row stride lda
  *   a_scales : E8M0 BLOCK_MAJOR [K/32][ldas], ldas >= M       (or NULL)
  *   w        : e4m3 [E, N, K]: expert g at w + g*w_group_stride, row stride ldw
+ *              (experts may overlap or interleave: e.g. column blocks of one
+ *              transposed weight matrix, as for dX = dY . W)
  *   w_scales : E8M0 BLOCK_MAJOR, expert g at + g*ws_group_stride: [K/32][ldws],
  *              ldws >= N                                       (or NULL)
  *   Scale strides and bases are multiples of 4 bytes, and a block-major array

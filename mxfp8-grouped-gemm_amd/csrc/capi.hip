@@ -208,10 +208,10 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
     return set_error(MXGG_ERR_SHAPE,
                      "grouped_fwd: leading dimension smaller than the row (block-major scales: "
                      "ldas >= M, ldws >= N)");
-  if (E > 1 && w_group_stride < N * ldw)
-    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: w_group_stride smaller than one expert");
-  if (scaled && E > 1 && ws_group_stride < N)
-    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: ws_group_stride < N overlaps experts");
+  // Experts may overlap or interleave (they are only read): the transposed
+  // weights of dgrad hold expert e in columns [e*N, (e+1)*N) of one matrix.
+  if (E > 1 && (w_group_stride < 0 || (scaled && ws_group_stride < 0)))
+    return set_error(MXGG_ERR_SHAPE, "grouped_fwd: negative expert stride");
   if (scaled && ((reinterpret_cast<uintptr_t>(a_scales) | reinterpret_cast<uintptr_t>(w_scales)) %
                      4 != 0 ||
                  ldas % 4 != 0 || ldws % 4 != 0 || (E > 1 && ws_group_stride % 4 != 0)))

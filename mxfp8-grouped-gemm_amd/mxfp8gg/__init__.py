@@ -10,9 +10,11 @@ from .ops import (
     _best_config,
     fused_grouped_fwd,
     fwd_ge,
+    grouped_dgrad,
     grouped_mm,
     grouped_wgrad,
     padded_token_capacity,
+    quant_weight_for_dgrad,
     to_mxfp8_dim0,
     to_mxfp8_dim1,
     wgrad_fused,
@@ -31,7 +33,7 @@ from .torchao_compat import (
 __all__ = [
     "MxggError", "load_library",
     "to_mxfp8_dim0", "to_mxfp8_dim1", "padded_token_capacity",
-    "grouped_mm", "grouped_wgrad",
+    "grouped_mm", "grouped_wgrad", "grouped_dgrad", "quant_weight_for_dgrad",
     "fused_grouped_fwd", "fwd_ge", "wgrad_fused", "wgrad_prepare", "wgrad_kernel",
     "triton_to_mxfp8_dim0", "triton_to_mxfp8_dim1",
     "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",

@@ -452,3 +452,50 @@ def wgrad_kernel(data: dict, **kwargs):
     out_dtype = _split_kw(dict(kwargs))
     return grouped_wgrad(data["A"], data["B"], data["offs"], data["As"], data["Bs"],
                          out_dtype=out_dtype)
+
+
+# ---------------------------------------------------------------------------
+# data gradient  dX = dY . W  (MXFP8 blocks along N)
+# ---------------------------------------------------------------------------
+def quant_weight_for_dgrad(w: torch.Tensor, scaling_mode="rceil"):
+    """W [E, N, K] bf16 -> W_e^T quantised with 1x32 blocks along N, for dgrad.
+
+    Runs the token-axis cast on W viewed as [E*N, K] with one group per
+    expert, so expert e's transposed weights are columns [e*N, (e+1)*N) of a
+    [K, E*N] e4m3 matrix.  Returns (wt, wts): wt a strided e4m3 view
+    [E, K, N] and wts an E8M0 view [E, K, N/32] of block-major storage, both
+    ready for grouped_mm.  N must be a multiple of 32 (no block may straddle
+    two experts).  Weights change only at the optimizer step, so a trainer
+    computes this once per step for the whole backward pass.
+    """
+    _need_gpu(w, "w")
+    if w.dtype != torch.bfloat16 or w.dim() != 3:
+        raise TypeError("w must be a 3-D bfloat16 tensor [E, N, K]")
+    E, N, K = w.shape
+    if N % 32 != 0:
+        raise ValueError(f"N={N} must be a multiple of 32 for MXFP8 blocks along N")
+    ends = torch.arange(1, E + 1, dtype=torch.int32, device=w.device) * N
+    qt, st, _ = to_mxfp8_dim1(w.reshape(E * N, K), ends, scaling_mode)
+    wt = qt.as_strided((E, K, N), (N, qt.stride(0), 1))
+    # st[k, b] lives at buf[b, k]: strides (1, ld); expert e starts at block-row e*N/32
+    wts = st.as_strided((E, K, N // 32), ((N // 32) * st.stride(1), st.stride(0), st.stride(1)))
+    return wt, wts
+
+
+def grouped_dgrad(dy: torch.Tensor, w: torch.Tensor | tuple, offs: torch.Tensor,
+                  out_dtype: torch.dtype = torch.bfloat16, scaling_mode="rceil",
+                  out: torch.Tensor | None = None):
+    """dX[rows of g] = dY[rows of g] . W[g] with MXFP8 operands blocked along N.
+
+    dy: bf16 [M, N] (gradient of the layer output); w: bf16 [E, N, K] or the
+    (wt, wts) pair from quant_weight_for_dgrad; offs: token group ends as for
+    grouped_mm.  dY is cast along N (dim0), W_e^T along N, and the product
+    runs on the forward grouped GEMM (contraction over N).  Returns [M, K].
+    (The reference computes this step in bf16 per expert, e2e_bench.py:91-108.)
+    """
+    _need_gpu(dy, "dy")
+    if dy.dtype != torch.bfloat16 or dy.dim() != 2:
+        raise TypeError("dy must be a 2-D bfloat16 tensor [M, N]")
+    wt, wts = w if isinstance(w, tuple) else quant_weight_for_dgrad(w, scaling_mode)
+    dyq, dys = to_mxfp8_dim0(dy, scaling_mode)
+    return grouped_mm(dyq, wt, offs, dys, wts, out_dtype=out_dtype, out=out)

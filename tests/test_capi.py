@@ -70,11 +70,13 @@ def _fwd(lib, **kw):
     (dict(out=FAKE + 2), _lib.ERR_ALIGNMENT),
     (dict(ends=FAKE, E=0), _lib.ERR_UNSUPPORTED),
     (dict(ends=FAKE, E=2000), _lib.ERR_UNSUPPORTED),
-    (dict(ends=FAKE, E=4, wg=100), _lib.ERR_SHAPE),    # expert stride too small
+    (dict(ends=FAKE, E=4, wg=-16), _lib.ERR_SHAPE),    # negative expert stride
+    (dict(ends=FAKE, E=4, wg=100), _lib.ERR_ALIGNMENT),  # expert stride not a multiple of 16
     (dict(a_s=FAKE, ldas=32, w_s=FAKE, ldws=512, wsg=512 * 8), _lib.ERR_SHAPE),  # ldas < M
     (dict(a_s=FAKE, ldas=66, w_s=FAKE, ldws=512, wsg=512 * 8), _lib.ERR_ALIGNMENT),
     (dict(a_s=FAKE + 2, ldas=64, w_s=FAKE, ldws=512, wsg=512 * 8), _lib.ERR_ALIGNMENT),
-    (dict(a_s=FAKE, ldas=64, w_s=FAKE, ldws=512, wsg=100, ends=FAKE, E=4), _lib.ERR_SHAPE),
+    (dict(a_s=FAKE, ldas=64, w_s=FAKE, ldws=512, wsg=-4, ends=FAKE, E=4), _lib.ERR_SHAPE),
+    (dict(a_s=FAKE, ldas=64, w_s=FAKE, ldws=512, wsg=102, ends=FAKE, E=4), _lib.ERR_ALIGNMENT),
 ])
 def test_grouped_fwd_rejects(lib, kw, status):
     assert _fwd(lib, **kw) == status
