@@ -13,7 +13,7 @@ forward, the C4 weight gradient (fp32 dW), the bf16->MXFP8 casts, and the
 reference's CPU path (dequantise + per-group fp32 matmul with torch on the
 host cores) on a bounded sample of C2.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|wgrad|copy|ref8]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|wgrad|copy|ref8|c5]
 """
 import argparse
 import json
@@ -86,6 +86,43 @@ def ref_equal_shapes(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
             "vs_reference_unscaled": round(gu / REF_GEOMEAN_UNSCALED, 3)}
 
 
+def layer_step_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
+    """one DSv3 expert-FFN layer step on one GPU --
+    131072 routed tokens, Zipf(1.0) over 32 experts, hidden 7168, intermediate
+    2048 -- forward (casts, gate+up, SiLU*up, down) and backward (dgrad and
+    wgrad of both projections with their casts) through mxfp8gg.moe_ffn.
+    TFLOPS counts the six GEMMs: 18 * tokens * 2048 * 7168 FLOP."""
+    sizes = workloads.c5_sizes()
+    M, H, F, E = int(sizes.sum()), 7168, 2048, 32
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((M, H), generator=gen, device=dev).to(torch.bfloat16).requires_grad_(True)
+    wgu = (torch.randn((E, 2 * F, H), generator=gen, device=dev) * 0.006).to(torch.bfloat16)
+    wd = (torch.randn((E, H, F), generator=gen, device=dev) * 0.006).to(torch.bfloat16)
+    wgu.requires_grad_(True)
+    wd.requires_grad_(True)
+    dy = (torch.randn((M, H), generator=gen, device=dev) * 1e-3).to(torch.bfloat16)
+    offs = torch.from_numpy(workloads.ends_of(sizes)).to(dev)
+
+    def step():
+        for t in (x, wgu, wd):
+            t.grad = None
+        mxfp8gg.moe_ffn(x, wgu, wd, offs).backward(dy)
+
+    def fwd():
+        with torch.no_grad():
+            mxfp8gg.moe_ffn(x, wgu, wd, offs)
+
+    ms = time_launches(step, steps, warmup, torch)
+    ms_f = time_launches(fwd, steps, warmup, torch)
+    flops = 18 * M * F * H
+    out = {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 1),
+           "frac_of_peak": round(flops / ms / 1e9 / PEAK_MXFP8_TFLOPS, 4),
+           "fwd_ms": round(ms_f, 3), "fwd_tflops": round(flops / 3 / ms_f / 1e9, 1),
+           "tokens": M, "group_sizes_min_max": [int(sizes.min()), int(sizes.max())]}
+    del x, wgu, wd, dy
+    return out
+
+
 def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, budget_s=12.0):
     """The reference's CPU path on a bounded sample of the workload: whole
     experts of C2, in order, until `budget_s` of CPU work has run."""
@@ -127,10 +164,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8"], default="all",
+    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "c5"], default="all",
                     help="fwd / wgrad: time only that GEMM (for profiler runs); copy: a plain "
                          "1 GiB device-to-device copy, the reference for HBM byte counters; "
-                         "ref8: the reference's 8 equal-group shapes only")
+                         "ref8: the reference's 8 equal-group shapes only; c5: the full "
+                         "expert-FFN layer step only")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the MXFP8 grouped GEMM shards by expert and "
@@ -146,6 +184,9 @@ def main():
     dev = torch.device("cuda:0")
     mxfp8gg.load_library()
 
+    if args.only == "c5":
+        print(json.dumps(layer_step_c5(torch, mxfp8gg, workloads, dev)), flush=True)
+        return
     if args.only == "ref8":
         print(json.dumps(ref_equal_shapes(torch, mxfp8gg, workloads, dev)), flush=True)
         return
@@ -243,6 +284,8 @@ def main():
         del go, gos, ia, ias, dw
         log("reference's 8 equal-group shapes")
         components["ref_equal_shapes"] = ref_equal_shapes(torch, mxfp8gg, workloads, dev)
+        log("C5: expert-FFN layer step (forward + backward)")
+        components["layer_step_c5"] = layer_step_c5(torch, mxfp8gg, workloads, dev)
 
     traffic = None
     tfile = ROOT / "profiles" / "traffic_grouped_fwd_c2.json"

@@ -21,6 +21,7 @@ from .ops import (
     wgrad_kernel,
     wgrad_prepare,
 )
+from .autograd import MXFP8GroupedMM, moe_ffn, mxfp8_grouped_mm
 from .torchao_compat import (
     apply,
     triton_mxfp8_grouped_mm,
@@ -37,4 +38,5 @@ __all__ = [
     "fused_grouped_fwd", "fwd_ge", "wgrad_fused", "wgrad_prepare", "wgrad_kernel",
     "triton_to_mxfp8_dim0", "triton_to_mxfp8_dim1",
     "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",
+    "MXFP8GroupedMM", "mxfp8_grouped_mm", "moe_ffn",
 ]
