@@ -339,14 +339,14 @@ __device__ __forceinline__ void release_barrier() {
 // A DMA instruction holds up its wave's issue until the address unit takes
 // it, so the 18 loads of a stage are spread one per MFMA.  Per stage, with the
 // MFMA count reached at each point:
-//    0  MFMA rows 0-1 of f0 while the rest of stage s is read: the P tail of
-//       k-step 0 and all of k-step 1 into f1
+//    0  MFMA rows 0-1 of f0 while all of k-step 1 is read into f1
 //    8  release barrier: every wave has read all of slot s%2 -> MFMA rows 2-3
 //       of f0 and rows 0-1 of f1, each followed by one data load of stage s+2
 //       into that slot (8 P, then 8 Q)
 //   24  publish barrier: everything older than those 16 loads, i.e. all of
 //       stage s+1, has landed -> MFMA rows 2-3 of f1 with the two scale loads
-//       of stage s+2 and the head of stage s+1's k-step 0 read into f0
+//       of stage s+2 and all of stage s+1's k-step 0 read into f0 (18 reads
+//       in each of the two read phases)
 // so every load has at least 31 MFMAs of compute to land in.  The wait counts
 // do not depend on whether scales are loaded: the scale loads of a stage come
 // after its data loads, and the publish wait keeps exactly the 16 newest
@@ -379,6 +379,7 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
   MXGG_FENCE();
   Frags f0, f1;
   read_head<SCALED, 0>(sm.ring[0], fa, f0);
+  read_tail<0>(sm.ring[0], fa, f0);
   // Past the last stage the loads fetch zeros into a slot nobody reads again,
   // and the final head read fetches a stale slot that is never used, so the
   // loop body has no branches.
@@ -387,9 +388,7 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
     uint8_t* nxt = sm.ring[(s & 1u) ^ 1u];
     uint32_t bp, bq;
     st.stage_base(kbeg + (s + 2) * kStageK, bp, bq);
-    // MFMA 0-7: rows 0-1 of f0 while the rest of stage s is read (f0 tail, all of f1)
-    read_tail<0>(cur, fa, f0);
-    MXGG_FENCE();
+    // MFMA 0-7: rows 0-1 of f0 while k-step 1 of stage s is read into f1
     mfma1<0, 0>(f0, acc); read_q<1>(cur, fa, f1, 0); MXGG_FENCE();
     mfma1<0, 1>(f0, acc); read_q<1>(cur, fa, f1, 1); MXGG_FENCE();
     mfma1<0, 2>(f0, acc); read_q<1>(cur, fa, f1, 2); MXGG_FENCE();
@@ -429,8 +428,8 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
     mfma1<2, 3>(f1, acc); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
     mfma1<3, 0>(f1, acc); st.load_q(cur, Q, bq, 7); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
     mfma1<3, 1>(f1, acc); st.template load_scale<0>(cur, P, k2); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
-    mfma1<3, 2>(f1, acc); st.template load_scale<1>(cur, Q, k2); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
-    mfma1<3, 3>(f1, acc); MXGG_FENCE();
+    mfma1<3, 2>(f1, acc); st.template load_scale<1>(cur, Q, k2); read_p<0>(nxt, fa, f0, 2); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
+    mfma1<3, 3>(f1, acc); read_p<0>(nxt, fa, f0, 3); MXGG_FENCE();
   }
   // Drain the loads past the end before the next tile's prologue reuses the slots.
   wait_barrier<0>();
