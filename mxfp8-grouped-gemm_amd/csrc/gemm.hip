@@ -497,26 +497,45 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
       // keep the reads here instead of letting them sink into the guarded stores
       asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
                    "+v"(v[6]), "+v"(v[7]));
+      if constexpr (F32) {
 #pragma unroll
-      for (uint32_t u = 0; u < 8u; ++u) {
-        const uint32_t q = q0 + wq * 128u + 4u * (t0 + u) + 2u * (uint32_t)pass + h;
-        if (q < qbeg || q >= qend || p >= pend) continue;
-        char* dst = out + (int64_t)q * ldo_bytes + (int64_t)p * (F32 ? 4 : 2);
-        if (p + 4u <= pend) {
-          if (F32)
+        for (uint32_t u = 0; u < 8u; ++u) {
+          const uint32_t q = q0 + wq * 128u + 4u * (t0 + u) + 2u * (uint32_t)pass + h;
+          if (q < qbeg || q >= qend || p >= pend) continue;
+          float* dst = reinterpret_cast<float*>(out + (int64_t)q * ldo_bytes) + p;
+          if (p + 4u <= pend) {
             *reinterpret_cast<v4f*>(dst) = v[u];
-          else
-            *reinterpret_cast<uint2*>(dst) =
-                make_uint2(pack_bf16x2(v[u][0], v[u][1]), pack_bf16x2(v[u][2], v[u][3]));
-        } else {
-          const float w[4] = {v[u][0], v[u][1], v[u][2], v[u][3]};
-          for (uint32_t k = 0; p + k < pend; ++k) {
-            if (F32) {
-              reinterpret_cast<float*>(dst)[k] = w[k];
-            } else {
-              const __bf16 b = (__bf16)w[k];
-              reinterpret_cast<uint16_t*>(dst)[k] = *reinterpret_cast<const uint16_t*>(&b);
-            }
+          } else {
+            for (uint32_t k = 0; p + k < pend; ++k) dst[k] = v[u][k];
+          }
+        }
+      } else {
+        // bf16: 8 bytes per lane and row.  Lanes 2i and 2i+1 swap halves of two
+        // consecutive rows so that each holds 8 consecutive values of one row
+        // and stores 16 bytes: the even lane row t at columns p..p+7, the odd
+        // lane row t+1 at p-4..p+3.
+        const bool odd = (l32 & 1u) != 0;
+        const uint32_t pe = p0 + wp * 128u + 8u * (l32 >> 1);
+#pragma unroll
+        for (uint32_t u = 0; u < 8u; u += 2u) {
+          const uint2 a = make_uint2(pack_bf16x2(v[u][0], v[u][1]), pack_bf16x2(v[u][2], v[u][3]));
+          const uint2 b =
+              make_uint2(pack_bf16x2(v[u + 1][0], v[u + 1][1]), pack_bf16x2(v[u + 1][2], v[u + 1][3]));
+          const uint2 send = odd ? a : b;
+          const uint2 recv = make_uint2((uint32_t)__shfl_xor((int)send.x, 1),
+                                        (uint32_t)__shfl_xor((int)send.y, 1));
+          const uint4 row8 = odd ? make_uint4(recv.x, recv.y, b.x, b.y)
+                                 : make_uint4(a.x, a.y, recv.x, recv.y);
+          const uint32_t t = t0 + u + (odd ? 1u : 0u);
+          const uint32_t q = q0 + wq * 128u + 4u * t + 2u * (uint32_t)pass + h;
+          if (q < qbeg || q >= qend || pe >= pend) continue;
+          uint16_t* dst = reinterpret_cast<uint16_t*>(out + (int64_t)q * ldo_bytes) + pe;
+          if (pe + 8u <= pend && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+            *reinterpret_cast<uint4*>(dst) = row8;
+          } else {
+            const uint32_t w[4] = {row8.x, row8.y, row8.z, row8.w};
+            for (uint32_t k = 0; k < 8u && pe + k < pend; ++k)
+              dst[k] = (uint16_t)(w[k >> 1] >> (16u * (k & 1u)));
           }
         }
       }
