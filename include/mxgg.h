@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 2
+#define MXGG_ABI_VERSION 3
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -175,6 +175,12 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
  * go_t and ia_t are 16-byte aligned, ldgo and ldia multiples of 16 and at most
  * 2^23, each operand spans less than 2 GiB; strides that are multiples of 128
  * let every load fetch whole cache lines (the fast case).
+ *   split_tokens : 0, or split-K: every expert's tokens are cut into chunks
+ *                  of split_tokens (a positive multiple of 128) processed as
+ *                  separate work items whose partial sums are added to dw
+ *                  with fp32 atomics.  Requires out_dtype F32 and dw zeroed
+ *                  by the caller; empty experts are then left untouched.  For
+ *                  calls with fewer 256x256 output tiles than compute units.
  * Replaces wgrad_fused / wgrad_prepare + wgrad_kernel (wgrad_fused.py:34-112),
  * which restack operands per group and call the forward kernel.
  */
@@ -182,7 +188,7 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
                        const void* ia_t, int64_t ldia, const void* ia_scales_t, int64_t ldias,
                        const int32_t* group_ends, int64_t num_groups,
                        int64_t M, int64_t N, int64_t K,
-                       void* dw, int out_dtype, void* stream);
+                       void* dw, int out_dtype, int64_t split_tokens, void* stream);
 
 #ifdef __cplusplus
 }

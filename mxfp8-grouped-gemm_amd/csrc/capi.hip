@@ -261,7 +261,7 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
 int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, int64_t ldgos,
                        const void* ia_t, int64_t ldia, const void* ia_scales_t, int64_t ldias,
                        const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t N,
-                       int64_t K, void* dw, int out_dtype, void* stream) {
+                       int64_t K, void* dw, int out_dtype, int64_t split_tokens, void* stream) {
   if (out_dtype != MXGG_OUT_BF16 && out_dtype != MXGG_OUT_F32)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: unknown out_dtype %d", out_dtype);
   if (M < 0 || N < 0 || K < 0)
@@ -278,6 +278,13 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
   if (M % 32 != 0)
     return set_error(MXGG_ERR_SHAPE, "grouped_wgrad: token count M=%lld not a multiple of 32",
                      (long long)M);
+  if (split_tokens < 0 || split_tokens % 128 != 0 || split_tokens > INT32_MAX)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT,
+                     "grouped_wgrad: split_tokens=%lld must be 0 or a positive multiple of 128",
+                     (long long)split_tokens);
+  if (split_tokens > 0 && out_dtype != MXGG_OUT_F32)
+    return set_error(MXGG_ERR_UNSUPPORTED,
+                     "grouped_wgrad: split-K accumulates with fp32 atomics (out_dtype F32 only)");
   if (N == 0 || K == 0) return MXGG_OK;
   if (!dw) return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: null dw");
   if (M > 0 && (!go_t || !ia_t))
@@ -321,6 +328,7 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
   args.N = (int32_t)N;
   args.K = (int32_t)K;
   args.E = (int32_t)num_groups;
+  args.split = (int32_t)split_tokens;
   args.out_f32 = out_dtype == MXGG_OUT_F32;
   args.scaled = scaled;
   return check_launch(launch_grouped_wgrad(args, static_cast<hipStream_t>(stream)),

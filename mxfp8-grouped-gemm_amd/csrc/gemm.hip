@@ -52,6 +52,8 @@ struct __align__(16) Smem {
   int32_t sched[kMaxGroups + 1];
   int32_t order[kMaxGroups];
   int32_t scan_tmp[kThreads];
+  int32_t chunks[kMaxGroups];      // wgrad: split-K chunks of the expert of each rank
+  int32_t items[kMaxGroups + 1];   // wgrad: prefix of work items over ranks
 };
 
 // Raw 128-bit buffer descriptor (gfx9 layout: base, stride 0, num_records,
@@ -461,7 +463,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 template <bool F32>
 __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char* out,
                                          int64_t ldo_bytes, uint32_t q0, uint32_t qbeg,
-                                         uint32_t qend, uint32_t p0, uint32_t pend) {
+                                         uint32_t qend, uint32_t p0, uint32_t pend,
+                                         bool accumulate = false) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t wp = wave & 1u, wq = wave >> 1;
@@ -503,7 +506,11 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
           const uint32_t q = q0 + wq * 128u + 4u * (t0 + u) + 2u * (uint32_t)pass + h;
           if (q < qbeg || q >= qend || p >= pend) continue;
           float* dst = reinterpret_cast<float*>(out + (int64_t)q * ldo_bytes) + p;
-          if (p + 4u <= pend) {
+          if (accumulate) {
+            // split-K partial sum: vector fp32 atomics into the zeroed output
+            for (uint32_t k = 0; k < 4u && p + k < pend; ++k)
+              __hip_atomic_fetch_add(dst + k, v[u][k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          } else if (p + 4u <= pend) {
             *reinterpret_cast<v4f*>(dst) = v[u];
           } else {
             for (uint32_t k = 0; p + k < pend; ++k) dst[k] = v[u][k];
@@ -567,9 +574,9 @@ __device__ __forceinline__ uint32_t xcd_slice(uint32_t base) {
   return base + (blockIdx.x & 7u) * (g >> 3) + (blockIdx.x >> 3);
 }
 
-// Block-wide inclusive scan of per-group tile counts into sm.sched[1..E]
-// (sched[0] = 0).  Each thread owns 4 consecutive groups.
-__device__ void scan_tiles(Smem& sm, const int32_t* tiles_of /*LDS, E*/, int E) {
+// Block-wide inclusive scan of per-group counts into out[1..E] (out[0] = 0),
+// both arrays in LDS.  Each thread owns 4 consecutive groups.
+__device__ void scan_counts(Smem& sm, const int32_t* tiles_of, int32_t* out, int E) {
   const int t = threadIdx.x;
   int32_t loc[4];
   int32_t sum = 0;
@@ -592,9 +599,9 @@ __device__ void scan_tiles(Smem& sm, const int32_t* tiles_of /*LDS, E*/, int E) 
   for (int u = 0; u < 4; ++u) {
     const int g = 4 * t + u;
     run += loc[u];
-    if (g < E) sm.sched[g + 1] = run;
+    if (g < E) out[g + 1] = run;
   }
-  if (t == 0) sm.sched[0] = 0;
+  if (t == 0) out[0] = 0;
   __syncthreads();
 }
 
@@ -625,7 +632,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
     sm.order[g] = e > b ? (e - (b & ~3) + kTileQ - 1) / kTileQ : 0;
   }
   __syncthreads();
-  scan_tiles(sm, sm.order, E);
+  scan_counts(sm, sm.order, sm.sched, E);
   const uint32_t m_tiles = (uint32_t)sm.sched[E];
   const uint32_t n_tiles = ((uint32_t)args.N + kTileP - 1) / kTileP;
   const uint32_t total = m_tiles * n_tiles;
@@ -674,12 +681,17 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
 // ---------------------------------------------------------------------------
 // Wgrad: dw[g][n][k] = sum_{t in g} go[n][t] ia[k][t].  Experts are visited
 // largest-first so the longest contraction runs start in the first round.
+// With split-K (args.split > 0 tokens, fp32 output zeroed by the caller) an
+// expert's tokens are cut into chunks of args.split, every (chunk, tile) is
+// one work item, and the partial sums are added with fp32 atomics; empty
+// experts then produce no work (their zeros are already in place).
 // ---------------------------------------------------------------------------
 template <bool SCALED, bool F32>
 __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, uint32_t gm) {
   __shared__ Smem sm;
   const int E = args.E;
   const int32_t M = args.M;
+  const int32_t split = args.split;
   // sizes into sched[0..E-1], then rank experts by descending size (ties by index)
   for (int g = threadIdx.x; g < E; g += kThreads) {
     int32_t b, e;
@@ -687,6 +699,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
     sm.sched[g] = e - b;
   }
   __syncthreads();
+  const uint32_t n_tiles = ((uint32_t)args.N + kTileQ - 1) / kTileQ;  // Q = go rows (n)
+  const uint32_t k_tiles = ((uint32_t)args.K + kTileP - 1) / kTileP;  // P = ia rows (k)
+  const uint32_t per_expert = n_tiles * k_tiles;
   for (int g = threadIdx.x; g < E; g += kThreads) {
     const int32_t sg = sm.sched[g];
     int rank = 0;
@@ -695,23 +710,39 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
       rank += (sj > sg) || (sj == sg && j < g);
     }
     sm.order[rank] = g;
+    const int32_t c = split > 0 ? (sg + split - 1) / split : 1;
+    sm.chunks[rank] = c;
   }
   __syncthreads();
-
-  const uint32_t n_tiles = ((uint32_t)args.N + kTileQ - 1) / kTileQ;  // Q = go rows (n)
-  const uint32_t k_tiles = ((uint32_t)args.K + kTileP - 1) / kTileP;  // P = ia rows (k)
-  const uint32_t per_expert = n_tiles * k_tiles;
-  const uint32_t total = per_expert * (uint32_t)E;
+  // work items per rank -> prefix in sm.items (sched is free again: reuse it
+  // as the scan input)
+  for (int r = threadIdx.x; r < E; r += kThreads) sm.sched[r] = sm.chunks[r] * (int32_t)per_expert;
+  __syncthreads();
+  scan_counts(sm, sm.sched, sm.items, E);
+  const uint32_t total = (uint32_t)sm.items[E];
 
   for (uint32_t base = 0;; base += gridDim.x) {
     const uint32_t lid = xcd_slice(base);
     if (lid >= total) break;
-    const uint32_t rank = lid / per_expert;
+    // rank of item lid: last r with items[r] <= lid
+    int lo = 0, hi = E - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((uint32_t)sm.items[mid] <= lid) lo = mid; else hi = mid - 1;
+    }
+    const int rank = lo;
     const int g = sm.order[rank];
+    const uint32_t local = lid - (uint32_t)sm.items[rank];
+    const uint32_t chunk = local / per_expert;  // consecutive items share a token range
     uint32_t nt, kt;
-    band_decode(lid - rank * per_expert, n_tiles, k_tiles, gm, nt, kt);
+    band_decode(local - chunk * per_expert, n_tiles, k_tiles, gm, nt, kt);
     int32_t tb, te;
     group_range(args.group_ends, g, M, tb, te);
+    int32_t cb = tb, ce = te;
+    if (split > 0) {
+      cb = tb + (int32_t)chunk * split;
+      ce = min(te, cb + split);
+    }
     const uint32_t q0 = nt * kTileQ;
     const uint32_t p0 = kt * kTileP;
 
@@ -739,12 +770,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_nanf("");
     } else {
-      mainloop<SCALED>(sm, P, Q, (uint32_t)tb, (uint32_t)te, acc);
+      mainloop<SCALED>(sm, P, Q, (uint32_t)cb, (uint32_t)ce, acc);
     }
     char* out = reinterpret_cast<char*>(args.dw) +
                 (int64_t)g * args.N * args.K * (F32 ? 4 : 2);
     epilogue<F32>(sm, acc, out, (int64_t)args.K * (F32 ? 4 : 2), q0, 0u, (uint32_t)args.N, p0,
-                  (uint32_t)args.K);
+                  (uint32_t)args.K, F32 && split > 0);
   }
 }
 

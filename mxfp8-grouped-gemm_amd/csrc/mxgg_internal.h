@@ -66,6 +66,7 @@ struct WgradArgs {
   void* dw;            // [E, N, K]
   int64_t ldgo, ldgos, ldia, ldias;
   int32_t M, N, K, E;
+  int32_t split;       // tokens per split-K chunk (multiple of 128), 0 = whole groups
   int32_t out_f32;
   int32_t scaled;
 };

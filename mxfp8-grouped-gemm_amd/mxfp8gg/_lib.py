@@ -31,7 +31,7 @@ OUT_F32 = 1
 SCALES_ROW_MAJOR = 0
 SCALES_BLOCK_MAJOR = 1
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -57,7 +57,7 @@ SIGNATURES = {
     ),
     "mxgg_grouped_wgrad": (
         _I,
-        [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I, _P],
+        [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I, _I64, _P],
     ),
 }
 

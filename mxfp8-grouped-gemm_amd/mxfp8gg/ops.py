@@ -342,9 +342,34 @@ def fwd_ge(x_fp8, w_fp8, BLOCK_M=256, BLOCK_N=256, BLOCK_K=128, NUM_WARPS=4, GRO
 # ---------------------------------------------------------------------------
 # wgrad grouped GEMM
 # ---------------------------------------------------------------------------
+def _cu_count(device) -> int:
+    return torch.cuda.get_device_properties(device).multi_processor_count
+
+
+def wgrad_split_tokens(M: int, N: int, K: int, E: int, cus: int) -> int:
+    """Split-K chunk (tokens) for a weight-gradient call, from shapes only.
+
+    The partial sums of a split are added with fp32 atomics, which move about
+    0.5 TB/s, so splitting pays only when most compute units would otherwise
+    idle: with at most cus/4 output tiles (E * ceil(N/256) * ceil(K/256)), the
+    tokens are cut into at most cus/tiles (<= 8) chunks of at least 4096
+    tokens (one round of work items), assuming the M tokens spread evenly over
+    the experts (group sizes live on the device and are not read back).
+    Returns 0 for no split."""
+    tiles = E * ((N + 255) // 256) * ((K + 255) // 256)
+    if tiles == 0 or M == 0 or 4 * tiles > cus:
+        return 0
+    per_expert = max(1, M // max(E, 1))
+    splits = min(8, cus // tiles)
+    chunk = max(4096, (per_expert + splits - 1) // splits)
+    chunk = (chunk + 127) // 128 * 128
+    return 0 if chunk >= per_expert else chunk
+
+
 def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
                   go_scales: torch.Tensor | None = None, ia_scales: torch.Tensor | None = None,
-                  out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None):
+                  out_dtype: torch.dtype = torch.float32, out: torch.Tensor | None = None,
+                  split_tokens: int | None = None):
     """dW[g] = dequant(go[:, tok of g]) @ dequant(ia[:, tok of g])^T  -> [E, N, K].
 
     go: e4m3 [N, M] (dY transposed, token-contiguous); ia: e4m3 [K, M]
@@ -352,6 +377,10 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
     [N, M/32] / [K, M/32] along tokens, both or neither.  With scales every
     group end must be a multiple of 32 (the layout to_mxfp8_dim1 produces).
     Empty groups yield zeros.
+    split_tokens: split-K chunk in tokens (multiple of 128), 0 for none, None
+    to choose from the shapes (wgrad_split_tokens) for fp32 output.  Split-K
+    adds fp32 partial sums atomically into a zeroed output, so the result can
+    differ from the unsplit one in the last bits (summation order).
     """
     _need_gpu(go, "go")
     _need_gpu(ia, "ia")
@@ -371,10 +400,16 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
         si, ldis = _scales_2d(ia_scales, K, M // 32, "ia_scales")
     E = offs.numel()
     ends = _group_ends(offs, E, go.device)
+    if split_tokens is None:
+        split_tokens = (wgrad_split_tokens(M, N, K, E, _cu_count(go.device))
+                        if out_dtype == torch.float32 else 0)
     if out is None:
-        out = torch.empty((E, N, K), dtype=out_dtype, device=go.device)
+        alloc = torch.zeros if split_tokens else torch.empty
+        out = alloc((E, N, K), dtype=out_dtype, device=go.device)
     elif out.shape != (E, N, K) or out.dtype != out_dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous [E, N, K] tensor of out_dtype")
+    elif split_tokens:
+        out.zero_()
     lib = _lib.load()
     _lib.check(
         lib.mxgg_grouped_wgrad(
@@ -382,7 +417,8 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
             sg.data_ptr() if sg is not None else None, ldgs,
             i8.data_ptr(), i8.stride(0),
             si.data_ptr() if si is not None else None, ldis,
-            ends.data_ptr(), E, M, N, K, out.data_ptr(), _out_code(out_dtype), _stream_ptr(go),
+            ends.data_ptr(), E, M, N, K, out.data_ptr(), _out_code(out_dtype), int(split_tokens),
+            _stream_ptr(go),
         ),
         "grouped_wgrad",
     )

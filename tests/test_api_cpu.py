@@ -93,3 +93,16 @@ def test_apply_without_torchao_raises():
         pytest.skip("torchao importable here")
     with pytest.raises(ImportError):
         patch_kernels.apply()
+
+
+def test_wgrad_split_choice():
+    # enough tiles for every compute unit: no split
+    assert ops.wgrad_split_tokens(65536, 4096, 7168, 32, 256) == 0
+    # 128 tiles on 256 units: atomics would cost what the idle half saves
+    assert ops.wgrad_split_tokens(65536, 2048, 1024, 4, 256) == 0
+    # 2 experts x 4 x 4 tiles = 32 on 256 units: 8 chunks of 4096 tokens
+    assert ops.wgrad_split_tokens(65536, 1024, 1024, 2, 256) == 4096
+    # 1 expert x 8 x 8 tiles = 64: 4 chunks
+    assert ops.wgrad_split_tokens(32768, 2048, 2048, 1, 256) == 8192
+    # short groups are not split below 4096 tokens
+    assert ops.wgrad_split_tokens(4096, 256, 256, 2, 256) == 0

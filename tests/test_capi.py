@@ -89,11 +89,12 @@ def test_grouped_fwd_empty_is_noop(lib):
 
 def _wg(lib, **kw):
     args = dict(go=FAKE, ldgo=128, gs=None, ldgs=0, ia=FAKE, ldia=128, is_=None, ldis=0,
-                ends=FAKE, E=4, M=128, N=64, K=64, dw=FAKE, dt=_lib.OUT_F32)
+                ends=FAKE, E=4, M=128, N=64, K=64, dw=FAKE, dt=_lib.OUT_F32, split=0)
     args.update(kw)
     return lib.mxgg_grouped_wgrad(args["go"], args["ldgo"], args["gs"], args["ldgs"], args["ia"],
                                   args["ldia"], args["is_"], args["ldis"], args["ends"], args["E"],
-                                  args["M"], args["N"], args["K"], args["dw"], args["dt"], None)
+                                  args["M"], args["N"], args["K"], args["dw"], args["dt"],
+                                  args["split"], None)
 
 
 @pytest.mark.parametrize("kw,status", [
@@ -108,6 +109,9 @@ def _wg(lib, **kw):
     (dict(dt=3), _lib.ERR_INVALID_ARGUMENT),
     (dict(gs=FAKE, ldgs=32, is_=FAKE, ldis=64), _lib.ERR_SHAPE),     # ldgos < N
     (dict(gs=FAKE, ldgs=66, is_=FAKE, ldis=64), _lib.ERR_ALIGNMENT),
+    (dict(split=100), _lib.ERR_INVALID_ARGUMENT),      # split-K chunk % 128
+    (dict(split=-128), _lib.ERR_INVALID_ARGUMENT),
+    (dict(split=256, dt=_lib.OUT_BF16), _lib.ERR_UNSUPPORTED),  # atomics need fp32
 ])
 def test_grouped_wgrad_rejects(lib, kw, status):
     assert _wg(lib, **kw) == status

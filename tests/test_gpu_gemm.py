@@ -336,3 +336,53 @@ def test_wgrad_c4_sampled(gpu):
     # linearity in the scales: one more on every dY scale doubles dW exactly
     dw2 = ops.grouped_wgrad(go, ia, pad, gos + 1, ias, out_dtype=torch.float32)
     assert torch.equal(dw2, 2 * dw)
+
+
+@pytest.mark.parametrize("sizes,split", [([1024, 0, 2976, 96], 256), ([4096, 4096], 1024),
+                                         ([640, 32], 128)])
+def test_wgrad_split_k_matches_oracle(gpu, sizes, split):
+    M = sum(sizes)
+    N, K = 256, 320
+    go_q, go_s = _rand_q((N, M), gpu, 53)
+    ia_q, ia_s = _rand_q((K, M), gpu, 54)
+    ends = workloads.ends_of(sizes)
+    offs = torch.from_numpy(ends).to(gpu)
+    go8, ia8 = go_q.view(torch.float8_e4m3fn), ia_q.view(torch.float8_e4m3fn)
+    dw = ops.grouped_wgrad(go8, ia8, offs, go_s, ia_s, out_dtype=torch.float32, split_tokens=split)
+    ref = O.grouped_wgrad(u8(go_q), u8(go_s), u8(ia_q), u8(ia_s), ends)
+    whole = ops.grouped_wgrad(go8, ia8, offs, go_s, ia_s, out_dtype=torch.float32, split_tokens=0)
+    for g in range(len(sizes)):
+        if sizes[g] == 0:
+            assert torch.all(dw[g] == 0)
+        else:
+            assert_close_to_oracle(dw[g], ref[g])
+            # same sum in another order: fp32 rounding differences only
+            assert (dw[g] - whole[g]).abs().max() <= 2.0 ** -12 * whole[g].abs().max()
+
+
+def test_wgrad_split_k_chosen_for_few_tiles(gpu):
+    # 2 experts x 2 x 2 output tiles: far fewer than compute units, so the
+    # call splits the 16384 tokens of each expert on its own
+    sizes = [16384, 16384]
+    M, N, K = sum(sizes), 512, 512
+    assert ops.wgrad_split_tokens(M, N, K, 2, ops._cu_count(gpu)) > 0
+    go_q, go_s = _rand_q((N, M), gpu, 55)
+    ia_q, ia_s = _rand_q((K, M), gpu, 56)
+    ends = workloads.ends_of(sizes)
+    dw = ops.grouped_wgrad(go_q.view(torch.float8_e4m3fn), ia_q.view(torch.float8_e4m3fn),
+                           torch.from_numpy(ends).to(gpu), go_s, ia_s, out_dtype=torch.float32)
+    ref = O.grouped_wgrad(u8(go_q), u8(go_s), u8(ia_q), u8(ia_s), ends, n_rows=np.arange(0, N, 7),
+                          k_rows=np.arange(0, K, 5))
+    for g in range(2):
+        assert_close_to_oracle(dw[g][::7, ::5], ref[g])
+
+
+def test_wgrad_split_k_misaligned_group_is_nan(gpu):
+    sizes = [1000, 1048]  # first end not a multiple of 32: both experts are NaN
+    M = sum(sizes)
+    go_q, go_s = _rand_q((256, M), gpu, 57)
+    ia_q, ia_s = _rand_q((256, M), gpu, 58)
+    dw = ops.grouped_wgrad(go_q.view(torch.float8_e4m3fn), ia_q.view(torch.float8_e4m3fn),
+                           torch.from_numpy(workloads.ends_of(sizes)).to(gpu), go_s, ia_s,
+                           out_dtype=torch.float32, split_tokens=256)
+    assert torch.isnan(dw).all()
