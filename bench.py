@@ -112,14 +112,37 @@ def layer_step_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
         with torch.no_grad():
             mxfp8gg.moe_ffn(x, wgu, wd, offs)
 
+    def step_unfused():
+        for t in (x, wgu, wd):
+            t.grad = None
+        mxfp8gg.moe_ffn_unfused(x, wgu, wd, offs).backward(dy)
+
     ms = time_launches(step, steps, warmup, torch)
     ms_f = time_launches(fwd, steps, warmup, torch)
+    ms_u = time_launches(step_unfused, steps, warmup, torch)
     flops = 18 * M * F * H
     out = {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 1),
            "frac_of_peak": round(flops / ms / 1e9 / PEAK_MXFP8_TFLOPS, 4),
            "fwd_ms": round(ms_f, 3), "fwd_tflops": round(flops / 3 / ms_f / 1e9, 1),
+           "unfused_activation_ms": round(ms_u, 3),
            "tokens": M, "group_sizes_min_max": [int(sizes.min()), int(sizes.max())]}
-    del x, wgu, wd, dy
+    for t in (x, wgu, wd):
+        t.grad = None
+    del wgu, wd
+    # the two SwiGLU kernels alone at this shape (HBM-bound; algorithmic bytes:
+    # forward reads h and writes a's cast, backward reads h and dA and writes
+    # three casts)
+    h = torch.randn((M, 2 * F), generator=gen, device=dev).to(torch.bfloat16)
+    da = (torch.randn((M, F), generator=gen, device=dev) * 0.05).to(torch.bfloat16)
+    cap = mxfp8gg.padded_token_capacity(M, E)
+    ms_sf = time_launches(lambda: mxfp8gg.swiglu_quant(h), 10, 3, torch)
+    ms_sb = time_launches(lambda: mxfp8gg.swiglu_backward_quant(h, da, offs), 10, 3, torch)
+    cast = 1 + 1 / 32
+    b_fwd = M * 2 * F * 2 + M * F * cast
+    b_bwd = M * 2 * F * 2 + M * F * 2 + M * 2 * F * cast + 3 * F * cap * cast
+    out["swiglu_fwd"] = {"ms": round(ms_sf, 4), "GBps": round(b_fwd / ms_sf / 1e6, 1)}
+    out["swiglu_bwd"] = {"ms": round(ms_sb, 4), "GBps": round(b_bwd / ms_sb / 1e6, 1)}
+    del x, dy, h, da
     return out
 
 

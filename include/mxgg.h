@@ -17,7 +17,7 @@
  * Groups ("experts") are described by `group_ends[num_groups]`, int32,
  * cumulative end offsets (group g covers [group_ends[g-1], group_ends[g]),
  * group 0 starts at 0) — the convention of torch._grouped_mm and of the
- * reference's callers (e2e_bench.py:245, wgrad_fused.py:64).  Empty groups are
+ * reference's callers (e2e_bench.py:42, wgrad_fused.py:64).  Empty groups are
  * allowed.  `group_ends` lives in device memory and is read only on the GPU.
  */
 #ifndef MXGG_H
@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 3
+#define MXGG_ABI_VERSION 4
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -83,7 +83,7 @@ const char* mxgg_last_error(void);
  * cols % 32 == 0.  Payload = RNE_e4m3(clamp(x * 2^(127-b), -448, 448)).
  * Replaces torchao's triton_to_mxfp8_dim0 (called by the reference's trainer
  * path, port_mxfp8.py:43-49) and the eager `.to(torch.float8_e4m3fn)` casts on
- * the forward path (e2e_bench.py:238-243, fused_fwd.py:274-275).
+ * the forward path (e2e_bench.py:35-40,60, fused_fwd.py:274-275).
  */
 int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx,
                     void* q, int64_t ldq, void* scales, int64_t lds, int scale_layout,
@@ -106,13 +106,59 @@ int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx,
  * Columns past the padded total are written as zero payload with the scale of an
  * all-zero block (byte 0).
  * Replaces torchao's triton_to_mxfp8_dim1 (port_mxfp8.py:43) plus the
- * transpose-and-stack copies of wgrad_fused.py:48-62 / e2e_bench.py:317-328.
+ * transpose-and-stack copies of wgrad_fused.py:48-62 / e2e_bench.py:114-126.
  */
 int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
                     const int32_t* group_ends, int64_t num_groups,
                     int64_t rows_pad_cap, void* qt, int64_t ldqt,
                     void* scales_t, int64_t ldst, int scale_layout,
                     int32_t* group_ends_pad, int scale_mode, void* stream);
+
+/*
+ * SwiGLU activation fused with the row-wise MXFP8 cast of its output:
+ *   a = bf16(bf16(silu(gate)) * up),  silu(g) = g / (1 + exp(-g)) in fp32
+ * (torch's eager bf16 result of F.silu(gate) * up).
+ *   gate, up : bf16 [rows, cols], common row stride ldh (e.g. the two column
+ *              halves of the gate+up projection output h = [gate | up])
+ *   q, scales: the cast of a, as mxgg_quant_dim0 writes it
+ *   a_out    : optional bf16 [rows, cols] copy of a (row stride lda), or NULL
+ * cols % 32 == 0.  Replaces the eager `silu(hg) * hu` and `.to(float8)` of the
+ * reference's layer step (e2e_bench.py:56-61).
+ */
+int mxgg_swiglu_quant_dim0(const void* gate, const void* up, int64_t ldh, int64_t rows,
+                           int64_t cols, void* a_out, int64_t lda, void* q, int64_t ldq,
+                           void* scales, int64_t lds, int scale_layout, int scale_mode,
+                           void* stream);
+
+/*
+ * SwiGLU backward fused with the three casts the backward GEMMs consume.
+ * From gate, up (bf16 [rows, cols], stride ldh) and grad_a = dL/da (bf16
+ * [rows, cols], stride ldga), with s = bf16(silu(gate)), sig = sigmoid(gate):
+ *   d_up   = bf16(grad_a * s)
+ *   d_gate = bf16(bf16(grad_a * up) * sig * (1 + gate * (1 - sig)))
+ *   a      = bf16(s * up)
+ * (torch's eager bf16 autograd of F.silu(gate) * up), and writes
+ *   dh_q, dh_scales      : row-wise cast of dh = [d_gate | d_up], [rows, 2*cols]
+ *                          (as mxgg_quant_dim0) — the dX operand
+ *   dh_qt, dh_scales_t   : token-axis cast of dh, transposed, [2*cols, rows_pad_cap]
+ *                          (as mxgg_quant_dim1) — the dW_gate_up operand
+ *   a_qt, a_scales_t     : token-axis cast of a, transposed, [cols, rows_pad_cap]
+ *                          — the dW_down operand
+ *   group_ends_pad       : padded group ends (as mxgg_quant_dim1)
+ *   dh_out               : optional bf16 dh [rows, 2*cols] (stride lddh), or NULL
+ * group_ends / num_groups / rows_pad_cap as for mxgg_quant_dim1.  Rows past the
+ * last group end get no row-wise output.  scale_layout applies to all three
+ * scale outputs.  cols % 32 == 0.  Replaces the reference's eager SiLU
+ * backward (e2e_bench.py:85-100) and the casts of its wgrad operands
+ * (e2e_bench.py:114-126).
+ */
+int mxgg_swiglu_bwd_quant(const void* gate, const void* up, int64_t ldh, const void* grad_a,
+                          int64_t ldga, int64_t rows, int64_t cols, const int32_t* group_ends,
+                          int64_t num_groups, int64_t rows_pad_cap, void* dh_q, int64_t lddq,
+                          void* dh_scales, int64_t ldds, void* dh_qt, int64_t lddqt,
+                          void* dh_scales_t, int64_t lddst, void* a_qt, int64_t ldaqt,
+                          void* a_scales_t, int64_t ldast, int32_t* group_ends_pad, void* dh_out,
+                          int64_t lddh, int scale_layout, int scale_mode, void* stream);
 
 /*
  * Re-lay E8M0 scales from ROW_MAJOR to BLOCK_MAJOR, batched:

@@ -162,6 +162,133 @@ int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
       "quant_dim1");
 }
 
+int mxgg_swiglu_quant_dim0(const void* gate, const void* up, int64_t ldh, int64_t rows,
+                           int64_t cols, void* a_out, int64_t lda, void* q, int64_t ldq,
+                           void* scales, int64_t lds, int scale_layout, int scale_mode,
+                           void* stream) {
+  const int mode = scale_mode & 0xFF;
+  if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "swiglu_quant_dim0: unknown scale_mode %d",
+                     scale_mode);
+  if (!valid_layout(scale_layout))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "swiglu_quant_dim0: unknown scale_layout %d",
+                     scale_layout);
+  if (rows < 0 || cols < 0)
+    return set_error(MXGG_ERR_SHAPE, "swiglu_quant_dim0: negative size");
+  if (cols % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "swiglu_quant_dim0: cols=%lld is not a multiple of 32",
+                     (long long)cols);
+  if (rows == 0 || cols == 0) return MXGG_OK;
+  if (!gate || !up || !q || !scales)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "swiglu_quant_dim0: null pointer");
+  if (ldh < cols || ldq < cols || (a_out && lda < cols) ||
+      lds < (scale_layout == MXGG_SCALES_BLOCK_MAJOR ? rows : cols / 32))
+    return set_error(MXGG_ERR_SHAPE, "swiglu_quant_dim0: leading dimension smaller than the row");
+  if (!aligned16(gate) || !aligned16(up) || ldh % 8 != 0 || ldq % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(q) & 7u) != 0 || (a_out && (!aligned16(a_out) || lda % 8 != 0)))
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "swiglu_quant_dim0: gate, up and a_out 16-byte aligned with strides multiples "
+                     "of 8; q 8-byte aligned with ldq %% 8 == 0");
+  return check_launch(
+      launch_swiglu_quant_dim0(static_cast<const uint16_t*>(gate), static_cast<const uint16_t*>(up),
+                               ldh, rows, cols, static_cast<uint16_t*>(a_out), lda,
+                               static_cast<uint8_t*>(q), ldq, static_cast<uint8_t*>(scales), lds,
+                               scale_layout, scale_mode, static_cast<hipStream_t>(stream)),
+      "swiglu_quant_dim0");
+}
+
+int mxgg_swiglu_bwd_quant(const void* gate, const void* up, int64_t ldh, const void* grad_a,
+                          int64_t ldga, int64_t rows, int64_t cols, const int32_t* group_ends,
+                          int64_t num_groups, int64_t rows_pad_cap, void* dh_q, int64_t lddq,
+                          void* dh_scales, int64_t ldds, void* dh_qt, int64_t lddqt,
+                          void* dh_scales_t, int64_t lddst, void* a_qt, int64_t ldaqt,
+                          void* a_scales_t, int64_t ldast, int32_t* group_ends_pad, void* dh_out,
+                          int64_t lddh, int scale_layout, int scale_mode, void* stream) {
+  const int mode = scale_mode & 0xFF;
+  if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "swiglu_bwd_quant: unknown scale_mode %d",
+                     scale_mode);
+  if (!valid_layout(scale_layout))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "swiglu_bwd_quant: unknown scale_layout %d",
+                     scale_layout);
+  if (rows < 0 || cols < 0 || rows_pad_cap < 0)
+    return set_error(MXGG_ERR_SHAPE, "swiglu_bwd_quant: negative size");
+  if (cols % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "swiglu_bwd_quant: cols=%lld is not a multiple of 32",
+                     (long long)cols);
+  if (rows_pad_cap % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "swiglu_bwd_quant: rows_pad_cap=%lld not a multiple of 32",
+                     (long long)rows_pad_cap);
+  if (group_ends) {
+    if (num_groups < 1 || num_groups > kMaxGroupsAbi)
+      return set_error(MXGG_ERR_UNSUPPORTED,
+                       "swiglu_bwd_quant: num_groups=%lld outside [1, %lld]",
+                       (long long)num_groups, (long long)kMaxGroupsAbi);
+    if (!group_ends_pad)
+      return set_error(MXGG_ERR_INVALID_ARGUMENT,
+                       "swiglu_bwd_quant: group_ends_pad is required with group_ends");
+  }
+  const int64_t need = ((rows + 31 * (group_ends ? num_groups : 0) + 31) / 32) * 32;
+  if (rows_pad_cap < need)
+    return set_error(MXGG_ERR_SHAPE, "swiglu_bwd_quant: rows_pad_cap=%lld < required %lld",
+                     (long long)rows_pad_cap, (long long)need);
+  if (cols == 0 || rows_pad_cap == 0) return MXGG_OK;
+  if (rows > 0 && (!gate || !up || !grad_a || !dh_q || !dh_scales))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "swiglu_bwd_quant: null input or dh_q");
+  if (!dh_qt || !dh_scales_t || !a_qt || !a_scales_t)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "swiglu_bwd_quant: null token-axis output");
+  const bool bm = scale_layout == MXGG_SCALES_BLOCK_MAJOR;
+  if (ldh < cols || ldga < cols || lddq < 2 * cols || (dh_out && lddh < 2 * cols) ||
+      ldds < (bm ? rows : 2 * cols / 32) || lddqt < rows_pad_cap || ldaqt < rows_pad_cap ||
+      lddst < (bm ? 2 * cols : rows_pad_cap / 32) || ldast < (bm ? cols : rows_pad_cap / 32))
+    return set_error(MXGG_ERR_SHAPE, "swiglu_bwd_quant: leading dimension smaller than the row");
+  const uintptr_t in_bits = reinterpret_cast<uintptr_t>(gate) |
+                            reinterpret_cast<uintptr_t>(up) | reinterpret_cast<uintptr_t>(grad_a);
+  if ((in_bits & 15u) != 0 || ldh % 8 != 0 || ldga % 8 != 0 ||
+      (dh_out && (!aligned16(dh_out) || lddh % 8 != 0)))
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "swiglu_bwd_quant: gate, up, grad_a and dh_out 16-byte aligned with strides "
+                     "multiples of 8");
+  if ((reinterpret_cast<uintptr_t>(dh_q) & 7u) != 0 || lddq % 8 != 0 || !aligned16(dh_qt) ||
+      !aligned16(a_qt) || lddqt % 16 != 0 || ldaqt % 16 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "swiglu_bwd_quant: dh_q 8-byte aligned with lddq %% 8 == 0; dh_qt and a_qt "
+                     "16-byte aligned with strides multiples of 16");
+  if (rows > INT32_MAX || rows_pad_cap > INT32_MAX || cols > 64 * INT64_C(65535))
+    return set_error(MXGG_ERR_UNSUPPORTED,
+                     "swiglu_bwd_quant: rows or rows_pad_cap above 2^31, or cols above 4194240");
+  SwigluBwdLaunch l;
+  l.gate = static_cast<const uint16_t*>(gate);
+  l.up = static_cast<const uint16_t*>(up);
+  l.da = static_cast<const uint16_t*>(grad_a);
+  l.group_ends = group_ends;
+  l.group_ends_pad = group_ends_pad;
+  l.dq = static_cast<uint8_t*>(dh_q);
+  l.ds = static_cast<uint8_t*>(dh_scales);
+  l.dqt = static_cast<uint8_t*>(dh_qt);
+  l.dst = static_cast<uint8_t*>(dh_scales_t);
+  l.aqt = static_cast<uint8_t*>(a_qt);
+  l.ast = static_cast<uint8_t*>(a_scales_t);
+  l.dh = static_cast<uint16_t*>(dh_out);
+  l.ldh = ldh;
+  l.ldda = ldga;
+  l.rows = rows;
+  l.cols = cols;
+  l.num_groups = group_ends ? num_groups : 1;
+  l.cap = rows_pad_cap;
+  l.lddq = lddq;
+  l.ldds = ldds;
+  l.lddqt = lddqt;
+  l.lddst = lddst;
+  l.ldaqt = ldaqt;
+  l.ldast = ldast;
+  l.lddh = lddh;
+  l.layout = scale_layout;
+  l.mode = scale_mode;
+  return check_launch(launch_swiglu_bwd_quant(l, static_cast<hipStream_t>(stream)),
+                      "swiglu_bwd_quant");
+}
+
 int mxgg_scales_to_block_major(const void* src, int64_t batch, int64_t rows, int64_t nblk,
                                int64_t src_bstride, int64_t lds, void* dst,
                                int64_t dst_bstride, int64_t ldd, void* stream) {

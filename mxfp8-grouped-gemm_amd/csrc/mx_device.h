@@ -19,6 +19,9 @@ namespace mxgg {
 
 enum { kModeRceil = 0, kModeFloor = 1 };
 
+// Largest group table a token-axis cast stages in LDS (the ABI's expert limit).
+constexpr int kMaxGroups = 1024;
+
 // amax16 = max over the block of (bf16 bits & 0x7FFF).  For non-negative bf16
 // bit patterns integer order equals magnitude order and every NaN pattern
 // (> 0x7F80) sorts above +Inf, so an integer max propagates NaN.
@@ -99,25 +102,102 @@ __device__ __forceinline__ uint32_t e4m3_pack4(float a, float b, float c, float 
   return w;
 }
 
-// Quantise two bf16 packed in one 32-bit word with block byte b, giving
-// two payload floats ready for packing.
-template <int MODE>
-__device__ __forceinline__ void bf16x2_to_scaled(uint32_t w, uint32_t b, int e, float& lo,
-                                                 float& hi) {
-  const float x0 = bf16_bits_to_f32(w & 0xFFFFu);
-  const float x1 = bf16_bits_to_f32(w >> 16);
-  if (MODE == kModeFloor && b == 255u) {
-    lo = floor_nan_block_value(x0);
-    hi = floor_nan_block_value(x1);
-  } else {
-    lo = scale_and_clamp(x0, e);
-    hi = scale_and_clamp(x1, e);
-  }
-}
-
 __device__ __forceinline__ uint32_t amax16_of_word(uint32_t w) {
   const uint32_t lo = w & 0x7FFFu, hi = (w >> 16) & 0x7FFFu;
   return lo > hi ? lo : hi;
+}
+
+// amax16 of the eight bf16 values of a 16-byte chunk.
+__device__ __forceinline__ uint32_t amax16_of_chunk(const uint4& v) {
+  uint32_t am = amax16_of_word(v.x);
+  am = max(am, amax16_of_word(v.y));
+  am = max(am, amax16_of_word(v.z));
+  return max(am, amax16_of_word(v.w));
+}
+
+// Payload bytes of four values (bf16 values widened to float) of a block with
+// scale byte b.  b == 255 exactly when the block holds a NaN (both modes), so
+// every other block takes the short path: scale, clamp, convert.
+template <int MODE, bool SW>
+__device__ __forceinline__ uint32_t encode4(float x0, float x1, float x2, float x3, uint32_t b) {
+  if (b != 255u) {
+    const int e = payload_exponent<MODE>(b);
+    const float y0 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x0, e), -448.0f), 448.0f);
+    const float y1 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x1, e), -448.0f), 448.0f);
+    const float y2 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x2, e), -448.0f), 448.0f);
+    const float y3 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x3, e), -448.0f), 448.0f);
+    if (SW)
+      return e4m3_encode_sw(y0) | (e4m3_encode_sw(y1) << 8) | (e4m3_encode_sw(y2) << 16) |
+             (e4m3_encode_sw(y3) << 24);
+    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y2, y3, (int)w, true);
+  }
+  const int e = payload_exponent<MODE>(b);
+  float y[4] = {x0, x1, x2, x3};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    y[i] = MODE == kModeFloor ? floor_nan_block_value(y[i]) : scale_and_clamp(y[i], e);
+  return e4m3_pack4<SW>(y[0], y[1], y[2], y[3]);
+}
+
+// Two bf16 packed in a word, widened to float.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+// Payload bytes of the eight bf16 values of a chunk under block byte b.
+template <int MODE, bool SW>
+__device__ __forceinline__ uint2 encode_chunk8(const uint4& v, uint32_t b) {
+  return make_uint2(encode4<MODE, SW>(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y), b),
+                    encode4<MODE, SW>(bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w), b));
+}
+
+// Two floats rounded to bf16 (round to nearest even, v_cvt_pk_bf16_f32) and
+// packed into one word, `lo` in bits 0-15.  Finite and infinite values round as
+// torch's float -> bfloat16 conversion does; a NaN stays a NaN.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+}
+
+// Group tables of the token-axis casts, staged in LDS by every workgroup:
+//   ends_s[g] : end of group g clamped to [0, rows]
+//   pend_s[g] : padded cumulative end (every group rounded up to 32 tokens),
+//               as written by the padded-ends kernel
+// Callers synchronise the workgroup before reading the tables.
+__device__ __forceinline__ void stage_group_tables(const int32_t* __restrict__ ends,
+                                                   const int32_t* __restrict__ ends_pad, int E,
+                                                   int64_t rows, int32_t* ends_s,
+                                                   int32_t* pend_s) {
+  for (int g = threadIdx.x; g < E; g += blockDim.x) {
+    const int32_t e = ends[g];
+    ends_s[g] = e < 0 ? 0 : (e > rows ? (int32_t)rows : e);
+    pend_s[g] = ends_pad[g];
+  }
+}
+
+// Padded token position P, the first of a run of `run` positions (run divides
+// 32, P a multiple of run, so the run never straddles two groups), to the
+// first real token tok0 and the number of real tokens ntok in the run.
+// Positions past a group's real tokens and past the padded total map to none.
+__device__ __forceinline__ void padded_run_tokens(int64_t P, int run, const int32_t* ends_s,
+                                                  const int32_t* pend_s, int E, int64_t& tok0,
+                                                  int& ntok) {
+  tok0 = 0;
+  ntok = 0;
+  int lo = 0, hi = E;  // first group whose padded end is > P
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if ((int64_t)pend_s[mid] > P) hi = mid; else lo = mid + 1;
+  }
+  if (lo < E) {
+    const int64_t pstart = lo > 0 ? pend_s[lo - 1] : 0;
+    const int64_t gstart = lo > 0 ? ends_s[lo - 1] : 0;
+    const int64_t gend = ends_s[lo];
+    tok0 = gstart + (P - pstart);
+    const int64_t n = gend - tok0;  // negative when the clamped start exceeds the end
+    ntok = n <= 0 ? 0 : (n >= run ? run : (int)n);
+  }
 }
 
 }  // namespace mxgg

@@ -39,6 +39,35 @@ hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int6
                              int64_t ldst, int layout, int32_t* group_ends_pad, int mode,
                              hipStream_t stream);
 
+// Padded cumulative group ends of the token-axis casts (one workgroup).
+hipError_t launch_pad_ends(const int32_t* group_ends, int64_t num_groups, int64_t rows,
+                           int32_t* group_ends_pad, hipStream_t stream);
+
+// SwiGLU fused with its casts (swiglu.hip).
+hipError_t launch_swiglu_quant_dim0(const uint16_t* gate, const uint16_t* up, int64_t ldh,
+                                    int64_t rows, int64_t cols, uint16_t* a_out, int64_t lda,
+                                    uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int layout,
+                                    int mode, hipStream_t stream);
+
+struct SwigluBwdLaunch {
+  const uint16_t* gate;
+  const uint16_t* up;
+  const uint16_t* da;
+  const int32_t* group_ends;  // nullptr = one group
+  int32_t* group_ends_pad;
+  uint8_t* dq;   // row-wise cast of [d_gate | d_up]
+  uint8_t* ds;
+  uint8_t* dqt;  // token-axis cast of [d_gate | d_up]
+  uint8_t* dst;
+  uint8_t* aqt;  // token-axis cast of a
+  uint8_t* ast;
+  uint16_t* dh;  // optional bf16 [d_gate | d_up]
+  int64_t ldh, ldda, rows, cols, num_groups, cap;
+  int64_t lddq, ldds, lddqt, lddst, ldaqt, ldast, lddh;
+  int layout, mode;
+};
+hipError_t launch_swiglu_bwd_quant(const SwigluBwdLaunch& l, hipStream_t stream);
+
 hipError_t launch_scales_to_block_major(const uint8_t* src, int64_t batch, int64_t rows,
                                         int64_t nblk, int64_t sb, int64_t lds, uint8_t* dst,
                                         int64_t db, int64_t ldd, hipStream_t stream);

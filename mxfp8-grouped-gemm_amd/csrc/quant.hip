@@ -12,8 +12,6 @@
 namespace mxgg {
 namespace {
 
-constexpr int kMaxGroups = 1024;
-
 // ---------------------------------------------------------------------------
 // dim0.  A wave covers 64 chunks of 8 bf16 (16 B) of one row; the four lanes
 // of a quad hold one 32-element block and combine their amax with two xor
@@ -43,22 +41,11 @@ __global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int64_t r = r0 + u;
-      uint32_t am = amax16_of_word(v[u].x);
-      am = max(am, amax16_of_word(v[u].y));
-      am = max(am, amax16_of_word(v[u].z));
-      am = max(am, amax16_of_word(v[u].w));
+      uint32_t am = amax16_of_chunk(v[u]);
       am = max(am, (uint32_t)__shfl_xor((int)am, 1));
       am = max(am, (uint32_t)__shfl_xor((int)am, 2));
       const uint32_t b = e8m0_from_amax16<MODE>(am);
-      const int e = payload_exponent<MODE>(b);
-      float f[8];
-      bf16x2_to_scaled<MODE>(v[u].x, b, e, f[0], f[1]);
-      bf16x2_to_scaled<MODE>(v[u].y, b, e, f[2], f[3]);
-      bf16x2_to_scaled<MODE>(v[u].z, b, e, f[4], f[5]);
-      bf16x2_to_scaled<MODE>(v[u].w, b, e, f[6], f[7]);
-      uint2 o;
-      o.x = e4m3_pack4<SW>(f[0], f[1], f[2], f[3]);
-      o.y = e4m3_pack4<SW>(f[4], f[5], f[6], f[7]);
+      const uint2 o = encode_chunk8<MODE, SW>(v[u], b);
       if (col_ok && r < rows) {
         *reinterpret_cast<uint2*>(q + r * ldq + (int64_t)cc * 8) = o;
         if ((lane & 3) == 0) s[r * s_row + (int64_t)(cc >> 2) * s_blk] = (uint8_t)b;
@@ -126,14 +113,6 @@ __global__ __launch_bounds__(256) void k_pad_ends(const int32_t* __restrict__ en
   for (int g = threadIdx.x; g < E; g += 256) ends_pad[g] = pend_s[g];
 }
 
-// One value of a block: x * 2^e clamped to +-448 (FLOOR NaN blocks divide by +inf).
-template <int MODE>
-__device__ __forceinline__ float scaled1(uint32_t bits16, uint32_t b, int e) {
-  const float x = bf16_bits_to_f32(bits16);
-  if (MODE == kModeFloor && b == 255u) return floor_nan_block_value(x);
-  return scale_and_clamp(x, e);
-}
-
 // ---------------------------------------------------------------------------
 // dim1.  A wave covers 128 padded token positions x 64 features; lane
 // (tg = lane % 8, fg = lane / 8) owns positions 16*tg .. +15 of the tile and
@@ -162,26 +141,9 @@ __global__ __launch_bounds__(256) void k_quant_dim1(
   int64_t tok0 = 0;
   int ntok = 0;
   if (ends != nullptr) {
-    for (int g = threadIdx.x; g < E; g += 256) {
-      const int32_t e = ends[g];
-      ends_s[g] = e < 0 ? 0 : (e > rows ? (int32_t)rows : e);
-      pend_s[g] = ends_pad[g];
-    }
+    stage_group_tables(ends, ends_pad, E, rows, ends_s, pend_s);
     __syncthreads();
-    // first group whose padded end is > P
-    int lo = 0, hi = E;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if ((int64_t)pend_s[mid] > P) hi = mid; else lo = mid + 1;
-    }
-    if (lo < E) {
-      const int64_t pstart = lo > 0 ? pend_s[lo - 1] : 0;
-      const int64_t gstart = lo > 0 ? ends_s[lo - 1] : 0;
-      const int64_t gend = ends_s[lo];
-      tok0 = gstart + (P - pstart);
-      const int64_t n = gend - tok0;  // negative when the clamped start exceeds the end
-      ntok = n <= 0 ? 0 : (n >= 16 ? 16 : (int)n);
-    }
+    padded_run_tokens(P, 16, ends_s, pend_s, E, tok0, ntok);
   } else {
     tok0 = P;
     const int64_t n = rows - P;
@@ -208,7 +170,6 @@ __global__ __launch_bounds__(256) void k_quant_dim1(
     }
     am = max(am, (uint32_t)__shfl_xor((int)am, 1));
     const uint32_t b = e8m0_from_amax16<MODE>(am);
-    const int e = payload_exponent<MODE>(b);
     bytes[j] = b;
     uint32_t o[4];
 #pragma unroll
@@ -218,9 +179,9 @@ __global__ __launch_bounds__(256) void k_quant_dim1(
       for (int u = 0; u < 4; ++u) {
         const int i = 4 * k + u;
         const uint32_t w = (j >> 1) == 0 ? v[i].x : (j >> 1) == 1 ? v[i].y : (j >> 1) == 2 ? v[i].z : v[i].w;
-        y[u] = scaled1<MODE>((w >> sh) & 0xFFFFu, b, e);
+        y[u] = bf16_bits_to_f32((w >> sh) & 0xFFFFu);
       }
-      o[k] = e4m3_pack4<SW>(y[0], y[1], y[2], y[3]);
+      o[k] = encode4<MODE, SW>(y[0], y[1], y[2], y[3], b);
     }
     if (out_ok)
       *reinterpret_cast<uint4*>(qt + (int64_t)(f + j) * ldqt + P) = make_uint4(o[0], o[1], o[2], o[3]);
@@ -317,6 +278,13 @@ hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int6
   if (m == kModeRceil) return sw ? MXGG_DIM1(kModeRceil, true) : MXGG_DIM1(kModeRceil, false);
   return sw ? MXGG_DIM1(kModeFloor, true) : MXGG_DIM1(kModeFloor, false);
 #undef MXGG_DIM1
+}
+
+hipError_t launch_pad_ends(const int32_t* group_ends, int64_t num_groups, int64_t rows,
+                           int32_t* group_ends_pad, hipStream_t stream) {
+  hipLaunchKernelGGL(k_pad_ends, dim3(1), dim3(256), 0, stream, group_ends, (int)num_groups, rows,
+                     group_ends_pad);
+  return hipGetLastError();
 }
 
 hipError_t launch_scales_to_block_major(const uint8_t* src, int64_t batch, int64_t rows,

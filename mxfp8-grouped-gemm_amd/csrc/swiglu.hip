@@ -1,0 +1,393 @@
+// SwiGLU activation of the expert FFN fused with the MXFP8 casts around it.
+//
+// The gate+up projection writes h = [gate | up] in bf16.  The down projection
+// needs a = SiLU(gate) * up cast along its features (row-wise, 1x32 blocks);
+// the backward pass needs, from h and the gradient da of a:
+//   dh = [d_gate | d_up]   cast row-wise      (dX = dh . W_gate_up)
+//   dh                     cast along tokens  (dW_gate_up = dh^T . X)
+//   a                      cast along tokens  (dW_down = dY^T . a)
+// Each of the two kernels reads its bf16 inputs once and writes every cast
+// directly; no bf16 intermediate goes through HBM.
+//
+// Arithmetic is torch's eager bf16 semantics for the same expression
+// (F.silu(gate) * up with autograd), so the fused path equals the unfused one:
+//   s      = bf16(g / (1 + exp(-g)))                 (silu, fp32 inside)
+//   a      = bf16(s * u)
+//   d_up   = bf16(da * s)
+//   d_gate = bf16(bf16(da * u) * sig * (1 + g * (1 - sig))),  sig = 1 / (1 + exp(-g))
+// The reference computes the same activation eagerly in bf16
+// (e2e_bench.py:56-61 forward, :85-100 backward).
+#include <algorithm>
+
+#include "mx_device.h"
+#include "mxgg_internal.h"
+
+namespace mxgg {
+namespace {
+
+// a for the two values of a word of gate and up (packed bf16 result).
+__device__ __forceinline__ uint32_t swiglu_a_word(uint32_t gw, uint32_t uw) {
+  const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
+  const uint32_t sw = pack_bf16x2(g0 / (1.0f + expf(-g0)), g1 / (1.0f + expf(-g1)));
+  return pack_bf16x2(bf16_lo(sw) * bf16_lo(uw), bf16_hi(sw) * bf16_hi(uw));
+}
+
+__device__ __forceinline__ uint4 swiglu_a_chunk(const uint4& g, const uint4& u) {
+  return make_uint4(swiglu_a_word(g.x, u.x), swiglu_a_word(g.y, u.y), swiglu_a_word(g.z, u.z),
+                    swiglu_a_word(g.w, u.w));
+}
+
+struct ActWord {
+  uint32_t a, dg, du;  // two packed bf16 results each
+};
+
+__device__ __forceinline__ float dsilu_term(float ds, float g, float ex) {
+  const float sig = 1.0f / (1.0f + ex);
+  return ds * sig * (1.0f + g * (1.0f - sig));
+}
+
+// a, d_gate and d_up for the two values of a word of gate, up and grad_a.
+__device__ __forceinline__ ActWord swiglu_bwd_word(uint32_t gw, uint32_t uw, uint32_t dw) {
+  const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
+  const float u0 = bf16_lo(uw), u1 = bf16_hi(uw);
+  const float d0 = bf16_lo(dw), d1 = bf16_hi(dw);
+  const float e0 = expf(-g0), e1 = expf(-g1);
+  const uint32_t sw = pack_bf16x2(g0 / (1.0f + e0), g1 / (1.0f + e1));  // s = bf16(silu(g))
+  const uint32_t dsw = pack_bf16x2(d0 * u0, d1 * u1);                   // bf16(grad_a * up)
+  const float s0 = bf16_lo(sw), s1 = bf16_hi(sw);
+  ActWord r;
+  r.a = pack_bf16x2(s0 * u0, s1 * u1);
+  r.du = pack_bf16x2(d0 * s0, d1 * s1);
+  r.dg = pack_bf16x2(dsilu_term(bf16_lo(dsw), g0, e0), dsilu_term(bf16_hi(dsw), g1, e1));
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Forward: a = SiLU(gate) * up, cast row-wise.  Same shape as the dim0 cast:
+// a lane owns one 8-feature chunk of a row (gate and up chunk loaded as one
+// 16-byte vector each), a quad holds one 32-feature block, a wave 4 rows per
+// trip, a workgroup 16 rows.
+// ---------------------------------------------------------------------------
+template <int MODE, bool SW>
+__global__ __launch_bounds__(256) void k_swiglu_dim0(
+    const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, int64_t ldh, int64_t rows,
+    int cols8, uint16_t* __restrict__ a_out, int64_t lda, uint8_t* __restrict__ q, int64_t ldq,
+    uint8_t* __restrict__ s, int64_t s_row, int64_t s_blk) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int cc = blockIdx.x * 64 + lane;
+  const bool col_ok = cc < cols8;  // whole quads share col_ok (cols8 % 4 == 0)
+  for (int64_t r0 = (int64_t)blockIdx.y * 16 + wave * 4; r0 < rows; r0 += (int64_t)gridDim.y * 16) {
+    uint4 g[4], u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t r = r0 + k;
+      if (col_ok && r < rows) {
+        g[k] = *reinterpret_cast<const uint4*>(gate + r * ldh + (int64_t)cc * 8);
+        u[k] = *reinterpret_cast<const uint4*>(up + r * ldh + (int64_t)cc * 8);
+      } else {
+        g[k] = make_uint4(0, 0, 0, 0);
+        u[k] = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t r = r0 + k;
+      const uint4 a = swiglu_a_chunk(g[k], u[k]);
+      uint32_t am = amax16_of_chunk(a);
+      am = max(am, (uint32_t)__shfl_xor((int)am, 1));
+      am = max(am, (uint32_t)__shfl_xor((int)am, 2));
+      const uint32_t b = e8m0_from_amax16<MODE>(am);
+      const uint2 o = encode_chunk8<MODE, SW>(a, b);
+      if (col_ok && r < rows) {
+        *reinterpret_cast<uint2*>(q + r * ldq + (int64_t)cc * 8) = o;
+        if ((lane & 3) == 0) s[r * s_row + (int64_t)(cc >> 2) * s_blk] = (uint8_t)b;
+        if (a_out != nullptr) *reinterpret_cast<uint4*>(a_out + r * lda + (int64_t)cc * 8) = a;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward.  A workgroup covers 128 padded token positions x 64 features of
+// a (so 2 x 64 features of h and dh); wave w takes positions 32w .. 32w+31,
+// exactly one 32-token scale block.  Lane (tg = lane % 4, fg = lane / 4) owns
+// 8 positions (8 tg ..) and 4 features (4 fg ..): it loads 8 token rows of
+// gate, up and da as 8-byte vectors (sixteen lanes read 128 contiguous bytes
+// of a row), computes a, d_gate and d_up in registers, and emits
+//   row-wise casts of d_gate / d_up: a 32-feature block is the eight lanes
+//     fg = 8k .. 8k+7 (amax combined with xor-4 / xor-8 / xor-16 shuffles);
+//   token-axis casts of a, d_gate, d_up: a 32-token block is the four lanes
+//     tg = 0 .. 3 (xor-1 / xor-2 shuffles), 8 payload bytes per feature, so the
+//     four waves write 128 contiguous bytes of every output row.
+// Padded positions map to tokens as in the token-axis cast; a run of 8 never
+// straddles a group because groups start on multiples of 32.
+// ---------------------------------------------------------------------------
+struct SwigluBwdArgs {
+  const uint16_t* gate;
+  const uint16_t* up;
+  const uint16_t* da;
+  const int32_t* ends;      // nullptr = one group of `rows` tokens
+  const int32_t* ends_pad;
+  uint8_t* dq;              // row-wise cast of [d_gate | d_up]: [rows, 2 cols]
+  uint8_t* ds;
+  uint8_t* dqt;             // token-axis cast of [d_gate | d_up]: [2 cols, cap]
+  uint8_t* dst;
+  uint8_t* aqt;             // token-axis cast of a: [cols, cap]
+  uint8_t* ast;
+  uint16_t* dh;             // optional bf16 [d_gate | d_up]: [rows, 2 cols]
+  int64_t ldh, ldda, rows, cap;
+  int64_t lddq, ds_row, ds_blk;
+  int64_t lddqt, dst_row, dst_blk;
+  int64_t ldaqt, ast_row, ast_blk;
+  int64_t lddh;
+  int32_t cols, E;
+};
+
+__device__ __forceinline__ float half_f(const uint2& v, int j) {
+  const uint32_t w = (j >> 1) == 0 ? v.x : v.y;
+  return (j & 1) ? bf16_hi(w) : bf16_lo(w);
+}
+
+__device__ __forceinline__ uint32_t half_bits(const uint2& v, int j) {
+  const uint32_t w = (j >> 1) == 0 ? v.x : v.y;
+  return (w >> (16 * (j & 1))) & 0x7FFFu;
+}
+
+// Writes n <= 8 scale bytes b[j] at p[j * stride], as one 8-byte store when
+// all eight are contiguous and aligned.
+__device__ __forceinline__ void store_scale8(uint8_t* p, int64_t stride, const uint32_t (&b)[8],
+                                             int n) {
+  if (stride == 1 && n == 8 && (reinterpret_cast<uintptr_t>(p) & 7u) == 0) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
+                                              b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < n) p[(int64_t)j * stride] = (uint8_t)b[j];
+  }
+}
+
+// Token-axis cast of the lane's 4 features x 8 positions held in v[0..7]:
+// feature j goes to row j of `qrow` (8 payload bytes; qrow already points at
+// column P of the lane's first feature row) and its scale byte to srow[j *
+// st_row]; the lane with tg == 0 writes the 4 scale bytes.
+template <int MODE, bool SW>
+__device__ __forceinline__ void emit_token_axis(const uint2 (&v)[8], uint8_t* qrow, int64_t ldqt,
+                                                uint8_t* srow, int64_t st_row, bool out_ok,
+                                                bool scale_lane) {
+  uint32_t bytes[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t am = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = max(am, half_bits(v[i], j));
+    am = max(am, (uint32_t)__shfl_xor((int)am, 1));
+    am = max(am, (uint32_t)__shfl_xor((int)am, 2));
+    const uint32_t b = e8m0_from_amax16<MODE>(am);
+    bytes[j] = b;
+    const uint32_t lo = encode4<MODE, SW>(half_f(v[0], j), half_f(v[1], j), half_f(v[2], j),
+                                          half_f(v[3], j), b);
+    const uint32_t hi = encode4<MODE, SW>(half_f(v[4], j), half_f(v[5], j), half_f(v[6], j),
+                                          half_f(v[7], j), b);
+    if (out_ok) *reinterpret_cast<uint2*>(qrow + j * ldqt) = make_uint2(lo, hi);
+  }
+  if (out_ok && scale_lane) {
+    if (st_row == 1 && (reinterpret_cast<uintptr_t>(srow) & 3u) == 0) {
+      *reinterpret_cast<uint32_t*>(srow) =
+          bytes[0] | (bytes[1] << 8) | (bytes[2] << 16) | (bytes[3] << 24);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) srow[(int64_t)j * st_row] = (uint8_t)bytes[j];
+    }
+  }
+}
+
+// Row-wise cast of 4 features x 8 tokens (chunk v[i] of token i) into qrow
+// (row of the first token, already offset to the lane's column), scale bytes
+// into srow[i * s_row]; the eight lanes of a 32-feature block share amax.
+template <int MODE, bool SW>
+__device__ __forceinline__ void emit_row_wise(const uint2 (&v)[8], uint8_t* qrow, int64_t ldq,
+                                              uint8_t* srow, int64_t s_row, int ntok,
+                                              bool scale_lane) {
+  uint32_t bytes[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t am = max(amax16_of_word(v[i].x), amax16_of_word(v[i].y));
+    am = max(am, (uint32_t)__shfl_xor((int)am, 4));
+    am = max(am, (uint32_t)__shfl_xor((int)am, 8));
+    am = max(am, (uint32_t)__shfl_xor((int)am, 16));
+    const uint32_t b = e8m0_from_amax16<MODE>(am);
+    bytes[i] = b;
+    const uint32_t o = encode4<MODE, SW>(bf16_lo(v[i].x), bf16_hi(v[i].x), bf16_lo(v[i].y),
+                                         bf16_hi(v[i].y), b);
+    if (i < ntok) *reinterpret_cast<uint32_t*>(qrow + i * ldq) = o;
+  }
+  if (scale_lane && ntok > 0) store_scale8(srow, s_row, bytes, ntok);
+}
+
+template <int MODE, bool SW>
+__global__ __launch_bounds__(256) void k_swiglu_bwd(const SwigluBwdArgs p) {
+  __shared__ int32_t ends_s[kMaxGroups];
+  __shared__ int32_t pend_s[kMaxGroups];
+  const int lane = threadIdx.x & 63;
+  const int tg = lane & 3, fg = lane >> 2;
+  const int64_t P = (int64_t)blockIdx.x * 128 + (threadIdx.x >> 6) * 32 + 8 * tg;
+  const int f = blockIdx.y * 64 + 4 * fg;
+
+  int64_t tok0 = 0;
+  int ntok = 0;
+  if (p.ends != nullptr) {
+    stage_group_tables(p.ends, p.ends_pad, p.E, p.rows, ends_s, pend_s);
+    __syncthreads();
+    padded_run_tokens(P, 8, ends_s, pend_s, p.E, tok0, ntok);
+  } else {
+    tok0 = P;
+    const int64_t n = p.rows - P;
+    ntok = n <= 0 ? 0 : (n >= 8 ? 8 : (int)n);
+  }
+  if (f >= p.cols) ntok = 0;
+
+  const uint16_t* gp = p.gate + tok0 * p.ldh + f;
+  const uint16_t* upp = p.up + tok0 * p.ldh + f;
+  const uint16_t* dp = p.da + tok0 * p.ldda + f;
+  uint2 g[8], u[8], d[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    g[i] = u[i] = d[i] = make_uint2(0, 0);
+    if (i < ntok) {
+      g[i] = *reinterpret_cast<const uint2*>(gp + i * p.ldh);
+      u[i] = *reinterpret_cast<const uint2*>(upp + i * p.ldh);
+      d[i] = *reinterpret_cast<const uint2*>(dp + i * p.ldda);
+    }
+  }
+  uint2 A[8], DG[8], DU[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const ActWord r0 = swiglu_bwd_word(g[i].x, u[i].x, d[i].x);
+    const ActWord r1 = swiglu_bwd_word(g[i].y, u[i].y, d[i].y);
+    A[i] = make_uint2(r0.a, r1.a);
+    DG[i] = make_uint2(r0.dg, r1.dg);
+    DU[i] = make_uint2(r0.du, r1.du);
+  }
+
+  const int64_t cols = p.cols;
+  if (p.dh != nullptr) {
+    uint16_t* row = p.dh + tok0 * p.lddh + f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (i < ntok) {
+        *reinterpret_cast<uint2*>(row + i * p.lddh) = DG[i];
+        *reinterpret_cast<uint2*>(row + i * p.lddh + cols) = DU[i];
+      }
+    }
+  }
+
+  // Row-wise casts: d_gate into columns f.., d_up into columns cols + f.. of dq.
+  const bool row_scale_lane = (fg & 7) == 0;
+  uint8_t* qrow = p.dq + tok0 * p.lddq + f;
+  uint8_t* srow = p.ds + tok0 * p.ds_row;
+  emit_row_wise<MODE, SW>(DG, qrow, p.lddq, srow + (int64_t)(f >> 5) * p.ds_blk, p.ds_row, ntok,
+                          row_scale_lane);
+  emit_row_wise<MODE, SW>(DU, qrow + cols, p.lddq, srow + ((cols + f) >> 5) * p.ds_blk, p.ds_row,
+                          ntok, row_scale_lane);
+
+  // Token-axis casts: a -> rows f.. of aqt; d_gate -> rows f.., d_up -> rows
+  // cols + f.. of dqt.  Padded positions carry zeros (zero payload, byte 0).
+  const bool out_ok = f < p.cols && P < p.cap;
+  const bool tok_scale_lane = tg == 0;
+  const int64_t sblk = P >> 5;
+  emit_token_axis<MODE, SW>(A, p.aqt + (int64_t)f * p.ldaqt + P, p.ldaqt,
+                            p.ast + (int64_t)f * p.ast_row + sblk * p.ast_blk, p.ast_row, out_ok,
+                            tok_scale_lane);
+  emit_token_axis<MODE, SW>(DG, p.dqt + (int64_t)f * p.lddqt + P, p.lddqt,
+                            p.dst + (int64_t)f * p.dst_row + sblk * p.dst_blk, p.dst_row, out_ok,
+                            tok_scale_lane);
+  emit_token_axis<MODE, SW>(DU, p.dqt + (cols + f) * p.lddqt + P, p.lddqt,
+                            p.dst + (cols + f) * p.dst_row + sblk * p.dst_blk, p.dst_row, out_ok,
+                            tok_scale_lane);
+}
+
+template <int MODE, bool SW>
+hipError_t swiglu_dim0_impl(const uint16_t* gate, const uint16_t* up, int64_t ldh, int64_t rows,
+                            int64_t cols, uint16_t* a_out, int64_t lda, uint8_t* q, int64_t ldq,
+                            uint8_t* s, int64_t s_row, int64_t s_blk, hipStream_t stream) {
+  const int cols8 = (int)(cols / 8);
+  dim3 grid((cols8 + 63) / 64, (unsigned)std::min<int64_t>((rows + 15) / 16, 65535));
+  hipLaunchKernelGGL((k_swiglu_dim0<MODE, SW>), grid, dim3(256), 0, stream, gate, up, ldh, rows,
+                     cols8, a_out, lda, q, ldq, s, s_row, s_blk);
+  return hipGetLastError();
+}
+
+template <int MODE, bool SW>
+hipError_t swiglu_bwd_impl(const SwigluBwdArgs& p, hipStream_t stream) {
+  dim3 grid((unsigned)((p.cap + 127) / 128), (unsigned)((p.cols + 63) / 64));
+  hipLaunchKernelGGL((k_swiglu_bwd<MODE, SW>), grid, dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_swiglu_quant_dim0(const uint16_t* gate, const uint16_t* up, int64_t ldh,
+                                    int64_t rows, int64_t cols, uint16_t* a_out, int64_t lda,
+                                    uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int layout,
+                                    int mode, hipStream_t stream) {
+  if (rows == 0 || cols == 0) return hipSuccess;
+  const bool sw = (mode & kCvtSoftwareFlag) != 0;
+  const int m = mode & 0xFF;
+  const int64_t s_row = layout == MXGG_SCALES_BLOCK_MAJOR ? 1 : lds;
+  const int64_t s_blk = layout == MXGG_SCALES_BLOCK_MAJOR ? lds : 1;
+#define MXGG_SWIGLU0(MODE, SWF) \
+  swiglu_dim0_impl<MODE, SWF>(gate, up, ldh, rows, cols, a_out, lda, q, ldq, s, s_row, s_blk, stream)
+  if (m == kModeRceil) return sw ? MXGG_SWIGLU0(kModeRceil, true) : MXGG_SWIGLU0(kModeRceil, false);
+  return sw ? MXGG_SWIGLU0(kModeFloor, true) : MXGG_SWIGLU0(kModeFloor, false);
+#undef MXGG_SWIGLU0
+}
+
+hipError_t launch_swiglu_bwd_quant(const SwigluBwdLaunch& l, hipStream_t stream) {
+  if (l.cols == 0 || l.cap == 0) return hipSuccess;
+  if (l.group_ends != nullptr) {
+    const hipError_t err = launch_pad_ends(l.group_ends, l.num_groups, l.rows, l.group_ends_pad,
+                                           stream);
+    if (err != hipSuccess) return err;
+  }
+  const bool bm = l.layout == MXGG_SCALES_BLOCK_MAJOR;
+  SwigluBwdArgs p;
+  p.gate = l.gate;
+  p.up = l.up;
+  p.da = l.da;
+  p.ends = l.group_ends;
+  p.ends_pad = l.group_ends_pad;
+  p.dq = l.dq;
+  p.ds = l.ds;
+  p.dqt = l.dqt;
+  p.dst = l.dst;
+  p.aqt = l.aqt;
+  p.ast = l.ast;
+  p.dh = l.dh;
+  p.ldh = l.ldh;
+  p.ldda = l.ldda;
+  p.rows = l.rows;
+  p.cap = l.cap;
+  p.lddq = l.lddq;
+  p.ds_row = bm ? 1 : l.ldds;
+  p.ds_blk = bm ? l.ldds : 1;
+  p.lddqt = l.lddqt;
+  p.dst_row = bm ? 1 : l.lddst;
+  p.dst_blk = bm ? l.lddst : 1;
+  p.ldaqt = l.ldaqt;
+  p.ast_row = bm ? 1 : l.ldast;
+  p.ast_blk = bm ? l.ldast : 1;
+  p.lddh = l.lddh;
+  p.cols = (int32_t)l.cols;
+  p.E = (int32_t)(l.group_ends != nullptr ? l.num_groups : 1);
+  const bool sw = (l.mode & kCvtSoftwareFlag) != 0;
+  const int m = l.mode & 0xFF;
+  if (m == kModeRceil)
+    return sw ? swiglu_bwd_impl<kModeRceil, true>(p, stream)
+              : swiglu_bwd_impl<kModeRceil, false>(p, stream);
+  return sw ? swiglu_bwd_impl<kModeFloor, true>(p, stream)
+            : swiglu_bwd_impl<kModeFloor, false>(p, stream);
+}
+
+}  // namespace mxgg

@@ -15,13 +15,15 @@ from .ops import (
     grouped_wgrad,
     padded_token_capacity,
     quant_weight_for_dgrad,
+    swiglu_backward_quant,
+    swiglu_quant,
     to_mxfp8_dim0,
     to_mxfp8_dim1,
     wgrad_fused,
     wgrad_kernel,
     wgrad_prepare,
 )
-from .autograd import MXFP8GroupedMM, moe_ffn, mxfp8_grouped_mm
+from .autograd import MXFP8ExpertFFN, MXFP8GroupedMM, moe_ffn, moe_ffn_unfused, mxfp8_grouped_mm
 from .torchao_compat import (
     apply,
     triton_mxfp8_grouped_mm,
@@ -35,8 +37,9 @@ __all__ = [
     "MxggError", "load_library",
     "to_mxfp8_dim0", "to_mxfp8_dim1", "padded_token_capacity",
     "grouped_mm", "grouped_wgrad", "grouped_dgrad", "quant_weight_for_dgrad",
+    "swiglu_quant", "swiglu_backward_quant",
     "fused_grouped_fwd", "fwd_ge", "wgrad_fused", "wgrad_prepare", "wgrad_kernel",
     "triton_to_mxfp8_dim0", "triton_to_mxfp8_dim1",
     "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",
-    "MXFP8GroupedMM", "mxfp8_grouped_mm", "moe_ffn",
+    "MXFP8GroupedMM", "mxfp8_grouped_mm", "MXFP8ExpertFFN", "moe_ffn", "moe_ffn_unfused",
 ]

@@ -62,12 +62,76 @@ def mxfp8_grouped_mm(x: torch.Tensor, w: torch.Tensor, offs: torch.Tensor,
     return MXFP8GroupedMM.apply(x, w, offs, scaling_mode)
 
 
+class MXFP8ExpertFFN(torch.autograd.Function):
+    """y = (SiLU(x . Wg^T) * (x . Wu^T)) . Wd^T per expert group, every GEMM in
+    MXFP8, the activation fused with the casts around it.
+
+    forward : x cast (dim0) -> gate+up GEMM -> h = [gate | up] (bf16, kept for
+              backward) -> SwiGLU + cast of a in one kernel -> down GEMM
+    backward: dA = dY . Wd (MXFP8 dgrad); one kernel turns (h, dA) into the
+              row-wise and token-axis casts of dh = [d_gate | d_up] and the
+              token-axis cast of a; then dWd = dY^T . a, dX = dh . Wgu and
+              dWgu = dh^T . X, all MXFP8.
+    """
+
+    @staticmethod
+    def forward(ctx, x, w_gate_up, w_down, offs, scaling_mode="rceil"):
+        for name, t in (("x", x), ("w_gate_up", w_gate_up), ("w_down", w_down)):
+            if t.dtype != torch.bfloat16:
+                raise TypeError(f"{name} must be bfloat16")
+        E, F2, H = w_gate_up.shape
+        if tuple(w_down.shape) != (E, H, F2 // 2) or x.shape[-1] != H:
+            raise ValueError("shapes must be x [M, H], w_gate_up [E, 2F, H], w_down [E, H, F]")
+        ends = ops._group_ends(offs, E, x.device)
+        xq, xs = ops.to_mxfp8_dim0(x, scaling_mode)
+        wq, ws = ops.to_mxfp8_dim0(w_gate_up, scaling_mode)
+        h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
+        aq, as_ = ops.swiglu_quant(h, scaling_mode)
+        dq, ds = ops.to_mxfp8_dim0(w_down, scaling_mode)
+        y = ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16)
+        ctx.save_for_backward(x, w_gate_up, w_down, ends, h)
+        ctx.scaling_mode = scaling_mode
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, wgu, wd, ends, h = ctx.saved_tensors
+        mode = ctx.scaling_mode
+        dy = dy.to(torch.bfloat16)
+        if dy.stride(-1) != 1:
+            dy = dy.contiguous()
+        da = ops.grouped_dgrad(dy, wd, ends, scaling_mode=mode)
+        act = ops.swiglu_backward_quant(h, da, ends, mode)
+        pad = act["offs_pad"]
+        dwd = dwgu = dx = None
+        if ctx.needs_input_grad[2]:
+            dyt, dyst, _ = ops.to_mxfp8_dim1(dy, ends, mode)
+            dwd = ops.grouped_wgrad(dyt, act["a_qt"], pad, dyst, act["a_st"], out_dtype=wd.dtype)
+        if ctx.needs_input_grad[0]:
+            wt, wts = ops.quant_weight_for_dgrad(wgu, mode)
+            dx = ops.grouped_mm(act["dh_q"], wt, ends, act["dh_s"], wts, out_dtype=torch.bfloat16)
+        if ctx.needs_input_grad[1]:
+            xt, xst, _ = ops.to_mxfp8_dim1(x, ends, mode)
+            dwgu = ops.grouped_wgrad(act["dh_qt"], xt, pad, act["dh_st"], xst, out_dtype=wgu.dtype)
+        return dx, dwgu, dwd, None, None
+
+
 def moe_ffn(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,
             offs: torch.Tensor, scaling_mode: str = "rceil") -> torch.Tensor:
     """One DeepSeek-V3-style expert FFN over routed tokens (the layer step of
     the reference's e2e_bench.py:56-134): gate+up projection with the fused
     weight w_gate_up [E, 2F, H] (gate rows first), SiLU(gate) * up, down
-    projection w_down [E, H, F]."""
+    projection w_down [E, H, F].  x: bf16 [M, H], tokens grouped by expert with
+    cumulative ends `offs`.  Rows after the last group end get no output and no
+    input gradient."""
+    return MXFP8ExpertFFN.apply(x, w_gate_up, w_down, offs, scaling_mode)
+
+
+def moe_ffn_unfused(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,
+                    offs: torch.Tensor, scaling_mode: str = "rceil") -> torch.Tensor:
+    """The same layer composed from two MXFP8GroupedMM calls and torch's eager
+    bf16 SiLU * up (the reference's own composition, e2e_bench.py:56-61); kept
+    as the comparison point for the fused path."""
     h = mxfp8_grouped_mm(x, w_gate_up, offs, scaling_mode)
     f = w_down.shape[2]
     a = torch.nn.functional.silu(h[:, :f]) * h[:, f:]

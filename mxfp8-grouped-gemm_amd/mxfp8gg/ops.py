@@ -249,6 +249,104 @@ def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mod
 
 
 # ---------------------------------------------------------------------------
+# SwiGLU fused with its casts (the expert FFN activation)
+# ---------------------------------------------------------------------------
+def _gate_up(h: torch.Tensor):
+    if h.dtype != torch.bfloat16 or h.dim() != 2 or h.shape[1] % 64 != 0:
+        raise TypeError("h must be a 2-D bfloat16 tensor [M, 2F] with F % 32 == 0")
+    if h.stride(-1) != 1 or h.stride(0) % 8 != 0 or h.data_ptr() % 16 != 0:
+        h = h.contiguous()
+    f = h.shape[1] // 2
+    return h, h[:, :f], h[:, f:], f
+
+
+def swiglu_quant(h: torch.Tensor, scaling_mode="rceil", return_bf16: bool = False):
+    """a = SiLU(gate) * up of the gate+up projection output h = [gate | up]
+    (bf16 [M, 2F]), cast row-wise to MXFP8 in the same pass.
+
+    Returns (q float8_e4m3fn [M, F], scales uint8 [M, F/32]) as to_mxfp8_dim0
+    does for a bf16 tensor, plus the bf16 a [M, F] when return_bf16.  a equals
+    torch's eager bf16 F.silu(gate) * up (the reference's layer step,
+    e2e_bench.py:56-61)."""
+    _need_gpu(h, "h")
+    h, gate, up, f = _gate_up(h)
+    M = h.shape[0]
+    q = torch.empty((M, f), dtype=_FP8, device=h.device)
+    buf = _block_major_buffer(M, f // 32, h.device)
+    a = torch.empty((M, f), dtype=torch.bfloat16, device=h.device) if return_bf16 else None
+    lib = _lib.load()
+    _lib.check(
+        lib.mxgg_swiglu_quant_dim0(
+            gate.data_ptr(), up.data_ptr(), h.stride(0), M, f,
+            a.data_ptr() if a is not None else None, f,
+            q.data_ptr(), f, buf.data_ptr(), buf.stride(0), _lib.SCALES_BLOCK_MAJOR,
+            _mode(scaling_mode), _stream_ptr(h)),
+        "swiglu_quant_dim0",
+    )
+    s = buf[:, :M].t()
+    return (q, s, a) if return_bf16 else (q, s)
+
+
+def swiglu_backward_quant(h: torch.Tensor, grad_a: torch.Tensor, offs: torch.Tensor | None,
+                          scaling_mode="rceil", return_bf16: bool = False):
+    """Backward of a = SiLU(gate) * up fused with the casts of the backward GEMMs.
+
+    h: bf16 [M, 2F] = [gate | up]; grad_a: bf16 [M, F]; offs: token group ends
+    (int32 [E] on the device) or None for one group.  Returns a dict:
+      dh_q, dh_s      row-wise cast of dh = [d_gate | d_up] [M, 2F]  (dX = dh . W_gate_up)
+      dh_qt, dh_st    token-axis cast of dh, [2F, M_pad]            (dW_gate_up)
+      a_qt, a_st      token-axis cast of a, [F, M_pad]              (dW_down)
+      offs_pad        padded group ends (None without offs)
+      dh              bf16 dh [M, 2F] (only with return_bf16)
+    Scales are views of block-major storage, as to_mxfp8_dim0 / to_mxfp8_dim1
+    return them; M_pad = padded_token_capacity(M, E).  Rows of dh_q past the
+    last group end are not written."""
+    _need_gpu(h, "h")
+    h, gate, up, f = _gate_up(h)
+    M = h.shape[0]
+    if grad_a.dtype != torch.bfloat16 or tuple(grad_a.shape) != (M, f):
+        raise TypeError(f"grad_a must be bfloat16 [{M}, {f}]")
+    if grad_a.stride(-1) != 1 or grad_a.stride(0) % 8 != 0 or grad_a.data_ptr() % 16 != 0:
+        grad_a = grad_a.contiguous()
+    dev = h.device
+    E = ends = ends_pad = None
+    if offs is not None:
+        E = offs.numel()
+        ends = _group_ends(offs, E, dev)
+        ends_pad = torch.empty(E, dtype=torch.int32, device=dev)
+    cap = padded_token_capacity(M, E)
+    dh_q = torch.empty((M, 2 * f), dtype=_FP8, device=dev)
+    dh_sb = _block_major_buffer(M, 2 * f // 32, dev)
+    dh_qt = torch.empty((2 * f, cap), dtype=_FP8, device=dev)
+    dh_stb = _block_major_buffer(2 * f, cap // 32, dev)
+    a_qt = torch.empty((f, cap), dtype=_FP8, device=dev)
+    a_stb = _block_major_buffer(f, cap // 32, dev)
+    dh = torch.empty((M, 2 * f), dtype=torch.bfloat16, device=dev) if return_bf16 else None
+    lib = _lib.load()
+    _lib.check(
+        lib.mxgg_swiglu_bwd_quant(
+            gate.data_ptr(), up.data_ptr(), h.stride(0), grad_a.data_ptr(), grad_a.stride(0),
+            M, f, ends.data_ptr() if ends is not None else None, E or 0, cap,
+            dh_q.data_ptr(), 2 * f, dh_sb.data_ptr(), dh_sb.stride(0),
+            dh_qt.data_ptr(), cap, dh_stb.data_ptr(), dh_stb.stride(0),
+            a_qt.data_ptr(), cap, a_stb.data_ptr(), a_stb.stride(0),
+            ends_pad.data_ptr() if ends_pad is not None else None,
+            dh.data_ptr() if dh is not None else None, 2 * f,
+            _lib.SCALES_BLOCK_MAJOR, _mode(scaling_mode), _stream_ptr(h)),
+        "swiglu_bwd_quant",
+    )
+    out = {
+        "dh_q": dh_q, "dh_s": dh_sb[:, :M].t(),
+        "dh_qt": dh_qt, "dh_st": dh_stb[:, :2 * f].t(),
+        "a_qt": a_qt, "a_st": a_stb[:, :f].t(),
+        "offs_pad": ends_pad,
+    }
+    if return_bf16:
+        out["dh"] = dh
+    return out
+
+
+# ---------------------------------------------------------------------------
 # forward grouped GEMM
 # ---------------------------------------------------------------------------
 def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,

@@ -18,7 +18,7 @@
  *              payload = clamp(x / max(2^(b-127), 2^-126), +-448)
  *       NaN anywhere in the block -> b = 0xFF.
  *   - Payload cast: round-to-nearest-even to OCP float8 e4m3fn, as
- *     torch's .to(torch.float8_e4m3fn) (e2e_bench.py:238-243); NaN -> 0x7F|sign.
+ *     torch's .to(torch.float8_e4m3fn) (e2e_bench.py:35-40); NaN -> 0x7F|sign.
  *   - Token-axis (dim1) quantisation with per-group restart and 32-padding:
  *     the transposed, token-contiguous wgrad operands of wgrad_fused.py:35-39,
  *     48-62 without the equal-group assumption.

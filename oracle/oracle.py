@@ -16,6 +16,10 @@ Pieces (reference paths under /root/reference):
   * cpu_baseline_*: the same dequant + per-group matmul in float32 with torch
     on all host cores — the reference's torch CPU dequant path, timed by
     bench.py as the CPU baseline.
+  * swiglu_fwd / swiglu_bwd: the expert FFN activation a = SiLU(gate) * up
+    and its gradients in float32 with bf16 rounding after each op, the eager
+    bf16 torch arithmetic of the reference's layer step (e2e_bench.py:56-61,
+    85-100) with the textbook SiLU derivative sig * (1 + g * (1 - sig)).
 """
 from __future__ import annotations
 
@@ -211,3 +215,52 @@ def cpu_baseline_fwd(a_q, a_s, w_q, w_s, ends):
         if e > b:
             out[b:e] = deq(a_q[b:e], a_s[b:e]) @ deq(w_q[g], w_s[g]).T
     return out
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU (expert FFN activation), bf16 in / bf16 out, float32 arithmetic
+# ---------------------------------------------------------------------------
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """float32 -> nearest bf16 (ties to even), returned as float32 values."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16).astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(x), np.float32(np.nan), r).astype(np.float32)
+
+
+def bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bits(x: np.ndarray) -> np.ndarray:
+    """bf16-representable float32 values -> uint16 bit patterns."""
+    return (np.ascontiguousarray(x, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def swiglu_fwd(g_bits: np.ndarray, u_bits: np.ndarray) -> np.ndarray:
+    """a = bf16(bf16(g / (1 + exp(-g))) * u) (torch's eager bf16 F.silu(g) * u)."""
+    g = bits_to_f32(g_bits)
+    u = bits_to_f32(u_bits)
+    with np.errstate(over="ignore", invalid="ignore"):
+        s = bf16_round(g / (np.float32(1) + np.exp(-g)))
+        return f32_to_bits(bf16_round(s * u))
+
+
+def swiglu_bwd(g_bits: np.ndarray, u_bits: np.ndarray, d_bits: np.ndarray):
+    """Gradients of a = silu(g) * u for upstream d = dL/da, as torch's eager
+    bf16 autograd computes them:
+      d_up   = bf16(d * s),  s = bf16(silu(g))
+      d_gate = bf16(bf16(d * u) * sig * (1 + g * (1 - sig))),  sig = 1/(1+exp(-g))
+    Returns (a, d_gate, d_up) as bf16 bit patterns."""
+    g = bits_to_f32(g_bits)
+    u = bits_to_f32(u_bits)
+    d = bits_to_f32(d_bits)
+    one = np.float32(1)
+    with np.errstate(over="ignore", invalid="ignore"):
+        ex = np.exp(-g)
+        s = bf16_round(g / (one + ex))
+        sig = one / (one + ex)
+        ds = bf16_round(d * u)
+        dg = bf16_round(ds * sig * (one + g * (one - sig)))
+        du = bf16_round(d * s)
+        a = bf16_round(s * u)
+    return f32_to_bits(a), f32_to_bits(dg), f32_to_bits(du)

@@ -173,6 +173,74 @@ def test_quant_dim1_rejects(lib, kw, status):
                                a["pad"], a["mode"], None) == status
 
 
+def _swiglu0(lib, **kw):
+    a = dict(g=FAKE, u=FAKE + 128, ldh=128, rows=8, cols=64, aout=None, lda=64, q=FAKE, ldq=64,
+             s=FAKE, lds=8, layout=BM, mode=0)
+    a.update(kw)
+    return lib.mxgg_swiglu_quant_dim0(a["g"], a["u"], a["ldh"], a["rows"], a["cols"], a["aout"],
+                                      a["lda"], a["q"], a["ldq"], a["s"], a["lds"], a["layout"],
+                                      a["mode"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(cols=48), _lib.ERR_SHAPE),
+    (dict(rows=-1), _lib.ERR_SHAPE),
+    (dict(mode=4), _lib.ERR_INVALID_ARGUMENT),
+    (dict(layout=2), _lib.ERR_INVALID_ARGUMENT),
+    (dict(u=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ldh=32), _lib.ERR_SHAPE),                  # ldh < cols
+    (dict(lds=4), _lib.ERR_SHAPE),                   # block-major ld < rows
+    (dict(u=FAKE + 8), _lib.ERR_ALIGNMENT),
+    (dict(ldh=132), _lib.ERR_ALIGNMENT),
+    (dict(aout=FAKE, lda=68), _lib.ERR_ALIGNMENT),
+])
+def test_swiglu_quant_dim0_rejects(lib, kw, status):
+    assert _swiglu0(lib, **kw) == status
+
+
+def test_swiglu_quant_dim0_empty_is_noop(lib):
+    assert _swiglu0(lib, rows=0, g=None, u=None, q=None, s=None) == _lib.OK
+
+
+def _swiglu_bwd(lib, **kw):
+    a = dict(g=FAKE, u=FAKE + 128, ldh=128, da=FAKE, ldga=64, rows=64, cols=64, ends=FAKE, E=2,
+             cap=128, dq=FAKE, lddq=128, ds=FAKE, ldds=64, dqt=FAKE, lddqt=128, dst=FAKE,
+             lddst=128, aqt=FAKE, ldaqt=128, ast=FAKE, ldast=64, pad=FAKE, dh=None, lddh=128,
+             layout=BM, mode=0)
+    a.update(kw)
+    return lib.mxgg_swiglu_bwd_quant(
+        a["g"], a["u"], a["ldh"], a["da"], a["ldga"], a["rows"], a["cols"], a["ends"], a["E"],
+        a["cap"], a["dq"], a["lddq"], a["ds"], a["ldds"], a["dqt"], a["lddqt"], a["dst"],
+        a["lddst"], a["aqt"], a["ldaqt"], a["ast"], a["ldast"], a["pad"], a["dh"], a["lddh"],
+        a["layout"], a["mode"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(cols=40), _lib.ERR_SHAPE),
+    (dict(cap=96), _lib.ERR_SHAPE),                  # below rows + 31 * groups
+    (dict(cap=120), _lib.ERR_SHAPE),                 # not a multiple of 32
+    (dict(E=0), _lib.ERR_UNSUPPORTED),
+    (dict(E=1025), _lib.ERR_UNSUPPORTED),
+    (dict(pad=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(da=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(aqt=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(mode=7), _lib.ERR_INVALID_ARGUMENT),
+    (dict(lddq=64), _lib.ERR_SHAPE),                 # dh row is 2 * cols wide
+    (dict(lddst=64), _lib.ERR_SHAPE),                # block-major ld < 2 * cols
+    (dict(ldast=32), _lib.ERR_SHAPE),
+    (dict(da=FAKE + 4), _lib.ERR_ALIGNMENT),
+    (dict(lddqt=136), _lib.ERR_ALIGNMENT),
+    (dict(dq=FAKE + 4), _lib.ERR_ALIGNMENT),
+    (dict(dh=FAKE + 8), _lib.ERR_ALIGNMENT),
+])
+def test_swiglu_bwd_quant_rejects(lib, kw, status):
+    assert _swiglu_bwd(lib, **kw) == status
+
+
+def test_swiglu_bwd_quant_empty_is_noop(lib):
+    assert _swiglu_bwd(lib, cols=0) == _lib.OK
+
+
 def test_python_maps_errors_to_exceptions(lib):
     with pytest.raises(ValueError, match="K=100"):
         _lib.check(_fwd(lib, K=100), "grouped_fwd")

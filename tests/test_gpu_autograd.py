@@ -86,3 +86,27 @@ def test_moe_ffn_layer_gradients_match_fp32(gpu):
     assert _rel(y, yr) < 0.1
     for got, want in zip(leaves, ref):
         assert _rel(got.grad, want.grad) < 0.15
+
+
+def test_moe_ffn_fused_matches_unfused_composition(gpu):
+    # The fused layer (SwiGLU kernels) against the composition of two
+    # MXFP8GroupedMM calls with torch's eager bf16 SiLU * up.
+    sizes = [64, 160, 0, 96, 32]
+    E, H, F = 5, 256, 192
+    g = torch.Generator(device=gpu).manual_seed(84)
+    M = sum(sizes)
+    x = torch.randn(M, H, generator=g, device=gpu).to(torch.bfloat16)
+    wgu = (torch.randn(E, 2 * F, H, generator=g, device=gpu) * 0.06).to(torch.bfloat16)
+    wd = (torch.randn(E, H, F, generator=g, device=gpu) * 0.06).to(torch.bfloat16)
+    dy = torch.randn(M, H, generator=g, device=gpu).to(torch.bfloat16)
+    offs = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    fused = [t.clone().requires_grad_(True) for t in (x, wgu, wd)]
+    plain = [t.clone().requires_grad_(True) for t in (x, wgu, wd)]
+    y1 = mxfp8gg.moe_ffn(*fused, offs)
+    y1.backward(dy)
+    y2 = mxfp8gg.moe_ffn_unfused(*plain, offs)
+    y2.backward(dy)
+    for got, want in [(y1, y2)] + [(a.grad, b.grad) for a, b in zip(fused, plain)]:
+        assert got.shape == want.shape
+        assert _rel(got, want) < 1e-2
+        assert (got == want).float().mean().item() > 0.99

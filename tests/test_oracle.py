@@ -338,3 +338,81 @@ def test_c1_golden_fixture():
     probe = np.array(fx["y_probe"])
     idx = np.array(fx["y_probe_index"])
     assert np.allclose(y[idx[:, 0], idx[:, 1]], probe, rtol=0, atol=1e-9)
+
+
+# ---------------------------------------------------------------------------
+# SwiGLU activation (expert FFN): pinned against torch's CPU bf16 eager ops
+# and autograd (an independent implementation with its own exp), and against
+# the float64 closed form of the derivative.
+# ---------------------------------------------------------------------------
+def _bf16_inputs(n, seed, scale=3.0):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(n, generator=g) * scale).to(torch.bfloat16)
+    return x, x.view(torch.int16).numpy().view(np.uint16)
+
+
+def _ulp_diff(a_bits, b_bits):
+    a = a_bits.astype(np.int32)
+    b = b_bits.astype(np.int32)
+    sa = np.where(a & 0x8000, -(a & 0x7FFF), a)
+    sb = np.where(b & 0x8000, -(b & 0x7FFF), b)
+    return np.abs(sa - sb)
+
+
+def test_swiglu_fwd_matches_torch_cpu_bf16():
+    gt, gb = _bf16_inputs(200000, 1)
+    ut, ub = _bf16_inputs(200000, 2, 1.0)
+    ref = (torch.nn.functional.silu(gt) * ut).view(torch.int16).numpy().view(np.uint16)
+    got = O.swiglu_fwd(gb, ub)
+    diff = _ulp_diff(got, ref)
+    assert diff.max() <= 1
+    assert (diff > 0).mean() < 1e-3  # exp implementations may differ in the last fp32 bit
+
+
+def test_swiglu_bwd_matches_torch_cpu_autograd():
+    gt, gb = _bf16_inputs(100000, 3)
+    ut, ub = _bf16_inputs(100000, 4, 1.0)
+    dt, db = _bf16_inputs(100000, 5, 0.01)
+    g_ = gt.clone().requires_grad_(True)
+    u_ = ut.clone().requires_grad_(True)
+    a = torch.nn.functional.silu(g_) * u_
+    a.backward(dt)
+    a_o, dg_o, du_o = O.swiglu_bwd(gb, ub, db)
+    for got, ref in ((a_o, a), (dg_o, g_.grad), (du_o, u_.grad)):
+        r = ref.detach().view(torch.int16).numpy().view(np.uint16)
+        diff = _ulp_diff(got, r)
+        assert diff.max() <= 1
+        assert (diff > 0).mean() < 1e-3
+
+
+def test_swiglu_derivative_closed_form_float64():
+    # d/dg [g * sigmoid(g) * u] = u * sig * (1 + g * (1 - sig)); d/du = silu(g)
+    gt, gb = _bf16_inputs(50000, 6)
+    ut, ub = _bf16_inputs(50000, 7, 1.0)
+    dt, db = _bf16_inputs(50000, 8, 0.01)
+    g = gt.double().numpy()
+    u = ut.double().numpy()
+    d = dt.double().numpy()
+    sig = 1.0 / (1.0 + np.exp(-g))
+    dg_ref = d * u * sig * (1.0 + g * (1.0 - sig))
+    du_ref = d * g * sig
+    a_ref = g * sig * u
+    a_o, dg_o, du_o = (O.bits_to_f32(x).astype(np.float64) for x in O.swiglu_bwd(gb, ub, db))
+    # three bf16 roundings in a chain: within 4 bf16 half-ulps of the exact value
+    for got, ref in ((a_o, a_ref), (dg_o, dg_ref), (du_o, du_ref)):
+        assert np.all(np.abs(got - ref) <= 2.0 ** -7 * np.abs(ref) + 1e-30)
+    # the forward of the backward oracle is the forward oracle
+    assert np.array_equal(O.swiglu_bwd(gb, ub, db)[0], O.swiglu_fwd(gb, ub))
+
+
+def test_swiglu_special_points():
+    g = np.array([0.0, 20.0, -20.0, np.inf, -np.inf, np.nan], np.float32)
+    u = np.ones_like(g)
+    d = np.ones_like(g)
+    gb = O.f32_to_bits(g)
+    a, dg, du = (O.bits_to_f32(x) for x in O.swiglu_bwd(gb, O.f32_to_bits(u), O.f32_to_bits(d)))
+    assert a[0] == 0 and du[0] == 0 and dg[0] == 0.5          # silu(0) = 0, silu'(0) = 1/2
+    assert a[1] == 20.0 and dg[1] == 1.0                       # sig(20) rounds to 1 in bf16 math
+    assert abs(a[2]) < 1e-7 and abs(dg[2]) < 1e-6
+    assert a[3] == np.inf and np.isnan(a[4])                   # -inf / (1 + inf) = NaN
+    assert np.isnan(a[5]) and np.isnan(dg[5]) and np.isnan(du[5])
