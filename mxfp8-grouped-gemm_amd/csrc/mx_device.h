@@ -29,16 +29,14 @@ template <int MODE>
 __device__ __forceinline__ uint32_t e8m0_from_amax16(uint32_t amax16) {
   const uint32_t ex = amax16 >> 7;
   const uint32_t mant = amax16 & 0x7Fu;
-  if (ex == 255u) return mant ? 255u : (MODE == kModeRceil ? 254u : 247u);
-  if (MODE == kModeRceil) {
-    // amax/448 <= 2^j  <=>  amax <= 1.75 * 2^(j+8).  With amax = 1.m * 2^(ex-127):
-    // j = ex-135 when 1.m <= 1.75 (mant <= 0x60), else ex-134.  b = j + 127.
-    int b = (int)ex - 8 + (mant > 0x60u ? 1 : 0);
-    return (uint32_t)(b < 0 ? 0 : (b > 254 ? 254 : b));
-  } else {
-    int b = (int)ex - 8;
-    return (uint32_t)(b < 0 ? 0 : b);
-  }
+  // RCEIL: amax/448 <= 2^j  <=>  amax <= 1.75 * 2^(j+8).  With amax = 1.m *
+  // 2^(ex-127): j = ex-135 when 1.m <= 1.75 (mant <= 0x60), else ex-134; b = j + 127.
+  // FLOOR: b = ex - 8.  Both clamp at 0; Inf gives 254 (RCEIL) / 247 (FLOOR),
+  // NaN 255.  Written as selects: no branch per block.
+  const int nb = (int)ex - 8 + (MODE == kModeRceil && mant > 0x60u ? 1 : 0);
+  const uint32_t finite = (uint32_t)(nb < 0 ? 0 : (nb > 254 ? 254 : nb));
+  const uint32_t special = mant ? 255u : (MODE == kModeRceil ? 254u : 247u);
+  return ex == 255u ? special : finite;
 }
 
 // Power-of-two exponent applied to the payload for a given scale byte.
@@ -107,37 +105,69 @@ __device__ __forceinline__ uint32_t amax16_of_word(uint32_t w) {
   return lo > hi ? lo : hi;
 }
 
+// Lane-wise max of two pairs of 16-bit integers (v_pk_max_u16).
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
+
+// |x| bit patterns of the two bf16 of a word, still packed.
+__device__ __forceinline__ uint32_t abs_bf16x2(uint32_t w) { return w & 0x7FFF7FFFu; }
+
 // amax16 of the eight bf16 values of a 16-byte chunk.
 __device__ __forceinline__ uint32_t amax16_of_chunk(const uint4& v) {
-  uint32_t am = amax16_of_word(v.x);
-  am = max(am, amax16_of_word(v.y));
-  am = max(am, amax16_of_word(v.z));
-  return max(am, amax16_of_word(v.w));
+  const uint32_t m = pk_max_u16(pk_max_u16(abs_bf16x2(v.x), abs_bf16x2(v.y)),
+                                pk_max_u16(abs_bf16x2(v.z), abs_bf16x2(v.w)));
+  return max(m & 0xFFFFu, m >> 16);
 }
 
 // Payload bytes of four values (bf16 values widened to float) of a block with
-// scale byte b.  b == 255 exactly when the block holds a NaN (both modes), so
-// every other block takes the short path: scale, clamp, convert.
+// scale byte b, for a block without NaN (b != 255): scale, clamp, convert.
 template <int MODE, bool SW>
-__device__ __forceinline__ uint32_t encode4(float x0, float x1, float x2, float x3, uint32_t b) {
-  if (b != 255u) {
-    const int e = payload_exponent<MODE>(b);
-    const float y0 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x0, e), -448.0f), 448.0f);
-    const float y1 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x1, e), -448.0f), 448.0f);
-    const float y2 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x2, e), -448.0f), 448.0f);
-    const float y3 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x3, e), -448.0f), 448.0f);
-    if (SW)
-      return e4m3_encode_sw(y0) | (e4m3_encode_sw(y1) << 8) | (e4m3_encode_sw(y2) << 16) |
-             (e4m3_encode_sw(y3) << 24);
-    uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
-    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y2, y3, (int)w, true);
-  }
+__device__ __forceinline__ uint32_t encode4_finite(float x0, float x1, float x2, float x3,
+                                                   uint32_t b) {
+  int e = payload_exponent<MODE>(b);
+  asm("" : "+v"(e));  // one exponent per block: keep it out of the per-value code
+  const float y0 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x0, e), -448.0f), 448.0f);
+  const float y1 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x1, e), -448.0f), 448.0f);
+  const float y2 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x2, e), -448.0f), 448.0f);
+  const float y3 = __builtin_fminf(__builtin_fmaxf(__builtin_ldexpf(x3, e), -448.0f), 448.0f);
+  if (SW)
+    return e4m3_encode_sw(y0) | (e4m3_encode_sw(y1) << 8) | (e4m3_encode_sw(y2) << 16) |
+           (e4m3_encode_sw(y3) << 24);
+  const uint32_t w = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y2, y3, (int)w, true);
+}
+
+// The same for any block, NaN blocks included (b == 255 in both modes exactly
+// when the block holds a NaN): NaN values keep their sign as code 0x7F | sign,
+// and FLOOR divides a NaN block by +inf.
+template <int MODE, bool SW>
+__device__ __forceinline__ uint32_t encode4_any(float x0, float x1, float x2, float x3,
+                                                uint32_t b) {
   const int e = payload_exponent<MODE>(b);
+  const bool floor_nan = MODE == kModeFloor && b == 255u;
   float y[4] = {x0, x1, x2, x3};
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    y[i] = MODE == kModeFloor ? floor_nan_block_value(y[i]) : scale_and_clamp(y[i], e);
+    y[i] = floor_nan ? floor_nan_block_value(y[i]) : scale_and_clamp(y[i], e);
   return e4m3_pack4<SW>(y[0], y[1], y[2], y[3]);
+}
+
+// Per-lane choice between the two.
+template <int MODE, bool SW>
+__device__ __forceinline__ uint32_t encode4(float x0, float x1, float x2, float x3, uint32_t b) {
+  return b != 255u ? encode4_finite<MODE, SW>(x0, x1, x2, x3, b)
+                   : encode4_any<MODE, SW>(x0, x1, x2, x3, b);
+}
+
+// Compile-time choice: ANY = the wave holds a NaN block somewhere.
+template <int MODE, bool SW, bool ANY>
+__device__ __forceinline__ uint32_t encode4_sel(float x0, float x1, float x2, float x3,
+                                                uint32_t b) {
+  return ANY ? encode4_any<MODE, SW>(x0, x1, x2, x3, b)
+             : encode4_finite<MODE, SW>(x0, x1, x2, x3, b);
 }
 
 // Two bf16 packed in a word, widened to float.

@@ -10,7 +10,10 @@
 // directly; no bf16 intermediate goes through HBM.
 //
 // Arithmetic is torch's eager bf16 semantics for the same expression
-// (F.silu(gate) * up with autograd), so the fused path equals the unfused one:
+// (F.silu(gate) * up with autograd), so the fused path equals the unfused one
+// (bit for bit on the GPU in the tests; the quotients below come from a
+// corrected reciprocal, which matches the IEEE quotient except in rare
+// near-tie cases, and bf16 rounding is the hardware round-to-nearest-even):
 //   s      = bf16(g / (1 + exp(-g)))                 (silu, fp32 inside)
 //   a      = bf16(s * u)
 //   d_up   = bf16(da * s)
@@ -25,10 +28,20 @@
 namespace mxgg {
 namespace {
 
+// a / b from the hardware reciprocal and one Newton step on the residual
+// (fma), the classic correction that returns the correctly rounded quotient
+// except in rare near-tie cases; infinities and NaN fall back to a * rcp(b).
+__device__ __forceinline__ float div_nr(float a, float b) {
+  const float r = __builtin_amdgcn_rcpf(b);
+  const float q = a * r;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-q, b, a), r, q);
+  return q1 == q1 ? q1 : q;
+}
+
 // a for the two values of a word of gate and up (packed bf16 result).
 __device__ __forceinline__ uint32_t swiglu_a_word(uint32_t gw, uint32_t uw) {
   const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
-  const uint32_t sw = pack_bf16x2(g0 / (1.0f + expf(-g0)), g1 / (1.0f + expf(-g1)));
+  const uint32_t sw = pack_bf16x2(div_nr(g0, 1.0f + expf(-g0)), div_nr(g1, 1.0f + expf(-g1)));
   return pack_bf16x2(bf16_lo(sw) * bf16_lo(uw), bf16_hi(sw) * bf16_hi(uw));
 }
 
@@ -42,7 +55,7 @@ struct ActWord {
 };
 
 __device__ __forceinline__ float dsilu_term(float ds, float g, float ex) {
-  const float sig = 1.0f / (1.0f + ex);
+  const float sig = div_nr(1.0f, 1.0f + ex);
   return ds * sig * (1.0f + g * (1.0f - sig));
 }
 
@@ -52,7 +65,7 @@ __device__ __forceinline__ ActWord swiglu_bwd_word(uint32_t gw, uint32_t uw, uin
   const float u0 = bf16_lo(uw), u1 = bf16_hi(uw);
   const float d0 = bf16_lo(dw), d1 = bf16_hi(dw);
   const float e0 = expf(-g0), e1 = expf(-g1);
-  const uint32_t sw = pack_bf16x2(g0 / (1.0f + e0), g1 / (1.0f + e1));  // s = bf16(silu(g))
+  const uint32_t sw = pack_bf16x2(div_nr(g0, 1.0f + e0), div_nr(g1, 1.0f + e1));  // s = bf16(silu(g))
   const uint32_t dsw = pack_bf16x2(d0 * u0, d1 * u1);                   // bf16(grad_a * up)
   const float s0 = bf16_lo(sw), s1 = bf16_hi(sw);
   ActWord r;
@@ -149,11 +162,6 @@ __device__ __forceinline__ float half_f(const uint2& v, int j) {
   return (j & 1) ? bf16_hi(w) : bf16_lo(w);
 }
 
-__device__ __forceinline__ uint32_t half_bits(const uint2& v, int j) {
-  const uint32_t w = (j >> 1) == 0 ? v.x : v.y;
-  return (w >> (16 * (j & 1))) & 0x7FFFu;
-}
-
 // Writes n <= 8 scale bytes b[j] at p[j * stride], as one 8-byte store when
 // all eight are contiguous and aligned.
 __device__ __forceinline__ void store_scale8(uint8_t* p, int64_t stride, const uint32_t (&b)[8],
@@ -171,27 +179,49 @@ __device__ __forceinline__ void store_scale8(uint8_t* p, int64_t stride, const u
 // Token-axis cast of the lane's 4 features x 8 positions held in v[0..7]:
 // feature j goes to row j of `qrow` (8 payload bytes; qrow already points at
 // column P of the lane's first feature row) and its scale byte to srow[j *
-// st_row]; the lane with tg == 0 writes the 4 scale bytes.
+// st_row]; the lane with tg == 0 writes the 4 scale bytes.  ANY: some block
+// of the wave holds a NaN (decided once per wave, so the common case runs the
+// short encoder without per-lane branches).
+template <int MODE, bool SW, bool ANY>
+__device__ __forceinline__ void token_axis_payload(const uint2 (&v)[8], const uint32_t (&bytes)[4],
+                                                   uint8_t* qrow, int64_t ldqt, bool out_ok) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = encode4_sel<MODE, SW, ANY>(half_f(v[0], j), half_f(v[1], j),
+                                                   half_f(v[2], j), half_f(v[3], j), bytes[j]);
+    const uint32_t hi = encode4_sel<MODE, SW, ANY>(half_f(v[4], j), half_f(v[5], j),
+                                                   half_f(v[6], j), half_f(v[7], j), bytes[j]);
+    if (out_ok) *reinterpret_cast<uint2*>(qrow + j * ldqt) = make_uint2(lo, hi);
+  }
+}
+
 template <int MODE, bool SW>
 __device__ __forceinline__ void emit_token_axis(const uint2 (&v)[8], uint8_t* qrow, int64_t ldqt,
                                                 uint8_t* srow, int64_t st_row, bool out_ok,
                                                 bool scale_lane) {
-  uint32_t bytes[4];
+  // amax of both features of a word at once (packed 16-bit max), combined
+  // over the four lanes of the 32-token block.
+  uint32_t mx = 0, my = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    uint32_t am = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) am = max(am, half_bits(v[i], j));
-    am = max(am, (uint32_t)__shfl_xor((int)am, 1));
-    am = max(am, (uint32_t)__shfl_xor((int)am, 2));
-    const uint32_t b = e8m0_from_amax16<MODE>(am);
-    bytes[j] = b;
-    const uint32_t lo = encode4<MODE, SW>(half_f(v[0], j), half_f(v[1], j), half_f(v[2], j),
-                                          half_f(v[3], j), b);
-    const uint32_t hi = encode4<MODE, SW>(half_f(v[4], j), half_f(v[5], j), half_f(v[6], j),
-                                          half_f(v[7], j), b);
-    if (out_ok) *reinterpret_cast<uint2*>(qrow + j * ldqt) = make_uint2(lo, hi);
+  for (int i = 0; i < 8; ++i) {
+    mx = pk_max_u16(mx, abs_bf16x2(v[i].x));
+    my = pk_max_u16(my, abs_bf16x2(v[i].y));
   }
+  mx = pk_max_u16(mx, (uint32_t)__shfl_xor((int)mx, 1));
+  my = pk_max_u16(my, (uint32_t)__shfl_xor((int)my, 1));
+  mx = pk_max_u16(mx, (uint32_t)__shfl_xor((int)mx, 2));
+  my = pk_max_u16(my, (uint32_t)__shfl_xor((int)my, 2));
+  uint32_t bytes[4];
+  bytes[0] = e8m0_from_amax16<MODE>(mx & 0xFFFFu);
+  bytes[1] = e8m0_from_amax16<MODE>(mx >> 16);
+  bytes[2] = e8m0_from_amax16<MODE>(my & 0xFFFFu);
+  bytes[3] = e8m0_from_amax16<MODE>(my >> 16);
+  const bool nan = (bytes[0] == 255u) | (bytes[1] == 255u) | (bytes[2] == 255u) |
+                   (bytes[3] == 255u);
+  if (__any(nan))
+    token_axis_payload<MODE, SW, true>(v, bytes, qrow, ldqt, out_ok);
+  else
+    token_axis_payload<MODE, SW, false>(v, bytes, qrow, ldqt, out_ok);
   if (out_ok && scale_lane) {
     if (st_row == 1 && (reinterpret_cast<uintptr_t>(srow) & 3u) == 0) {
       *reinterpret_cast<uint32_t*>(srow) =
@@ -206,24 +236,63 @@ __device__ __forceinline__ void emit_token_axis(const uint2 (&v)[8], uint8_t* qr
 // Row-wise cast of 4 features x 8 tokens (chunk v[i] of token i) into qrow
 // (row of the first token, already offset to the lane's column), scale bytes
 // into srow[i * s_row]; the eight lanes of a 32-feature block share amax.
+template <int MODE, bool SW, bool ANY>
+__device__ __forceinline__ void row_wise_payload(const uint2 (&v)[8], const uint32_t (&bytes)[8],
+                                                 uint8_t* qrow, int64_t ldq, int ntok) {
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    o[i] = encode4_sel<MODE, SW, ANY>(bf16_lo(v[i].x), bf16_hi(v[i].x), bf16_lo(v[i].y),
+                                      bf16_hi(v[i].y), bytes[i]);
+  if (ntok == 8) {  // every run but the last one of a group
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint32_t*>(qrow + i * ldq) = o[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i < ntok) *reinterpret_cast<uint32_t*>(qrow + i * ldq) = o[i];
+  }
+}
+
 template <int MODE, bool SW>
 __device__ __forceinline__ void emit_row_wise(const uint2 (&v)[8], uint8_t* qrow, int64_t ldq,
                                               uint8_t* srow, int64_t s_row, int ntok,
                                               bool scale_lane) {
+  // amax of each token's 4 features, two tokens packed per shuffle, combined
+  // over the eight lanes of the 32-feature block.
   uint32_t bytes[8];
+  bool nan = false;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    uint32_t am = max(amax16_of_word(v[i].x), amax16_of_word(v[i].y));
-    am = max(am, (uint32_t)__shfl_xor((int)am, 4));
-    am = max(am, (uint32_t)__shfl_xor((int)am, 8));
-    am = max(am, (uint32_t)__shfl_xor((int)am, 16));
-    const uint32_t b = e8m0_from_amax16<MODE>(am);
-    bytes[i] = b;
-    const uint32_t o = encode4<MODE, SW>(bf16_lo(v[i].x), bf16_hi(v[i].x), bf16_lo(v[i].y),
-                                         bf16_hi(v[i].y), b);
-    if (i < ntok) *reinterpret_cast<uint32_t*>(qrow + i * ldq) = o;
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t m0 = pk_max_u16(abs_bf16x2(v[2 * t].x), abs_bf16x2(v[2 * t].y));
+    const uint32_t m1 = pk_max_u16(abs_bf16x2(v[2 * t + 1].x), abs_bf16x2(v[2 * t + 1].y));
+    uint32_t m = max(m0 & 0xFFFFu, m0 >> 16) | (max(m1 & 0xFFFFu, m1 >> 16) << 16);
+    m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 4));
+    m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 8));
+    m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 16));
+    bytes[2 * t] = e8m0_from_amax16<MODE>(m & 0xFFFFu);
+    bytes[2 * t + 1] = e8m0_from_amax16<MODE>(m >> 16);
+    nan |= (bytes[2 * t] == 255u) | (bytes[2 * t + 1] == 255u);
   }
+  if (__any(nan))
+    row_wise_payload<MODE, SW, true>(v, bytes, qrow, ldq, ntok);
+  else
+    row_wise_payload<MODE, SW, false>(v, bytes, qrow, ldq, ntok);
   if (scale_lane && ntok > 0) store_scale8(srow, s_row, bytes, ntok);
+}
+
+// Optional bf16 copy of 8 token rows x 4 features (dh may be null).
+__device__ __forceinline__ void store_bf16_rows(const uint2 (&v)[8], uint16_t* dh, int64_t off,
+                                                int64_t ld, int ntok) {
+  if (dh == nullptr) return;
+  if (ntok == 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint2*>(dh + off + i * ld) = v[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (i < ntok) *reinterpret_cast<uint2*>(dh + off + i * ld) = v[i];
+  }
 }
 
 template <int MODE, bool SW>
@@ -269,19 +338,14 @@ __global__ __launch_bounds__(256) void k_swiglu_bwd(const SwigluBwdArgs p) {
     A[i] = make_uint2(r0.a, r1.a);
     DG[i] = make_uint2(r0.dg, r1.dg);
     DU[i] = make_uint2(r0.du, r1.du);
+    // One token at a time: interleaving all 32 exp/div chains would need far
+    // more registers than the occupancy of this streaming kernel allows.
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   const int64_t cols = p.cols;
-  if (p.dh != nullptr) {
-    uint16_t* row = p.dh + tok0 * p.lddh + f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if (i < ntok) {
-        *reinterpret_cast<uint2*>(row + i * p.lddh) = DG[i];
-        *reinterpret_cast<uint2*>(row + i * p.lddh + cols) = DU[i];
-      }
-    }
-  }
+  store_bf16_rows(DG, p.dh, tok0 * p.lddh + f, p.lddh, ntok);
+  store_bf16_rows(DU, p.dh, tok0 * p.lddh + cols + f, p.lddh, ntok);
 
   // Row-wise casts: d_gate into columns f.., d_up into columns cols + f.. of dq.
   const bool row_scale_lane = (fg & 7) == 0;

@@ -2,9 +2,10 @@
 through the C ABI.
 
 The activation is floating point: the kernel's bf16 results are compared with
-the CPU oracle (float32 math, bf16 rounding after every op) and with torch's
-own GPU eager ops, to at most one bf16 ulp in a small fraction of elements
-(exp implementations differ in the last fp32 bit).  Every cast the kernels
+the CPU oracle (float32 math, bf16 rounding after every op) to at most one
+bf16 ulp in a small fraction of elements (numpy's and the GPU's exp differ in
+the last fp32 bit), and with torch's own GPU eager ops, which they match bit
+for bit (at most one value in a million may differ by one ulp).  Every cast the kernels
 write is then checked bit for bit against the oracle's cast of the kernel's
 own bf16 values, so the quantisation parity is exact."""
 import numpy as np
@@ -18,7 +19,8 @@ from tests._helpers import bits, u8
 
 pytestmark = pytest.mark.gpu
 
-MAX_ULP_FRACTION = 1e-3
+MAX_ULP_FRACTION = 1e-3     # vs the numpy oracle
+TORCH_ULP_FRACTION = 1e-6   # vs torch's GPU eager ops
 
 
 def _ulp_diff(a_bits, b_bits):
@@ -34,13 +36,13 @@ def _ulp_diff(a_bits, b_bits):
     return d
 
 
-def _assert_bf16_close(got_bits, ref_bits, what):
+def _assert_bf16_close(got_bits, ref_bits, what, frac=MAX_ULP_FRACTION):
     assert got_bits.shape == ref_bits.shape
     if got_bits.size == 0:
         return
     d = _ulp_diff(got_bits, ref_bits)
     assert d.max() <= 1, f"{what}: {int(d.max())} ulp at {np.unravel_index(d.argmax(), d.shape)}"
-    assert (d > 0).mean() <= MAX_ULP_FRACTION, f"{what}: {(d > 0).mean():.2e} of values differ"
+    assert (d > 0).mean() <= frac, f"{what}: {(d > 0).mean():.2e} of values differ"
 
 
 def _h(gpu, M, F, seed, specials=False):
@@ -66,7 +68,7 @@ def test_swiglu_quant_dim0(gpu, mode_name, mode, M, F):
     a_ref = O.swiglu_fwd(hb[:, :F], hb[:, F:])
     _assert_bf16_close(bits(a), a_ref, "a vs oracle")
     torch_a = torch.nn.functional.silu(h[:, :F]) * h[:, F:]
-    _assert_bf16_close(bits(a), bits(torch_a), "a vs torch eager")
+    _assert_bf16_close(bits(a), bits(torch_a), "a vs torch eager", TORCH_ULP_FRACTION)
     rq, rs = O.quant_dim0(bits(a), mode)
     assert np.array_equal(u8(q), rq)
     assert np.array_equal(u8(s), rs)
@@ -103,8 +105,8 @@ def test_swiglu_backward_quant(gpu, mode_name, mode, sizes, F):
     gt = h[:, :F].clone().requires_grad_(True)
     ut = h[:, F:].clone().requires_grad_(True)
     (torch.nn.functional.silu(gt) * ut).backward(da)
-    _assert_bf16_close(dh[:, :F], bits(gt.grad), "d_gate vs torch autograd")
-    _assert_bf16_close(dh[:, F:], bits(ut.grad), "d_up vs torch autograd")
+    _assert_bf16_close(dh[:, :F], bits(gt.grad), "d_gate vs torch autograd", TORCH_ULP_FRACTION)
+    _assert_bf16_close(dh[:, F:], bits(ut.grad), "d_up vs torch autograd", TORCH_ULP_FRACTION)
     # every cast is bit-exact against the oracle cast of the kernel's own values
     rq, rs = O.quant_dim0(dh, mode)
     assert np.array_equal(u8(out["dh_q"]), rq)
