@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 4
+#define MXGG_ABI_VERSION 5
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -113,6 +113,24 @@ int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
                     int64_t rows_pad_cap, void* qt, int64_t ldqt,
                     void* scales_t, int64_t ldst, int scale_layout,
                     int32_t* group_ends_pad, int scale_mode, void* stream);
+
+/*
+ * Both casts of one bf16 matrix from a single read: the row-wise cast of
+ * mxgg_quant_dim0 (q, scales) and the token-axis cast of mxgg_quant_dim1
+ * (qt, scales_t, group_ends_pad), with the argument rules of each.  For
+ * operands that a training step contracts both ways: the layer input X and the
+ * output gradient dY (forward / dgrad vs wgrad), and expert weights viewed as
+ * [E*N, K] with group_ends = N, 2N, .. (forward vs dgrad).  cols % 32 == 0.
+ * Row-wise rows are written for the rows inside the groups (all rows when
+ * group_ends is NULL).  scale_layout applies to both scale outputs.
+ * Replaces the pair of torchao casts triton_to_mxfp8_dim0 / _dim1 that the
+ * reference's trainer path runs on the same tensor (port_mxfp8.py:43-49).
+ */
+int mxgg_quant_dual(const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                    const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap, void* q,
+                    int64_t ldq, void* scales, int64_t lds, void* qt, int64_t ldqt,
+                    void* scales_t, int64_t ldst, int scale_layout, int32_t* group_ends_pad,
+                    int scale_mode, void* stream);
 
 /*
  * SwiGLU activation fused with the row-wise MXFP8 cast of its output:

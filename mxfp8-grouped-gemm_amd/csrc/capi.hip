@@ -162,6 +162,61 @@ int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
       "quant_dim1");
 }
 
+int mxgg_quant_dual(const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                    const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap, void* q,
+                    int64_t ldq, void* scales, int64_t lds, void* qt, int64_t ldqt,
+                    void* scales_t, int64_t ldst, int scale_layout, int32_t* group_ends_pad,
+                    int scale_mode, void* stream) {
+  const int mode = scale_mode & 0xFF;
+  if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dual: unknown scale_mode %d", scale_mode);
+  if (!valid_layout(scale_layout))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dual: unknown scale_layout %d",
+                     scale_layout);
+  if (rows < 0 || cols < 0 || rows_pad_cap < 0)
+    return set_error(MXGG_ERR_SHAPE, "quant_dual: negative size");
+  if (cols % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "quant_dual: cols=%lld is not a multiple of 32",
+                     (long long)cols);
+  if (rows_pad_cap % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "quant_dual: rows_pad_cap=%lld is not a multiple of 32",
+                     (long long)rows_pad_cap);
+  if (group_ends) {
+    if (num_groups < 1 || num_groups > kMaxGroupsAbi)
+      return set_error(MXGG_ERR_UNSUPPORTED, "quant_dual: num_groups=%lld outside [1, %lld]",
+                       (long long)num_groups, (long long)kMaxGroupsAbi);
+    if (!group_ends_pad)
+      return set_error(MXGG_ERR_INVALID_ARGUMENT,
+                       "quant_dual: group_ends_pad is required with group_ends");
+  }
+  const int64_t need = ((rows + 31 * (group_ends ? num_groups : 0) + 31) / 32) * 32;
+  if (rows_pad_cap < need)
+    return set_error(MXGG_ERR_SHAPE, "quant_dual: rows_pad_cap=%lld < required %lld",
+                     (long long)rows_pad_cap, (long long)need);
+  if (cols == 0 || rows_pad_cap == 0) return MXGG_OK;
+  if (rows > 0 && (!x || !q || !scales))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dual: null x, q or scales");
+  if (!qt || !scales_t) return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dual: null qt");
+  const bool bm = scale_layout == MXGG_SCALES_BLOCK_MAJOR;
+  if (ldx < cols || ldq < cols || lds < (bm ? rows : cols / 32) || ldqt < rows_pad_cap ||
+      ldst < (bm ? cols : rows_pad_cap / 32))
+    return set_error(MXGG_ERR_SHAPE, "quant_dual: leading dimension smaller than the row");
+  if ((x && !aligned16(x)) || ldx % 8 != 0 || (q && (reinterpret_cast<uintptr_t>(q) & 7u) != 0) ||
+      ldq % 8 != 0 || !aligned16(qt) || ldqt % 16 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "quant_dual: x 16-byte aligned with ldx %% 8 == 0, q 8-byte aligned with ldq "
+                     "%% 8 == 0, qt 16-byte aligned with ldqt %% 16 == 0");
+  if (rows > INT32_MAX || rows_pad_cap > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "quant_dual: more than 2^31 rows");
+  return check_launch(
+      launch_quant_dual(static_cast<const uint16_t*>(x), rows, cols, ldx, group_ends,
+                        group_ends ? num_groups : 1, rows_pad_cap, static_cast<uint8_t*>(q), ldq,
+                        static_cast<uint8_t*>(scales), lds, static_cast<uint8_t*>(qt), ldqt,
+                        static_cast<uint8_t*>(scales_t), ldst, scale_layout, group_ends_pad,
+                        scale_mode, static_cast<hipStream_t>(stream)),
+      "quant_dual");
+}
+
 int mxgg_swiglu_quant_dim0(const void* gate, const void* up, int64_t ldh, int64_t rows,
                            int64_t cols, void* a_out, int64_t lda, void* q, int64_t ldq,
                            void* scales, int64_t lds, int scale_layout, int scale_mode,

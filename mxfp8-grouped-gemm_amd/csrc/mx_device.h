@@ -155,14 +155,9 @@ __device__ __forceinline__ uint32_t encode4_any(float x0, float x1, float x2, fl
   return e4m3_pack4<SW>(y[0], y[1], y[2], y[3]);
 }
 
-// Per-lane choice between the two.
-template <int MODE, bool SW>
-__device__ __forceinline__ uint32_t encode4(float x0, float x1, float x2, float x3, uint32_t b) {
-  return b != 255u ? encode4_finite<MODE, SW>(x0, x1, x2, x3, b)
-                   : encode4_any<MODE, SW>(x0, x1, x2, x3, b);
-}
-
-// Compile-time choice: ANY = the wave holds a NaN block somewhere.
+// Compile-time choice: ANY = the wave holds a NaN block somewhere (callers
+// test that once per wave with __any, so the common case has no per-lane
+// branch and no NaN handling).
 template <int MODE, bool SW, bool ANY>
 __device__ __forceinline__ uint32_t encode4_sel(float x0, float x1, float x2, float x3,
                                                 uint32_t b) {
@@ -174,11 +169,13 @@ __device__ __forceinline__ uint32_t encode4_sel(float x0, float x1, float x2, fl
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// Payload bytes of the eight bf16 values of a chunk under block byte b.
-template <int MODE, bool SW>
+// Payload bytes of the eight bf16 values of a chunk under block byte b
+// (ANY: NaN blocks possible, see encode4_sel).
+template <int MODE, bool SW, bool ANY>
 __device__ __forceinline__ uint2 encode_chunk8(const uint4& v, uint32_t b) {
-  return make_uint2(encode4<MODE, SW>(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y), b),
-                    encode4<MODE, SW>(bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w), b));
+  return make_uint2(
+      encode4_sel<MODE, SW, ANY>(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y), b),
+      encode4_sel<MODE, SW, ANY>(bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w), b));
 }
 
 // Two floats rounded to bf16 (round to nearest even, v_cvt_pk_bf16_f32) and

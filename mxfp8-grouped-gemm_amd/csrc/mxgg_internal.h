@@ -39,6 +39,15 @@ hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int6
                              int64_t ldst, int layout, int32_t* group_ends_pad, int mode,
                              hipStream_t stream);
 
+// Both casts from one read: row-wise (q, s: as launch_quant_dim0, rows inside
+// groups) and token-axis (qt, st: as launch_quant_dim1).  q == nullptr gives the
+// token-axis cast alone.
+hipError_t launch_quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                             const int32_t* group_ends, int64_t num_groups,
+                             int64_t rows_pad_cap, uint8_t* q, int64_t ldq, uint8_t* s,
+                             int64_t lds, uint8_t* qt, int64_t ldqt, uint8_t* st, int64_t ldst,
+                             int layout, int32_t* group_ends_pad, int mode, hipStream_t stream);
+
 // Padded cumulative group ends of the token-axis casts (one workgroup).
 hipError_t launch_pad_ends(const int32_t* group_ends, int64_t num_groups, int64_t rows,
                            int32_t* group_ends_pad, hipStream_t stream);

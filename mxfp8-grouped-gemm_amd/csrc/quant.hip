@@ -17,6 +17,22 @@ namespace {
 // of a quad hold one 32-element block and combine their amax with two xor
 // shuffles.  Each wave handles 4 rows per trip, a block 16 rows.
 // ---------------------------------------------------------------------------
+template <int MODE, bool SW, bool ANY>
+__device__ __forceinline__ void dim0_store(const uint4 (&v)[4], const uint32_t (&b)[4], uint8_t* q,
+                                           int64_t ldq, uint8_t* s, int64_t s_row, int64_t s_blk,
+                                           int64_t r0, int64_t rows, int cc, bool col_ok,
+                                           int lane) {
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t r = r0 + u;
+    const uint2 o = encode_chunk8<MODE, SW, ANY>(v[u], b[u]);
+    if (col_ok && r < rows) {
+      *reinterpret_cast<uint2*>(q + r * ldq + (int64_t)cc * 8) = o;
+      if ((lane & 3) == 0) s[r * s_row + (int64_t)(cc >> 2) * s_blk] = (uint8_t)b[u];
+    }
+  }
+}
+
 template <int MODE, bool SW>
 __global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__ x, int64_t rows,
                                                     int cols8, int64_t ldx,
@@ -38,19 +54,20 @@ __global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__
         v[u] = make_uint4(0, 0, 0, 0);
       }
     }
+    uint32_t b[4];
+    bool nan = false;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int64_t r = r0 + u;
       uint32_t am = amax16_of_chunk(v[u]);
       am = max(am, (uint32_t)__shfl_xor((int)am, 1));
       am = max(am, (uint32_t)__shfl_xor((int)am, 2));
-      const uint32_t b = e8m0_from_amax16<MODE>(am);
-      const uint2 o = encode_chunk8<MODE, SW>(v[u], b);
-      if (col_ok && r < rows) {
-        *reinterpret_cast<uint2*>(q + r * ldq + (int64_t)cc * 8) = o;
-        if ((lane & 3) == 0) s[r * s_row + (int64_t)(cc >> 2) * s_blk] = (uint8_t)b;
-      }
+      b[u] = e8m0_from_amax16<MODE>(am);
+      nan |= b[u] == 255u;
     }
+    if (__any(nan))
+      dim0_store<MODE, SW, true>(v, b, q, ldq, s, s_row, s_blk, r0, rows, cc, col_ok, lane);
+    else
+      dim0_store<MODE, SW, false>(v, b, q, ldq, s, s_row, s_blk, r0, rows, cc, col_ok, lane);
   }
 }
 
@@ -118,19 +135,65 @@ __global__ __launch_bounds__(256) void k_pad_ends(const int32_t* __restrict__ en
 // (tg = lane % 8, fg = lane / 8) owns positions 16*tg .. +15 of the tile and
 // features 8*fg .. +7.  It loads its 16 token rows as 16-byte vectors (eight
 // lanes read one whole 128-byte line of a row), takes each feature's amax over
-// its 16 tokens, combines it with lane tg^1 (the other half of the 32-token
-// block), and writes 16 payload bytes per feature (eight lanes write one whole
-// 128-byte line of an output row).  No LDS transpose is needed.  Padded
-// positions map to tokens through the padded group ends; a run of 16 never
-// straddles two groups because every group starts on a multiple of 32.
-// A workgroup is 4 waves along the features (128 positions x 256 features).
+// its 16 tokens (two features at once with packed 16-bit max), combines it
+// with lane tg^1 (the other half of the 32-token block), and writes 16 payload
+// bytes per feature (eight lanes write one whole 128-byte line of an output
+// row).  No LDS transpose is needed.  Padded positions map to tokens through
+// the padded group ends; a run of 16 never straddles two groups because every
+// group starts on a multiple of 32.  A workgroup is 4 waves along the
+// features (128 positions x 256 features).
+//
+// ROW (the dual cast) also writes the row-wise cast of the same data from the
+// same registers: for each of its tokens a lane holds one 8-feature chunk, the
+// four lanes fg = 4k .. 4k+3 hold a 32-feature block (amax over xor-8 / xor-16
+// shuffles, two tokens per shuffle).  Every token inside a group is covered by
+// exactly one lane run, so each row-wise row is written once.
 // ---------------------------------------------------------------------------
-template <int MODE, bool SW>
+// Row-wise payload of a lane's 16 token chunks (row i at qrow + i * ldq).
+template <int MODE, bool SW, bool ANY>
+__device__ __forceinline__ void row_payload(const uint4 (&v)[16], const uint32_t (&rb)[16],
+                                            uint8_t* qrow, int64_t ldq, int ntok) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (i < ntok)
+      *reinterpret_cast<uint2*>(qrow + i * ldq) = encode_chunk8<MODE, SW, ANY>(v[i], rb[i]);
+}
+
+// Token-axis payload: feature j (half j & 1 of word j >> 1) of 16 positions,
+// 16 bytes at row j of qrow.
+template <int MODE, bool SW, bool ANY>
+__device__ __forceinline__ void token_payload(const uint4 (&v)[16], const uint32_t (&bytes)[8],
+                                              uint8_t* qrow, int64_t ldqt, bool out_ok) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float y[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = 4 * k + u;
+        const uint32_t w = (j >> 1) == 0 ? v[i].x : (j >> 1) == 1 ? v[i].y : (j >> 1) == 2 ? v[i].z : v[i].w;
+        y[u] = (j & 1) ? bf16_hi(w) : bf16_lo(w);
+      }
+      o[k] = encode4_sel<MODE, SW, ANY>(y[0], y[1], y[2], y[3], bytes[j]);
+    }
+    if (out_ok) *reinterpret_cast<uint4*>(qrow + (int64_t)j * ldqt) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+struct RowOut {
+  uint8_t* q;     // [rows, cols] row-wise payload
+  uint8_t* s;     // scale bytes, byte (r, b) at s[r * s_row + b * s_blk]
+  int64_t ldq, s_row, s_blk;
+};
+
+template <int MODE, bool SW, bool ROW>
 __global__ __launch_bounds__(256) void k_quant_dim1(
     const uint16_t* __restrict__ x, int64_t rows, int cols, int64_t ldx,
     const int32_t* __restrict__ ends, const int32_t* __restrict__ ends_pad, int E,
     int64_t rows_pad_cap, uint8_t* __restrict__ qt, int64_t ldqt, uint8_t* __restrict__ st,
-    int64_t st_row, int64_t st_blk) {
+    int64_t st_row, int64_t st_blk, RowOut ro) {
   __shared__ int32_t ends_s[kMaxGroups];
   __shared__ int32_t pend_s[kMaxGroups];
   const int lane = threadIdx.x & 63;
@@ -157,35 +220,67 @@ __global__ __launch_bounds__(256) void k_quant_dim1(
     v[i] = i < ntok ? *reinterpret_cast<const uint4*>(x + (tok0 + i) * ldx + f)
                     : make_uint4(0, 0, 0, 0);
   }
+
+  if (ROW) {
+    // Row-wise cast: block amax of token i in the low / high half of a word
+    // for tokens 2t / 2t + 1, so one shuffle serves two tokens.
+    uint32_t rb[16];
+    bool nan = false;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const uint32_t m0 = amax16_of_chunk(v[2 * t]);
+      const uint32_t m1 = amax16_of_chunk(v[2 * t + 1]);
+      uint32_t m = m0 | (m1 << 16);
+      m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 8));
+      m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 16));
+      rb[2 * t] = e8m0_from_amax16<MODE>(m & 0xFFFFu);
+      rb[2 * t + 1] = e8m0_from_amax16<MODE>(m >> 16);
+      nan |= (rb[2 * t] == 255u) | (rb[2 * t + 1] == 255u);
+    }
+    uint8_t* qrow = ro.q + tok0 * ro.ldq + f;
+    if (__any(nan))
+      row_payload<MODE, SW, true>(v, rb, qrow, ro.ldq, ntok);
+    else
+      row_payload<MODE, SW, false>(v, rb, qrow, ro.ldq, ntok);
+    if ((fg & 3) == 0 && ntok > 0) {
+      uint8_t* sp = ro.s + tok0 * ro.s_row + (int64_t)(f >> 5) * ro.s_blk;
+      if (ro.s_row == 1 && ntok == 16 && (reinterpret_cast<uintptr_t>(sp) & 15u) == 0) {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          w[k] = rb[4 * k] | (rb[4 * k + 1] << 8) | (rb[4 * k + 2] << 16) | (rb[4 * k + 3] << 24);
+        *reinterpret_cast<uint4*>(sp) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (i < ntok) sp[(int64_t)i * ro.s_row] = (uint8_t)rb[i];
+      }
+    }
+  }
+
+  if (ROW) __builtin_amdgcn_sched_barrier(0);  // keep the two casts' temporaries apart
+
+  // Token-axis cast: features 2k, 2k + 1 are the halves of word k.
   const bool out_ok = f < cols && P < rows_pad_cap;
   uint32_t bytes[8];
+  bool tnan = false;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int sh = 16 * (j & 1);
-    uint32_t am = 0;
+  for (int k = 0; k < 4; ++k) {
+    uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const uint32_t w = (j >> 1) == 0 ? v[i].x : (j >> 1) == 1 ? v[i].y : (j >> 1) == 2 ? v[i].z : v[i].w;
-      am = max(am, (w >> sh) & 0x7FFFu);
+      const uint32_t w = k == 0 ? v[i].x : k == 1 ? v[i].y : k == 2 ? v[i].z : v[i].w;
+      m = pk_max_u16(m, abs_bf16x2(w));
     }
-    am = max(am, (uint32_t)__shfl_xor((int)am, 1));
-    const uint32_t b = e8m0_from_amax16<MODE>(am);
-    bytes[j] = b;
-    uint32_t o[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float y[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = 4 * k + u;
-        const uint32_t w = (j >> 1) == 0 ? v[i].x : (j >> 1) == 1 ? v[i].y : (j >> 1) == 2 ? v[i].z : v[i].w;
-        y[u] = bf16_bits_to_f32((w >> sh) & 0xFFFFu);
-      }
-      o[k] = encode4<MODE, SW>(y[0], y[1], y[2], y[3], b);
-    }
-    if (out_ok)
-      *reinterpret_cast<uint4*>(qt + (int64_t)(f + j) * ldqt + P) = make_uint4(o[0], o[1], o[2], o[3]);
+    m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 1));
+    bytes[2 * k] = e8m0_from_amax16<MODE>(m & 0xFFFFu);
+    bytes[2 * k + 1] = e8m0_from_amax16<MODE>(m >> 16);
+    tnan |= (bytes[2 * k] == 255u) | (bytes[2 * k + 1] == 255u);
   }
+  if (__any(tnan))
+    token_payload<MODE, SW, true>(v, bytes, qt + (int64_t)f * ldqt + P, ldqt, out_ok);
+  else
+    token_payload<MODE, SW, false>(v, bytes, qt + (int64_t)f * ldqt + P, ldqt, out_ok);
   if (out_ok && (tg & 1) == 0) {
     uint8_t* sp = st + (int64_t)f * st_row + (P >> 5) * st_blk;
     if (st_row == 1 && (reinterpret_cast<uintptr_t>(sp) & 7u) == 0) {
@@ -209,19 +304,19 @@ hipError_t dim0_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
   return hipGetLastError();
 }
 
-template <int MODE, bool SW>
+template <int MODE, bool SW, bool ROW>
 hipError_t dim1_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
                      const int32_t* ends, int64_t E, int64_t cap, uint8_t* qt, int64_t ldqt,
                      uint8_t* st, int64_t st_row, int64_t st_blk, int32_t* ends_pad,
-                     hipStream_t stream) {
+                     const RowOut& ro, hipStream_t stream) {
   if (ends != nullptr) {
     hipLaunchKernelGGL(k_pad_ends, dim3(1), dim3(256), 0, stream, ends, (int)E, rows, ends_pad);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   dim3 grid((unsigned)((cap + 127) / 128), (unsigned)((cols + 255) / 256));
-  hipLaunchKernelGGL((k_quant_dim1<MODE, SW>), grid, dim3(256), 0, stream, x, rows, (int)cols, ldx,
-                     ends, ends_pad, (int)E, cap, qt, ldqt, st, st_row, st_blk);
+  hipLaunchKernelGGL((k_quant_dim1<MODE, SW, ROW>), grid, dim3(256), 0, stream, x, rows,
+                     (int)cols, ldx, ends, ends_pad, (int)E, cap, qt, ldqt, st, st_row, st_blk, ro);
   return hipGetLastError();
 }
 
@@ -267,16 +362,38 @@ hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int6
                              int64_t rows_pad_cap, uint8_t* qt, int64_t ldqt, uint8_t* st,
                              int64_t ldst, int layout, int32_t* group_ends_pad, int mode,
                              hipStream_t stream) {
+  return launch_quant_dual(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, nullptr, 0,
+                           nullptr, 0, qt, ldqt, st, ldst, layout, group_ends_pad, mode, stream);
+}
+
+hipError_t launch_quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                             const int32_t* group_ends, int64_t num_groups,
+                             int64_t rows_pad_cap, uint8_t* q, int64_t ldq, uint8_t* s,
+                             int64_t lds, uint8_t* qt, int64_t ldqt, uint8_t* st, int64_t ldst,
+                             int layout, int32_t* group_ends_pad, int mode, hipStream_t stream) {
   if (cols == 0 || rows_pad_cap == 0) return hipSuccess;
   const bool sw = (mode & kCvtSoftwareFlag) != 0;
   const int m = mode & 0xFF;
-  const int64_t st_row = layout == MXGG_SCALES_BLOCK_MAJOR ? 1 : ldst;
-  const int64_t st_blk = layout == MXGG_SCALES_BLOCK_MAJOR ? ldst : 1;
-#define MXGG_DIM1(MODE, SWF)                                                                   \
-  dim1_impl<MODE, SWF>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, qt, ldqt, st, \
-                       st_row, st_blk, group_ends_pad, stream)
-  if (m == kModeRceil) return sw ? MXGG_DIM1(kModeRceil, true) : MXGG_DIM1(kModeRceil, false);
-  return sw ? MXGG_DIM1(kModeFloor, true) : MXGG_DIM1(kModeFloor, false);
+  const bool bm = layout == MXGG_SCALES_BLOCK_MAJOR;
+  const int64_t st_row = bm ? 1 : ldst;
+  const int64_t st_blk = bm ? ldst : 1;
+  RowOut ro;
+  ro.q = q;
+  ro.s = s;
+  ro.ldq = ldq;
+  ro.s_row = bm ? 1 : lds;
+  ro.s_blk = bm ? lds : 1;
+#define MXGG_DIM1(MODE, SWF, ROWF)                                                             \
+  dim1_impl<MODE, SWF, ROWF>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, qt, ldqt, \
+                             st, st_row, st_blk, group_ends_pad, ro, stream)
+  if (q == nullptr) {
+    if (m == kModeRceil)
+      return sw ? MXGG_DIM1(kModeRceil, true, false) : MXGG_DIM1(kModeRceil, false, false);
+    return sw ? MXGG_DIM1(kModeFloor, true, false) : MXGG_DIM1(kModeFloor, false, false);
+  }
+  if (m == kModeRceil)
+    return sw ? MXGG_DIM1(kModeRceil, true, true) : MXGG_DIM1(kModeRceil, false, true);
+  return sw ? MXGG_DIM1(kModeFloor, true, true) : MXGG_DIM1(kModeFloor, false, true);
 #undef MXGG_DIM1
 }
 

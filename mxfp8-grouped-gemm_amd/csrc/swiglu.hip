@@ -81,6 +81,24 @@ __device__ __forceinline__ ActWord swiglu_bwd_word(uint32_t gw, uint32_t uw, uin
 // 16-byte vector each), a quad holds one 32-feature block, a wave 4 rows per
 // trip, a workgroup 16 rows.
 // ---------------------------------------------------------------------------
+template <int MODE, bool SW, bool ANY>
+__device__ __forceinline__ void swiglu_dim0_store(const uint4 (&a)[4], const uint32_t (&b)[4],
+                                                  uint16_t* a_out, int64_t lda, uint8_t* q,
+                                                  int64_t ldq, uint8_t* s, int64_t s_row,
+                                                  int64_t s_blk, int64_t r0, int64_t rows, int cc,
+                                                  bool col_ok, int lane) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t r = r0 + k;
+    const uint2 o = encode_chunk8<MODE, SW, ANY>(a[k], b[k]);
+    if (col_ok && r < rows) {
+      *reinterpret_cast<uint2*>(q + r * ldq + (int64_t)cc * 8) = o;
+      if ((lane & 3) == 0) s[r * s_row + (int64_t)(cc >> 2) * s_blk] = (uint8_t)b[k];
+      if (a_out != nullptr) *reinterpret_cast<uint4*>(a_out + r * lda + (int64_t)cc * 8) = a[k];
+    }
+  }
+}
+
 template <int MODE, bool SW>
 __global__ __launch_bounds__(256) void k_swiglu_dim0(
     const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up, int64_t ldh, int64_t rows,
@@ -103,21 +121,24 @@ __global__ __launch_bounds__(256) void k_swiglu_dim0(
         u[k] = make_uint4(0, 0, 0, 0);
       }
     }
+    uint4 a[4];
+    uint32_t b[4];
+    bool nan = false;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int64_t r = r0 + k;
-      const uint4 a = swiglu_a_chunk(g[k], u[k]);
-      uint32_t am = amax16_of_chunk(a);
+      a[k] = swiglu_a_chunk(g[k], u[k]);
+      uint32_t am = amax16_of_chunk(a[k]);
       am = max(am, (uint32_t)__shfl_xor((int)am, 1));
       am = max(am, (uint32_t)__shfl_xor((int)am, 2));
-      const uint32_t b = e8m0_from_amax16<MODE>(am);
-      const uint2 o = encode_chunk8<MODE, SW>(a, b);
-      if (col_ok && r < rows) {
-        *reinterpret_cast<uint2*>(q + r * ldq + (int64_t)cc * 8) = o;
-        if ((lane & 3) == 0) s[r * s_row + (int64_t)(cc >> 2) * s_blk] = (uint8_t)b;
-        if (a_out != nullptr) *reinterpret_cast<uint4*>(a_out + r * lda + (int64_t)cc * 8) = a;
-      }
+      b[k] = e8m0_from_amax16<MODE>(am);
+      nan |= b[k] == 255u;
     }
+    if (__any(nan))
+      swiglu_dim0_store<MODE, SW, true>(a, b, a_out, lda, q, ldq, s, s_row, s_blk, r0, rows, cc,
+                                        col_ok, lane);
+    else
+      swiglu_dim0_store<MODE, SW, false>(a, b, a_out, lda, q, ldq, s, s_row, s_blk, r0, rows, cc,
+                                         col_ok, lane);
   }
 }
 

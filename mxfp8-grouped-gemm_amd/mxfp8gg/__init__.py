@@ -14,11 +14,13 @@ from .ops import (
     grouped_mm,
     grouped_wgrad,
     padded_token_capacity,
+    quant_weight_dual,
     quant_weight_for_dgrad,
     swiglu_backward_quant,
     swiglu_quant,
     to_mxfp8_dim0,
     to_mxfp8_dim1,
+    to_mxfp8_dual,
     wgrad_fused,
     wgrad_kernel,
     wgrad_prepare,
@@ -35,9 +37,9 @@ from .torchao_compat import (
 
 __all__ = [
     "MxggError", "load_library",
-    "to_mxfp8_dim0", "to_mxfp8_dim1", "padded_token_capacity",
+    "to_mxfp8_dim0", "to_mxfp8_dim1", "to_mxfp8_dual", "padded_token_capacity",
     "grouped_mm", "grouped_wgrad", "grouped_dgrad", "quant_weight_for_dgrad",
-    "swiglu_quant", "swiglu_backward_quant",
+    "quant_weight_dual", "swiglu_quant", "swiglu_backward_quant",
     "fused_grouped_fwd", "fwd_ge", "wgrad_fused", "wgrad_prepare", "wgrad_kernel",
     "triton_to_mxfp8_dim0", "triton_to_mxfp8_dim1",
     "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",

@@ -31,7 +31,7 @@ OUT_F32 = 1
 SCALES_ROW_MAJOR = 0
 SCALES_BLOCK_MAJOR = 1
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -46,6 +46,11 @@ SIGNATURES = {
     "mxgg_quant_dim1": (
         _I,
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I, _P, _I, _P],
+    ),
+    "mxgg_quant_dual": (
+        _I,
+        [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I, _P, _I,
+         _P],
     ),
     "mxgg_swiglu_quant_dim0": (
         _I, [_P, _P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I, _I, _P],

@@ -23,34 +23,61 @@ from . import ops
 
 
 class MXFP8GroupedMM(torch.autograd.Function):
-    """y = grouped x . W^T with MXFP8 operands and fp32 accumulation."""
+    """y = grouped x . W^T with MXFP8 operands and fp32 accumulation.
+
+    Every operand that the backward pass contracts the other way is cast both
+    ways from one read (to_mxfp8_dual / quant_weight_dual): the forward keeps
+    the token-axis cast of x and the N-blocked cast of W for backward instead
+    of the bf16 tensors, and dY is cast once for dgrad and wgrad together."""
 
     @staticmethod
     def forward(ctx, x, w, offs, scaling_mode="rceil"):
         if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
             raise TypeError("x and w must be bfloat16")
         offs = ops._group_ends(offs, w.shape[0], x.device)
-        xq, xs = ops.to_mxfp8_dim0(x, scaling_mode)
-        wq, ws = ops.to_mxfp8_dim0(w, scaling_mode)
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        saved = [offs]
+        if need_dw:
+            xq, xs, xqt, xst, pad = ops.to_mxfp8_dual(x, offs, scaling_mode)
+            saved += [xqt, xst, pad]
+        else:
+            xq, xs = ops.to_mxfp8_dim0(x, scaling_mode)
+        if need_dx:
+            (wq, ws), (wt, wts) = ops.quant_weight_dual(w, scaling_mode)
+            saved += [wt, wts]
+        else:
+            wq, ws = ops.to_mxfp8_dim0(w, scaling_mode)
         y = ops.grouped_mm(xq, wq, offs, xs, ws, out_dtype=torch.bfloat16)
-        ctx.save_for_backward(x, w, offs)
+        ctx.save_for_backward(*saved)
         ctx.scaling_mode = scaling_mode
+        ctx.w_dtype = w.dtype
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x, w, offs = ctx.saved_tensors
+        need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        saved = list(ctx.saved_tensors)
+        offs = saved.pop(0)
+        if need_dw:
+            xqt, xst, pad = saved[:3]
+            saved = saved[3:]
+        if need_dx:
+            wt, wts = saved[:2]
         mode = ctx.scaling_mode
         dy = dy.to(torch.bfloat16)
         if dy.stride(-1) != 1:
             dy = dy.contiguous()
         dx = dw = None
-        if ctx.needs_input_grad[0]:
-            dx = ops.grouped_dgrad(dy, w, offs, scaling_mode=mode)
-        if ctx.needs_input_grad[1]:
-            go, gos, pad = ops.to_mxfp8_dim1(dy, offs, mode)
-            ia, ias, _ = ops.to_mxfp8_dim1(x, offs, mode)
-            dw = ops.grouped_wgrad(go, ia, pad, gos, ias, out_dtype=w.dtype)
+        if need_dx and need_dw:
+            dyq, dys, dyqt, dyst, _ = ops.to_mxfp8_dual(dy, offs, mode)
+        elif need_dx:
+            dyq, dys = ops.to_mxfp8_dim0(dy, mode)
+        elif need_dw:
+            dyqt, dyst, _ = ops.to_mxfp8_dim1(dy, offs, mode)
+        if need_dx:
+            dx = ops.grouped_mm(dyq, wt, offs, dys, wts, out_dtype=torch.bfloat16)
+        if need_dw:
+            dw = ops.grouped_wgrad(dyqt, xqt, pad, dyst, xst, out_dtype=ctx.w_dtype)
         return dx, dw, None, None
 
 
@@ -66,54 +93,70 @@ class MXFP8ExpertFFN(torch.autograd.Function):
     """y = (SiLU(x . Wg^T) * (x . Wu^T)) . Wd^T per expert group, every GEMM in
     MXFP8, the activation fused with the casts around it.
 
-    forward : x cast (dim0) -> gate+up GEMM -> h = [gate | up] (bf16, kept for
-              backward) -> SwiGLU + cast of a in one kernel -> down GEMM
-    backward: dA = dY . Wd (MXFP8 dgrad); one kernel turns (h, dA) into the
-              row-wise and token-axis casts of dh = [d_gate | d_up] and the
-              token-axis cast of a; then dWd = dY^T . a, dX = dh . Wgu and
-              dWgu = dh^T . X, all MXFP8.
+    forward : x and both weights cast both ways from one read each (the
+              token-axis / N-blocked casts are kept for backward) -> gate+up
+              GEMM -> h = [gate | up] (bf16, kept) -> SwiGLU + cast of a in
+              one kernel -> down GEMM
+    backward: dY cast both ways; dA = dY . Wd (MXFP8 dgrad); one kernel turns
+              (h, dA) into the row-wise and token-axis casts of dh =
+              [d_gate | d_up] and the token-axis cast of a; then dWd = dY^T . a,
+              dX = dh . Wgu and dWgu = dh^T . X, all MXFP8.
     """
 
     @staticmethod
     def forward(ctx, x, w_gate_up, w_down, offs, scaling_mode="rceil"):
-        for name, t in (("x", x), ("w_gate_up", w_gate_up), ("w_down", w_down)):
-            if t.dtype != torch.bfloat16:
-                raise TypeError(f"{name} must be bfloat16")
-        E, F2, H = w_gate_up.shape
-        if tuple(w_down.shape) != (E, H, F2 // 2) or x.shape[-1] != H:
-            raise ValueError("shapes must be x [M, H], w_gate_up [E, 2F, H], w_down [E, H, F]")
-        ends = ops._group_ends(offs, E, x.device)
-        xq, xs = ops.to_mxfp8_dim0(x, scaling_mode)
-        wq, ws = ops.to_mxfp8_dim0(w_gate_up, scaling_mode)
+        E, ends = _check_ffn(x, w_gate_up, w_down, offs)
+        xq, xs, xqt, xst, _ = ops.to_mxfp8_dual(x, ends, scaling_mode)
+        (wq, ws), (wgt, wgts) = ops.quant_weight_dual(w_gate_up, scaling_mode)
         h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
         aq, as_ = ops.swiglu_quant(h, scaling_mode)
-        dq, ds = ops.to_mxfp8_dim0(w_down, scaling_mode)
+        (dq, ds), (wdt, wdts) = ops.quant_weight_dual(w_down, scaling_mode)
         y = ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16)
-        ctx.save_for_backward(x, w_gate_up, w_down, ends, h)
+        ctx.save_for_backward(ends, h, xqt, xst, wgt, wgts, wdt, wdts)
         ctx.scaling_mode = scaling_mode
+        ctx.dtypes = (w_gate_up.dtype, w_down.dtype)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x, wgu, wd, ends, h = ctx.saved_tensors
+        ends, h, xqt, xst, wgt, wgts, wdt, wdts = ctx.saved_tensors
         mode = ctx.scaling_mode
         dy = dy.to(torch.bfloat16)
         if dy.stride(-1) != 1:
             dy = dy.contiguous()
-        da = ops.grouped_dgrad(dy, wd, ends, scaling_mode=mode)
+        dyq, dys, dyqt, dyst, _ = ops.to_mxfp8_dual(dy, ends, mode)
+        da = ops.grouped_mm(dyq, wdt, ends, dys, wdts, out_dtype=torch.bfloat16)
         act = ops.swiglu_backward_quant(h, da, ends, mode)
         pad = act["offs_pad"]
-        dwd = dwgu = dx = None
+        dx = dwgu = dwd = None
         if ctx.needs_input_grad[2]:
-            dyt, dyst, _ = ops.to_mxfp8_dim1(dy, ends, mode)
-            dwd = ops.grouped_wgrad(dyt, act["a_qt"], pad, dyst, act["a_st"], out_dtype=wd.dtype)
+            dwd = ops.grouped_wgrad(dyqt, act["a_qt"], pad, dyst, act["a_st"], out_dtype=ctx.dtypes[1])
         if ctx.needs_input_grad[0]:
-            wt, wts = ops.quant_weight_for_dgrad(wgu, mode)
-            dx = ops.grouped_mm(act["dh_q"], wt, ends, act["dh_s"], wts, out_dtype=torch.bfloat16)
+            dx = ops.grouped_mm(act["dh_q"], wgt, ends, act["dh_s"], wgts, out_dtype=torch.bfloat16)
         if ctx.needs_input_grad[1]:
-            xt, xst, _ = ops.to_mxfp8_dim1(x, ends, mode)
-            dwgu = ops.grouped_wgrad(act["dh_qt"], xt, pad, act["dh_st"], xst, out_dtype=wgu.dtype)
+            dwgu = ops.grouped_wgrad(act["dh_qt"], xqt, pad, act["dh_st"], xst,
+                                     out_dtype=ctx.dtypes[0])
         return dx, dwgu, dwd, None, None
+
+
+def _check_ffn(x, w_gate_up, w_down, offs):
+    for name, t in (("x", x), ("w_gate_up", w_gate_up), ("w_down", w_down)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16")
+    E, F2, H = w_gate_up.shape
+    if tuple(w_down.shape) != (E, H, F2 // 2) or x.shape[-1] != H:
+        raise ValueError("shapes must be x [M, H], w_gate_up [E, 2F, H], w_down [E, H, F]")
+    return E, ops._group_ends(offs, E, x.device)
+
+
+def _ffn_forward_only(x, w_gate_up, w_down, offs, scaling_mode):
+    _, ends = _check_ffn(x, w_gate_up, w_down, offs)
+    xq, xs = ops.to_mxfp8_dim0(x, scaling_mode)
+    wq, ws = ops.to_mxfp8_dim0(w_gate_up, scaling_mode)
+    h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
+    aq, as_ = ops.swiglu_quant(h, scaling_mode)
+    dq, ds = ops.to_mxfp8_dim0(w_down, scaling_mode)
+    return ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16)
 
 
 def moe_ffn(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,
@@ -124,6 +167,9 @@ def moe_ffn(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,
     projection w_down [E, H, F].  x: bf16 [M, H], tokens grouped by expert with
     cumulative ends `offs`.  Rows after the last group end get no output and no
     input gradient."""
+    if not torch.is_grad_enabled() or not any(
+            t.requires_grad for t in (x, w_gate_up, w_down)):
+        return _ffn_forward_only(x, w_gate_up, w_down, offs, scaling_mode)
     return MXFP8ExpertFFN.apply(x, w_gate_up, w_down, offs, scaling_mode)
 
 

@@ -248,6 +248,71 @@ def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mod
     return qt, st, ends_pad
 
 
+def to_mxfp8_dual(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mode="rceil"):
+    """Both MXFP8 casts of x from one read of it: the row-wise cast of
+    to_mxfp8_dim0 and the token-axis cast of to_mxfp8_dim1, for operands a
+    training step contracts both ways (X and dY of a grouped GEMM).
+
+    x: bf16 [M, C] (C % 32 == 0); offs: token group ends (int32 [E] on the
+    device) or None.  Returns (q, s, qt, st, offs_pad) with q, s as
+    to_mxfp8_dim0(x) (rows inside the groups) and qt, st, offs_pad as
+    to_mxfp8_dim1(x, offs)."""
+    _need_gpu(x, "x")
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] % 32 != 0:
+        raise TypeError("x must be a 2-D bfloat16 tensor [M, C] with C % 32 == 0")
+    M, C = x.shape
+    x2 = x if (x.stride(-1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0) else x.contiguous()
+    E = ends = ends_pad = None
+    if offs is not None:
+        E = offs.numel()
+        ends = _group_ends(offs, E, x.device)
+        ends_pad = torch.empty(E, dtype=torch.int32, device=x.device)
+    cap = padded_token_capacity(M, E)
+    q = torch.empty((M, C), dtype=_FP8, device=x.device)
+    sbuf = _block_major_buffer(M, C // 32, x.device)
+    qt = torch.empty((C, cap), dtype=_FP8, device=x.device)
+    stbuf = _block_major_buffer(C, cap // 32, x.device)
+    lib = _lib.load()
+    _lib.check(
+        lib.mxgg_quant_dual(
+            x2.data_ptr(), M, C, x2.stride(0),
+            ends.data_ptr() if ends is not None else None, E or 0, cap,
+            q.data_ptr(), C, sbuf.data_ptr(), sbuf.stride(0),
+            qt.data_ptr(), cap, stbuf.data_ptr(), stbuf.stride(0), _lib.SCALES_BLOCK_MAJOR,
+            ends_pad.data_ptr() if ends_pad is not None else None,
+            _mode(scaling_mode), _stream_ptr(x)),
+        "quant_dual",
+    )
+    return q, sbuf[:, :M].t(), qt, stbuf[:, :C].t(), ends_pad
+
+
+def _expert_ends(E: int, N: int, device) -> torch.Tensor:
+    return torch.arange(1, E + 1, dtype=torch.int32, device=device) * N
+
+
+def _weight_t_views(qt: torch.Tensor, st: torch.Tensor, E: int, N: int, K: int):
+    """[E, K, N] / [E, K, N/32] views of the token-axis cast of W viewed as
+    [E*N, K] with one group per expert (expert e = columns [e*N, (e+1)*N))."""
+    wt = qt.as_strided((E, K, N), (N, qt.stride(0), 1))
+    # st[k, b] lives at buf[b, k]: strides (1, ld); expert e starts at block-row e*N/32
+    wts = st.as_strided((E, K, N // 32), ((N // 32) * st.stride(1), st.stride(0), st.stride(1)))
+    return wt, wts
+
+
+def quant_weight_dual(w: torch.Tensor, scaling_mode="rceil"):
+    """Both casts of expert weights W [E, N, K] from one read: returns
+    ((wq, ws), (wt, wts)) equal to to_mxfp8_dim0(w) (forward operand, blocks
+    along K) and quant_weight_for_dgrad(w) (dgrad operand, blocks along N)."""
+    _need_gpu(w, "w")
+    if w.dtype != torch.bfloat16 or w.dim() != 3:
+        raise TypeError("w must be a 3-D bfloat16 tensor [E, N, K]")
+    E, N, K = w.shape
+    if N % 32 != 0:
+        raise ValueError(f"N={N} must be a multiple of 32 for MXFP8 blocks along N")
+    q, s, qt, st, _ = to_mxfp8_dual(w.reshape(E * N, K), _expert_ends(E, N, w.device), scaling_mode)
+    return (q.reshape(E, N, K), s.reshape(E, N, K // 32)), _weight_t_views(qt, st, E, N, K)
+
+
 # ---------------------------------------------------------------------------
 # SwiGLU fused with its casts (the expert FFN activation)
 # ---------------------------------------------------------------------------
@@ -608,12 +673,8 @@ def quant_weight_for_dgrad(w: torch.Tensor, scaling_mode="rceil"):
     E, N, K = w.shape
     if N % 32 != 0:
         raise ValueError(f"N={N} must be a multiple of 32 for MXFP8 blocks along N")
-    ends = torch.arange(1, E + 1, dtype=torch.int32, device=w.device) * N
-    qt, st, _ = to_mxfp8_dim1(w.reshape(E * N, K), ends, scaling_mode)
-    wt = qt.as_strided((E, K, N), (N, qt.stride(0), 1))
-    # st[k, b] lives at buf[b, k]: strides (1, ld); expert e starts at block-row e*N/32
-    wts = st.as_strided((E, K, N // 32), ((N // 32) * st.stride(1), st.stride(0), st.stride(1)))
-    return wt, wts
+    qt, st, _ = to_mxfp8_dim1(w.reshape(E * N, K), _expert_ends(E, N, w.device), scaling_mode)
+    return _weight_t_views(qt, st, E, N, K)
 
 
 def grouped_dgrad(dy: torch.Tensor, w: torch.Tensor | tuple, offs: torch.Tensor,

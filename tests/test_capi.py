@@ -173,6 +173,39 @@ def test_quant_dim1_rejects(lib, kw, status):
                                a["pad"], a["mode"], None) == status
 
 
+def _dual(lib, **kw):
+    a = dict(x=FAKE, rows=64, cols=64, ldx=64, ends=FAKE, E=2, cap=128, q=FAKE, ldq=64, s=FAKE,
+             lds=64, qt=FAKE, ldqt=128, st=FAKE, ldst=64, layout=BM, pad=FAKE, mode=0)
+    a.update(kw)
+    return lib.mxgg_quant_dual(a["x"], a["rows"], a["cols"], a["ldx"], a["ends"], a["E"],
+                               a["cap"], a["q"], a["ldq"], a["s"], a["lds"], a["qt"], a["ldqt"],
+                               a["st"], a["ldst"], a["layout"], a["pad"], a["mode"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(cols=40), _lib.ERR_SHAPE),                 # the row-wise cast needs cols % 32
+    (dict(cap=64), _lib.ERR_SHAPE),                  # below rows + 31 * groups
+    (dict(cap=100), _lib.ERR_SHAPE),
+    (dict(E=0), _lib.ERR_UNSUPPORTED),
+    (dict(pad=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(q=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(qt=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(mode=3), _lib.ERR_INVALID_ARGUMENT),
+    (dict(layout=5), _lib.ERR_INVALID_ARGUMENT),
+    (dict(lds=32), _lib.ERR_SHAPE),                  # block-major ld < rows
+    (dict(ldst=32), _lib.ERR_SHAPE),                 # block-major ld < cols
+    (dict(x=FAKE + 8), _lib.ERR_ALIGNMENT),
+    (dict(q=FAKE + 4), _lib.ERR_ALIGNMENT),
+    (dict(ldqt=136), _lib.ERR_ALIGNMENT),
+])
+def test_quant_dual_rejects(lib, kw, status):
+    assert _dual(lib, **kw) == status
+
+
+def test_quant_dual_empty_is_noop(lib):
+    assert _dual(lib, cols=0) == _lib.OK
+
+
 def _swiglu0(lib, **kw):
     a = dict(g=FAKE, u=FAKE + 128, ldh=128, rows=8, cols=64, aout=None, lda=64, q=FAKE, ldq=64,
              s=FAKE, lds=8, layout=BM, mode=0)

@@ -142,3 +142,75 @@ def test_dim1_c4_sampled_features(gpu):
     idx = torch.from_numpy(feats).to(gpu)
     assert np.array_equal(pad.cpu().numpy(), rpad)
     assert np.array_equal(u8(qt[idx]), rq) and np.array_equal(u8(st[idx]), rs)
+
+
+# ---------------------------------------------------------------------------
+# dual cast: both casts of one tensor from a single read
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("name,mode", MODES)
+@pytest.mark.parametrize("enc", ENCODERS)
+@pytest.mark.parametrize("sizes,cols", [([5, 0, 64, 33, 1, 40, 0], 96), ([128, 128], 64),
+                                        ([300], 288), ([0, 0, 7], 32)])
+def test_dual_matches_oracle(gpu, name, mode, enc, sizes, cols):
+    g = torch.Generator(device=gpu).manual_seed(17)
+    M = sum(sizes)
+    x = torch.randn(M, cols, generator=g, device=gpu) * 3
+    x = x * torch.exp2(torch.randint(-40, 40, (M, 1), generator=g, device=gpu).float())
+    if M > 50:
+        x[3, 2] = float("nan")
+        x[40, 5] = float("inf")
+        x[41, cols - 1] = -float("inf")
+    x = x.to(torch.bfloat16)
+    ends = workloads.ends_of(sizes)
+    q, s, qt, st, pad = ops.to_mxfp8_dual(x, torch.from_numpy(ends).to(gpu), mode | enc)
+    rq, rs = O.quant_dim0(bits(x), mode)
+    assert np.array_equal(u8(q), rq) and np.array_equal(u8(s), rs)
+    rqt, rst, rpad = O.quant_dim1(bits(x), ends, qt.shape[1], mode)
+    assert np.array_equal(pad.cpu().numpy(), rpad)
+    assert np.array_equal(u8(qt), rqt) and np.array_equal(u8(st), rst)
+
+
+def test_dual_ungrouped_and_partial_groups(gpu):
+    g = torch.Generator(device=gpu).manual_seed(18)
+    x = torch.randn(100, 64, generator=g, device=gpu).to(torch.bfloat16)
+    q, s, qt, st, pad = ops.to_mxfp8_dual(x)
+    assert pad is None
+    rq, rs = O.quant_dim0(bits(x), O.RCEIL)
+    assert np.array_equal(u8(q), rq) and np.array_equal(u8(s), rs)
+    rqt, rst, _ = O.quant_dim1(bits(x), None, qt.shape[1], O.RCEIL)
+    assert np.array_equal(u8(qt), rqt) and np.array_equal(u8(st), rst)
+    # groups ending before the last row: row-wise rows inside the groups only
+    ends = np.array([10, 10, 70], dtype=np.int32)
+    q, s, qt, st, pad = ops.to_mxfp8_dual(x, torch.from_numpy(ends).to(gpu))
+    assert np.array_equal(u8(q[:70]), rq[:70]) and np.array_equal(u8(s[:70]), rs[:70])
+    rqt, rst, _ = O.quant_dim1(bits(x), ends, qt.shape[1], O.RCEIL)
+    assert np.array_equal(u8(qt), rqt) and np.array_equal(u8(st), rst)
+
+
+@pytest.mark.parametrize("name,mode", MODES)
+def test_quant_weight_dual_equals_separate_casts(gpu, name, mode):
+    g = torch.Generator(device=gpu).manual_seed(19)
+    w = (torch.randn(3, 64, 96, generator=g, device=gpu) * 0.02).to(torch.bfloat16)
+    (wq, ws), (wt, wts) = mxfp8gg.quant_weight_dual(w, mode)
+    q0, s0 = ops.to_mxfp8_dim0(w, mode)
+    t0, ts0 = mxfp8gg.quant_weight_for_dgrad(w, mode)
+    assert wq.shape == q0.shape and ws.shape == s0.shape
+    assert wt.shape == t0.shape and wts.shape == ts0.shape
+    assert np.array_equal(u8(wq), u8(q0)) and np.array_equal(u8(ws), u8(s0))
+    assert np.array_equal(u8(wt), u8(t0)) and np.array_equal(u8(wts), u8(ts0))
+
+
+def test_dual_c2_activation_full_size(gpu):
+    # full C2 activation: byte-identical to the two single casts (each pinned
+    # against the oracle above)
+    x, w, sizes = workloads.c2(gpu)
+    del w
+    e = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    q, s, qt, st, pad = ops.to_mxfp8_dual(x, e)
+    q0, s0 = ops.to_mxfp8_dim0(x)
+    qt1, st1, pad1 = ops.to_mxfp8_dim1(x, e)
+    assert torch.equal(q.view(torch.uint8), q0.view(torch.uint8))
+    assert torch.equal(s.contiguous(), s0.contiguous())
+    assert torch.equal(qt.view(torch.uint8), qt1.view(torch.uint8))
+    assert torch.equal(st.contiguous(), st1.contiguous())
+    assert torch.equal(pad, pad1)
