@@ -439,6 +439,12 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
 
 #undef MXGG_FENCE
 
+// Value of the neighbouring lane (lane ^ 1) through a DPP quad permutation
+// [1, 0, 3, 2]: a VALU move, no LDS round trip (unlike a shuffle).
+__device__ __forceinline__ uint32_t swap_lane_pair(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);
+}
+
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   const __bf16 ha = (__bf16)a, hb = (__bf16)b;
   const uint16_t ua = *reinterpret_cast<const uint16_t*>(&ha);
@@ -459,7 +465,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 // chunk k of staged row s sits at k ^ ((s/2) mod 16), so a half-wave writing
 // one chunk column of 32 rows, and one reading a whole row, touches each LDS
 // bank exactly twice.  The staging writes take the accumulators straight from
-// AGPRs.
+// AGPRs.  The output is written once and not read again by the kernel, so the
+// row stores are nontemporal (measured faster, most for fp32 output).
 template <bool F32>
 __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char* out,
                                          int64_t ldo_bytes, uint32_t q0, uint32_t qbeg,
@@ -511,7 +518,7 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
             for (uint32_t k = 0; k < 4u && p + k < pend; ++k)
               __hip_atomic_fetch_add(dst + k, v[u][k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           } else if (p + 4u <= pend) {
-            *reinterpret_cast<v4f*>(dst) = v[u];
+            __builtin_nontemporal_store(v[u], reinterpret_cast<v4f*>(dst));
           } else {
             for (uint32_t k = 0; p + k < pend; ++k) dst[k] = v[u][k];
           }
@@ -529,8 +536,7 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
           const uint2 b =
               make_uint2(pack_bf16x2(v[u + 1][0], v[u + 1][1]), pack_bf16x2(v[u + 1][2], v[u + 1][3]));
           const uint2 send = odd ? a : b;
-          const uint2 recv = make_uint2((uint32_t)__shfl_xor((int)send.x, 1),
-                                        (uint32_t)__shfl_xor((int)send.y, 1));
+          const uint2 recv = make_uint2(swap_lane_pair(send.x), swap_lane_pair(send.y));
           const uint4 row8 = odd ? make_uint4(recv.x, recv.y, b.x, b.y)
                                  : make_uint4(a.x, a.y, recv.x, recv.y);
           const uint32_t t = t0 + u + (odd ? 1u : 0u);
@@ -538,7 +544,7 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
           if (q < qbeg || q >= qend || pe >= pend) continue;
           uint16_t* dst = reinterpret_cast<uint16_t*>(out + (int64_t)q * ldo_bytes) + pe;
           if (pe + 8u <= pend && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
-            *reinterpret_cast<uint4*>(dst) = row8;
+            __builtin_nontemporal_store(u32x4{row8.x, row8.y, row8.z, row8.w}, reinterpret_cast<u32x4*>(dst));
           } else {
             const uint32_t w[4] = {row8.x, row8.y, row8.z, row8.w};
             for (uint32_t k = 0; k < 8u && pe + k < pend; ++k)
