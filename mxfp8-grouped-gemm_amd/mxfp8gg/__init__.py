@@ -25,6 +25,7 @@ from .ops import (
     wgrad_kernel,
     wgrad_prepare,
 )
+from .weight_cache import WeightCastCache
 from .autograd import MXFP8ExpertFFN, MXFP8GroupedMM, moe_ffn, moe_ffn_unfused, mxfp8_grouped_mm
 from .torchao_compat import (
     apply,
@@ -43,5 +44,6 @@ __all__ = [
     "fused_grouped_fwd", "fwd_ge", "wgrad_fused", "wgrad_prepare", "wgrad_kernel",
     "triton_to_mxfp8_dim0", "triton_to_mxfp8_dim1",
     "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",
+    "WeightCastCache",
     "MXFP8GroupedMM", "mxfp8_grouped_mm", "MXFP8ExpertFFN", "moe_ffn", "moe_ffn_unfused",
 ]

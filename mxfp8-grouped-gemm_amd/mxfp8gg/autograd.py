@@ -31,7 +31,7 @@ class MXFP8GroupedMM(torch.autograd.Function):
     of the bf16 tensors, and dY is cast once for dgrad and wgrad together."""
 
     @staticmethod
-    def forward(ctx, x, w, offs, scaling_mode="rceil"):
+    def forward(ctx, x, w, offs, scaling_mode="rceil", weight_cache=None):
         if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
             raise TypeError("x and w must be bfloat16")
         offs = ops._group_ends(offs, w.shape[0], x.device)
@@ -42,7 +42,11 @@ class MXFP8GroupedMM(torch.autograd.Function):
             saved += [xqt, xst, pad]
         else:
             xq, xs = ops.to_mxfp8_dim0(x, scaling_mode)
-        if need_dx:
+        if weight_cache is not None:
+            (wq, ws), (wt, wts) = weight_cache.get(w, scaling_mode)
+            if need_dx:
+                saved += [wt, wts]
+        elif need_dx:
             (wq, ws), (wt, wts) = ops.quant_weight_dual(w, scaling_mode)
             saved += [wt, wts]
         else:
@@ -78,15 +82,17 @@ class MXFP8GroupedMM(torch.autograd.Function):
             dx = ops.grouped_mm(dyq, wt, offs, dys, wts, out_dtype=torch.bfloat16)
         if need_dw:
             dw = ops.grouped_wgrad(dyqt, xqt, pad, dyst, xst, out_dtype=ctx.w_dtype)
-        return dx, dw, None, None
+        return dx, dw, None, None, None
 
 
 def mxfp8_grouped_mm(x: torch.Tensor, w: torch.Tensor, offs: torch.Tensor,
-                     scaling_mode: str = "rceil") -> torch.Tensor:
+                     scaling_mode: str = "rceil", weight_cache=None) -> torch.Tensor:
     """Differentiable MXFP8 grouped GEMM: x bf16 [M, K], w bf16 [E, N, K],
     offs int32 group ends [E] (or [E+1] with a leading 0) -> bf16 [M, N].
-    Rows after the last group end are left unwritten, as in the forward op."""
-    return MXFP8GroupedMM.apply(x, w, offs, scaling_mode)
+    Rows after the last group end are left unwritten, as in the forward op.
+    weight_cache: an optional WeightCastCache reusing w's casts while w is
+    unchanged."""
+    return MXFP8GroupedMM.apply(x, w, offs, scaling_mode, weight_cache)
 
 
 class MXFP8ExpertFFN(torch.autograd.Function):
@@ -104,13 +110,14 @@ class MXFP8ExpertFFN(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, x, w_gate_up, w_down, offs, scaling_mode="rceil"):
+    def forward(ctx, x, w_gate_up, w_down, offs, scaling_mode="rceil", weight_cache=None):
         E, ends = _check_ffn(x, w_gate_up, w_down, offs)
+        wcast = weight_cache.get if weight_cache is not None else ops.quant_weight_dual
         xq, xs, xqt, xst, _ = ops.to_mxfp8_dual(x, ends, scaling_mode)
-        (wq, ws), (wgt, wgts) = ops.quant_weight_dual(w_gate_up, scaling_mode)
+        (wq, ws), (wgt, wgts) = wcast(w_gate_up, scaling_mode)
         h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
         aq, as_ = ops.swiglu_quant(h, scaling_mode)
-        (dq, ds), (wdt, wdts) = ops.quant_weight_dual(w_down, scaling_mode)
+        (dq, ds), (wdt, wdts) = wcast(w_down, scaling_mode)
         y = ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16)
         ctx.save_for_backward(ends, h, xqt, xst, wgt, wgts, wdt, wdts)
         ctx.scaling_mode = scaling_mode
@@ -136,7 +143,7 @@ class MXFP8ExpertFFN(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             dwgu = ops.grouped_wgrad(act["dh_qt"], xqt, pad, act["dh_st"], xst,
                                      out_dtype=ctx.dtypes[0])
-        return dx, dwgu, dwd, None, None
+        return dx, dwgu, dwd, None, None, None
 
 
 def _check_ffn(x, w_gate_up, w_down, offs):
@@ -149,28 +156,36 @@ def _check_ffn(x, w_gate_up, w_down, offs):
     return E, ops._group_ends(offs, E, x.device)
 
 
-def _ffn_forward_only(x, w_gate_up, w_down, offs, scaling_mode):
+def _weight_dim0(w, scaling_mode, weight_cache):
+    if weight_cache is not None:
+        return weight_cache.get(w, scaling_mode)[0]
+    return ops.to_mxfp8_dim0(w, scaling_mode)
+
+
+def _ffn_forward_only(x, w_gate_up, w_down, offs, scaling_mode, weight_cache=None):
     _, ends = _check_ffn(x, w_gate_up, w_down, offs)
     xq, xs = ops.to_mxfp8_dim0(x, scaling_mode)
-    wq, ws = ops.to_mxfp8_dim0(w_gate_up, scaling_mode)
+    wq, ws = _weight_dim0(w_gate_up, scaling_mode, weight_cache)
     h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
     aq, as_ = ops.swiglu_quant(h, scaling_mode)
-    dq, ds = ops.to_mxfp8_dim0(w_down, scaling_mode)
+    dq, ds = _weight_dim0(w_down, scaling_mode, weight_cache)
     return ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16)
 
 
 def moe_ffn(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,
-            offs: torch.Tensor, scaling_mode: str = "rceil") -> torch.Tensor:
+            offs: torch.Tensor, scaling_mode: str = "rceil", weight_cache=None) -> torch.Tensor:
     """One DeepSeek-V3-style expert FFN over routed tokens (the layer step of
     the reference's e2e_bench.py:56-134): gate+up projection with the fused
     weight w_gate_up [E, 2F, H] (gate rows first), SiLU(gate) * up, down
     projection w_down [E, H, F].  x: bf16 [M, H], tokens grouped by expert with
     cumulative ends `offs`.  Rows after the last group end get no output and no
-    input gradient."""
+    input gradient.  weight_cache: an optional WeightCastCache reusing the
+    weights' casts while they are unchanged (micro-batches between optimizer
+    steps, evaluation)."""
     if not torch.is_grad_enabled() or not any(
             t.requires_grad for t in (x, w_gate_up, w_down)):
-        return _ffn_forward_only(x, w_gate_up, w_down, offs, scaling_mode)
-    return MXFP8ExpertFFN.apply(x, w_gate_up, w_down, offs, scaling_mode)
+        return _ffn_forward_only(x, w_gate_up, w_down, offs, scaling_mode, weight_cache)
+    return MXFP8ExpertFFN.apply(x, w_gate_up, w_down, offs, scaling_mode, weight_cache)
 
 
 def moe_ffn_unfused(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,

@@ -106,3 +106,44 @@ def test_wgrad_split_choice():
     assert ops.wgrad_split_tokens(32768, 2048, 2048, 1, 256) == 8192
     # short groups are not split below 4096 tokens
     assert ops.wgrad_split_tokens(4096, 256, 256, 2, 256) == 0
+
+
+# ---------------------------------------------------------------------------
+# weight-cast cache (host logic only: a stub stands in for the GPU cast)
+# ---------------------------------------------------------------------------
+def _stub_cache(max_entries=4):
+    from mxfp8gg.weight_cache import WeightCastCache
+    calls = []
+
+    def cast(w, mode):
+        calls.append((id(w), w._version, mode))
+        return (("q", len(calls)), ("t", len(calls)))
+
+    return WeightCastCache(max_entries=max_entries, cast=cast), calls
+
+
+def test_weight_cache_hits_until_the_weight_changes():
+    cache, calls = _stub_cache()
+    w = torch.zeros(2, 32, 64)
+    a = cache.get(w, "rceil")
+    assert cache.get(w, "rceil") is a and len(calls) == 1 and cache.hits == 1
+    w.add_(1.0)                                   # in-place update bumps the version
+    b = cache.get(w, "rceil")
+    assert b is not a and len(calls) == 2
+    assert len(cache) == 1                         # the stale entry was dropped
+    cache.get(w, "floor")                          # the scale mode is part of the key
+    assert len(calls) == 3
+
+
+def test_weight_cache_distinguishes_tensors_and_evicts_lru():
+    cache, calls = _stub_cache(max_entries=2)
+    ws = [torch.zeros(1, 32, 32) for _ in range(3)]
+    for w in ws:
+        cache.get(w)
+    assert len(calls) == 3 and len(cache) == 2     # the oldest entry was evicted
+    cache.get(ws[2])
+    assert len(calls) == 3                          # still cached
+    cache.get(ws[0])
+    assert len(calls) == 4                          # evicted earlier, cast again
+    cache.clear()
+    assert len(cache) == 0

@@ -110,3 +110,31 @@ def test_moe_ffn_fused_matches_unfused_composition(gpu):
         assert got.shape == want.shape
         assert _rel(got, want) < 1e-2
         assert (got == want).float().mean().item() > 0.99
+
+
+def test_moe_ffn_weight_cache(gpu):
+    sizes = [64, 96, 32]
+    E, H, F = 3, 256, 128
+    g = torch.Generator(device=gpu).manual_seed(85)
+    M = sum(sizes)
+    x = torch.randn(M, H, generator=g, device=gpu).to(torch.bfloat16)
+    wgu = (torch.randn(E, 2 * F, H, generator=g, device=gpu) * 0.06).to(torch.bfloat16)
+    wd = (torch.randn(E, H, F, generator=g, device=gpu) * 0.06).to(torch.bfloat16)
+    offs = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    cache = mxfp8gg.WeightCastCache()
+    ref = mxfp8gg.moe_ffn(x, wgu, wd, offs)
+    for _ in range(2):                             # second call reuses both weight casts
+        assert torch.equal(mxfp8gg.moe_ffn(x, wgu, wd, offs, weight_cache=cache), ref)
+    assert cache.misses == 2 and cache.hits == 2
+    with torch.no_grad():
+        wd.mul_(0.5)                               # an optimizer-style in-place update
+    upd = mxfp8gg.moe_ffn(x, wgu, wd, offs)
+    assert torch.equal(mxfp8gg.moe_ffn(x, wgu, wd, offs, weight_cache=cache), upd)
+    assert cache.misses == 3
+    # with autograd: gradients identical with and without the cache
+    leaves = [t.clone().requires_grad_(True) for t in (x, wgu, wd)]
+    mxfp8gg.moe_ffn(*leaves, offs).backward(ref)
+    leaves_c = [t.clone().requires_grad_(True) for t in (x, wgu, wd)]
+    mxfp8gg.moe_ffn(*leaves_c, offs, weight_cache=cache).backward(ref)
+    for a, b in zip(leaves, leaves_c):
+        assert torch.equal(a.grad, b.grad)
