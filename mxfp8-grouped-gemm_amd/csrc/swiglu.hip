@@ -316,14 +316,22 @@ __device__ __forceinline__ void store_bf16_rows(const uint2 (&v)[8], uint16_t* d
   }
 }
 
+// At most 168 VGPRs (three waves per SIMD): the kernel streams and needs the
+// extra waves to keep loads in flight; the compiler fits it without spills.
 template <int MODE, bool SW>
-__global__ __launch_bounds__(256) void k_swiglu_bwd(const SwigluBwdArgs p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_swiglu_bwd(
+    const SwigluBwdArgs p) {
   __shared__ int32_t ends_s[kMaxGroups];
   __shared__ int32_t pend_s[kMaxGroups];
   const int lane = threadIdx.x & 63;
   const int tg = lane & 3, fg = lane >> 2;
-  const int64_t P = (int64_t)blockIdx.x * 128 + (threadIdx.x >> 6) * 32 + 8 * tg;
-  const int f = blockIdx.y * 64 + 4 * fg;
+  // Feature blocks vary fastest over the (one-dimensional) grid, so the
+  // workgroups that write the two 64-byte halves of a row-wise output line run
+  // at the same time.
+  const uint32_t nfb = ((uint32_t)p.cols + 63u) / 64u;
+  const uint32_t fb = blockIdx.x % nfb, pb = blockIdx.x / nfb;
+  const int64_t P = (int64_t)pb * 128 + (threadIdx.x >> 6) * 32 + 8 * tg;
+  const int f = (int)fb * 64 + 4 * fg;
 
   int64_t tok0 = 0;
   int ntok = 0;
@@ -406,7 +414,7 @@ hipError_t swiglu_dim0_impl(const uint16_t* gate, const uint16_t* up, int64_t ld
 
 template <int MODE, bool SW>
 hipError_t swiglu_bwd_impl(const SwigluBwdArgs& p, hipStream_t stream) {
-  dim3 grid((unsigned)((p.cap + 127) / 128), (unsigned)((p.cols + 63) / 64));
+  dim3 grid((unsigned)(((p.cap + 127) / 128) * ((p.cols + 63) / 64)));
   hipLaunchKernelGGL((k_swiglu_bwd<MODE, SW>), grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
