@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 5
+#define MXGG_ABI_VERSION 6
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -253,6 +253,85 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
                        const int32_t* group_ends, int64_t num_groups,
                        int64_t M, int64_t N, int64_t K,
                        void* dw, int out_dtype, int64_t split_tokens, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Token routing of a top-k MoE layer on one GPU (the layer's dispatch and
+ * combine around the expert GEMMs).  A slot is one (token, k) pair,
+ * s = t * topk + k; the routed layout holds one row per slot, grouped by
+ * expert, each group padded with empty rows to a multiple of pad_multiple.
+ * The reference's trainer gets this layout from torchtitan's token dispatcher,
+ * swapped in with pad_multiple = 32 (port_mxfp8.py:214, 240); the dispatcher
+ * orders slots by a stable argsort of the expert ids, which is the order here.
+ * ------------------------------------------------------------------------- */
+
+/*
+ * Dispatch plan, computed on the device by one workgroup (no host sync):
+ *   expert_idx  : int32 [tokens, topk] expert of each slot; ids outside
+ *                 [0, num_experts) drop the slot
+ *   perm        : int32 [tokens * topk] routed row of each slot, -1 if dropped
+ *   src         : int32 [rows_cap] slot of each routed row, -1 for padding rows
+ *                 and for every row past the last group
+ *   group_ends  : int32 [num_experts] cumulative padded group ends (the
+ *                 group_ends of the GEMMs and casts over the routed layout)
+ *   counts      : int32 [num_experts] slots routed to each expert
+ * Slots of one expert keep their slot order.  rows_cap >= tokens * topk +
+ * num_experts * (pad_multiple - 1) rows always suffice;
+ * 1 <= num_experts <= 1024, 1 <= pad_multiple <= 1024.
+ */
+int mxgg_route_plan(const int32_t* expert_idx, int64_t tokens, int64_t topk, int64_t num_experts,
+                    int64_t pad_multiple, int64_t rows_cap, int32_t* perm, int32_t* src,
+                    int32_t* group_ends, int32_t* counts, void* stream);
+
+/*
+ * Routed rows in bf16: out[r] = x[src[r] / topk] for src[r] >= 0, times
+ * row_scale[src[r]] rounded to bf16 when row_scale (fp32 [tokens * topk]) is
+ * given; zero rows for src[r] < 0 and for slots whose token is not below
+ * `tokens`.  x: bf16 [tokens, cols] (stride ldx); out: bf16 [rows, cols].
+ * cols % 8 == 0, rows 16-byte aligned, strides multiples of 8.  The routed
+ * input of the dispatcher (`x[sorted_slots // topk]`), materialised; the MXFP8
+ * path uses mxgg_gather_quant_dual instead.
+ */
+int mxgg_gather_rows(const void* x, int64_t tokens, int64_t cols, int64_t ldx, const int32_t* src,
+                     int64_t topk, const float* row_scale, int64_t rows, void* out, int64_t ldo,
+                     void* stream);
+
+/*
+ * mxgg_quant_dual of the routed rows (as mxgg_gather_rows would write them),
+ * read straight from token order: the bf16 routed layout is never written.
+ * rows = rows of the routed layout; every other argument as mxgg_quant_dual.
+ * Without row_scale: the MXFP8 expert input of the forward pass.  With the
+ * combine weights as row_scale and grad_out as x: the MXFP8 casts of the
+ * combine's input gradient (the down projection's dY).
+ */
+int mxgg_gather_quant_dual(const void* x, int64_t tokens, int64_t cols, int64_t ldx,
+                           const int32_t* src, int64_t topk, const float* row_scale, int64_t rows,
+                           const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap,
+                           void* q, int64_t ldq, void* scales, int64_t lds, void* qt, int64_t ldqt,
+                           void* scales_t, int64_t ldst, int scale_layout,
+                           int32_t* group_ends_pad, int scale_mode, void* stream);
+
+/*
+ * Combine: out[t] = bf16(sum over k of float(bf16(float(y[perm[s]]) *
+ * scores[s]))), s = t * topk + k, summed in fp32 in k order (one rounding of
+ * the sum); without scores each term is the row itself.  Slots with perm < 0
+ * or perm >= rows add nothing.  y: bf16 [rows, cols] routed layout; out: bf16
+ * [tokens, cols].  cols % 8 == 0, 16-byte aligned rows.  The dispatcher's
+ * weighted scatter-add back to token order; without scores, the input
+ * gradient of the gather (dX from the routed dX).
+ */
+int mxgg_combine(const void* y, int64_t rows, int64_t cols, int64_t ldy, const int32_t* perm,
+                 const float* scores, int64_t tokens, int64_t topk, void* out, int64_t ldo,
+                 void* stream);
+
+/*
+ * Gradient of the combine with respect to its weights:
+ *   grad_scores[s] = sum over h of float(grad_out[t][h]) * float(y[perm[s]][h])
+ * (fp32), 0 for a dropped slot.  grad_out: bf16 [tokens, cols]; y as in
+ * mxgg_combine; grad_scores: fp32 [tokens * topk].
+ */
+int mxgg_combine_score_grad(const void* grad_out, int64_t ldg, const void* y, int64_t rows,
+                            int64_t cols, int64_t ldy, const int32_t* perm, int64_t tokens,
+                            int64_t topk, float* grad_scores, void* stream);
 
 #ifdef __cplusplus
 }

@@ -20,6 +20,9 @@ constexpr int64_t kMaxBufferBytes = 0x7FFFFFF0LL;  // one buffer resource per op
 // GEMM tiles run up to 255 rows past an operand's last row; those offsets must
 // stay below 2^32 (they read as zero through the buffer range check).
 constexpr int64_t kMaxRowStride = INT64_C(1) << 23;
+// Kernels with one wave per row and four rows per 256-thread workgroup: the
+// grid holds at most 2^32 - 1 work-items.
+constexpr int64_t kMaxWaveRows = 4 * ((INT64_C(1) << 24) - 1);
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 }  // namespace
@@ -162,52 +165,67 @@ int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
       "quant_dim1");
 }
 
+// Argument rules shared by the dual casts (plain and gathered); returns
+// MXGG_OK, or the status with the error message set, naming `what`.
+static int check_dual(const char* what, bool have_x, int64_t rows, int64_t cols, int64_t ldx,
+                      const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap,
+                      const void* q, int64_t ldq, const void* scales, int64_t lds, const void* qt,
+                      int64_t ldqt, const void* scales_t, int64_t ldst, int scale_layout,
+                      const int32_t* group_ends_pad, int scale_mode, const void* x) {
+  const int mode = scale_mode & 0xFF;
+  if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "%s: unknown scale_mode %d", what, scale_mode);
+  if (!valid_layout(scale_layout))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "%s: unknown scale_layout %d", what,
+                     scale_layout);
+  if (rows < 0 || cols < 0 || rows_pad_cap < 0)
+    return set_error(MXGG_ERR_SHAPE, "%s: negative size", what);
+  if (cols % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "%s: cols=%lld is not a multiple of 32", what,
+                     (long long)cols);
+  if (rows_pad_cap % 32 != 0)
+    return set_error(MXGG_ERR_SHAPE, "%s: rows_pad_cap=%lld is not a multiple of 32", what,
+                     (long long)rows_pad_cap);
+  if (group_ends) {
+    if (num_groups < 1 || num_groups > kMaxGroupsAbi)
+      return set_error(MXGG_ERR_UNSUPPORTED, "%s: num_groups=%lld outside [1, %lld]", what,
+                       (long long)num_groups, (long long)kMaxGroupsAbi);
+    if (!group_ends_pad)
+      return set_error(MXGG_ERR_INVALID_ARGUMENT, "%s: group_ends_pad is required with group_ends",
+                       what);
+  }
+  const int64_t need = ((rows + 31 * (group_ends ? num_groups : 0) + 31) / 32) * 32;
+  if (rows_pad_cap < need)
+    return set_error(MXGG_ERR_SHAPE, "%s: rows_pad_cap=%lld < required %lld", what,
+                     (long long)rows_pad_cap, (long long)need);
+  if (cols == 0 || rows_pad_cap == 0) return MXGG_OK;
+  if (rows > 0 && (!have_x || !q || !scales))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "%s: null x, q or scales", what);
+  if (!qt || !scales_t) return set_error(MXGG_ERR_INVALID_ARGUMENT, "%s: null qt", what);
+  const bool bm = scale_layout == MXGG_SCALES_BLOCK_MAJOR;
+  if (ldx < cols || ldq < cols || lds < (bm ? rows : cols / 32) || ldqt < rows_pad_cap ||
+      ldst < (bm ? cols : rows_pad_cap / 32))
+    return set_error(MXGG_ERR_SHAPE, "%s: leading dimension smaller than the row", what);
+  if ((x && !aligned16(x)) || ldx % 8 != 0 || (q && (reinterpret_cast<uintptr_t>(q) & 7u) != 0) ||
+      ldq % 8 != 0 || !aligned16(qt) || ldqt % 16 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "%s: x 16-byte aligned with ldx %% 8 == 0, q 8-byte aligned with ldq "
+                     "%% 8 == 0, qt 16-byte aligned with ldqt %% 16 == 0",
+                     what);
+  if (rows > INT32_MAX || rows_pad_cap > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "%s: more than 2^31 rows", what);
+  return MXGG_OK;
+}
+
 int mxgg_quant_dual(const void* x, int64_t rows, int64_t cols, int64_t ldx,
                     const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap, void* q,
                     int64_t ldq, void* scales, int64_t lds, void* qt, int64_t ldqt,
                     void* scales_t, int64_t ldst, int scale_layout, int32_t* group_ends_pad,
                     int scale_mode, void* stream) {
-  const int mode = scale_mode & 0xFF;
-  if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
-    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dual: unknown scale_mode %d", scale_mode);
-  if (!valid_layout(scale_layout))
-    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dual: unknown scale_layout %d",
-                     scale_layout);
-  if (rows < 0 || cols < 0 || rows_pad_cap < 0)
-    return set_error(MXGG_ERR_SHAPE, "quant_dual: negative size");
-  if (cols % 32 != 0)
-    return set_error(MXGG_ERR_SHAPE, "quant_dual: cols=%lld is not a multiple of 32",
-                     (long long)cols);
-  if (rows_pad_cap % 32 != 0)
-    return set_error(MXGG_ERR_SHAPE, "quant_dual: rows_pad_cap=%lld is not a multiple of 32",
-                     (long long)rows_pad_cap);
-  if (group_ends) {
-    if (num_groups < 1 || num_groups > kMaxGroupsAbi)
-      return set_error(MXGG_ERR_UNSUPPORTED, "quant_dual: num_groups=%lld outside [1, %lld]",
-                       (long long)num_groups, (long long)kMaxGroupsAbi);
-    if (!group_ends_pad)
-      return set_error(MXGG_ERR_INVALID_ARGUMENT,
-                       "quant_dual: group_ends_pad is required with group_ends");
-  }
-  const int64_t need = ((rows + 31 * (group_ends ? num_groups : 0) + 31) / 32) * 32;
-  if (rows_pad_cap < need)
-    return set_error(MXGG_ERR_SHAPE, "quant_dual: rows_pad_cap=%lld < required %lld",
-                     (long long)rows_pad_cap, (long long)need);
-  if (cols == 0 || rows_pad_cap == 0) return MXGG_OK;
-  if (rows > 0 && (!x || !q || !scales))
-    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dual: null x, q or scales");
-  if (!qt || !scales_t) return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dual: null qt");
-  const bool bm = scale_layout == MXGG_SCALES_BLOCK_MAJOR;
-  if (ldx < cols || ldq < cols || lds < (bm ? rows : cols / 32) || ldqt < rows_pad_cap ||
-      ldst < (bm ? cols : rows_pad_cap / 32))
-    return set_error(MXGG_ERR_SHAPE, "quant_dual: leading dimension smaller than the row");
-  if ((x && !aligned16(x)) || ldx % 8 != 0 || (q && (reinterpret_cast<uintptr_t>(q) & 7u) != 0) ||
-      ldq % 8 != 0 || !aligned16(qt) || ldqt % 16 != 0)
-    return set_error(MXGG_ERR_ALIGNMENT,
-                     "quant_dual: x 16-byte aligned with ldx %% 8 == 0, q 8-byte aligned with ldq "
-                     "%% 8 == 0, qt 16-byte aligned with ldqt %% 16 == 0");
-  if (rows > INT32_MAX || rows_pad_cap > INT32_MAX)
-    return set_error(MXGG_ERR_UNSUPPORTED, "quant_dual: more than 2^31 rows");
+  const int st = check_dual("quant_dual", x != nullptr, rows, cols, ldx, group_ends, num_groups,
+                            rows_pad_cap, q, ldq, scales, lds, qt, ldqt, scales_t, ldst,
+                            scale_layout, group_ends_pad, scale_mode, x);
+  if (st != MXGG_OK || cols == 0 || rows_pad_cap == 0) return st;
   return check_launch(
       launch_quant_dual(static_cast<const uint16_t*>(x), rows, cols, ldx, group_ends,
                         group_ends ? num_groups : 1, rows_pad_cap, static_cast<uint8_t*>(q), ldq,
@@ -519,6 +537,136 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
   args.scaled = scaled;
   return check_launch(launch_grouped_wgrad(args, static_cast<hipStream_t>(stream)),
                       "grouped_wgrad");
+}
+
+// ---------------------------------------------------------------------------
+// Token routing.
+// ---------------------------------------------------------------------------
+int mxgg_route_plan(const int32_t* expert_idx, int64_t tokens, int64_t topk, int64_t num_experts,
+                    int64_t pad_multiple, int64_t rows_cap, int32_t* perm, int32_t* src,
+                    int32_t* group_ends, int32_t* counts, void* stream) {
+  if (tokens < 0 || topk < 1 || rows_cap < 0)
+    return set_error(MXGG_ERR_SHAPE, "route_plan: tokens=%lld, topk=%lld, rows_cap=%lld",
+                     (long long)tokens, (long long)topk, (long long)rows_cap);
+  if (num_experts < 1 || num_experts > kMaxGroupsAbi)
+    return set_error(MXGG_ERR_UNSUPPORTED, "route_plan: num_experts=%lld outside [1, %lld]",
+                     (long long)num_experts, (long long)kMaxGroupsAbi);
+  if (pad_multiple < 1 || pad_multiple > 1024)
+    return set_error(MXGG_ERR_UNSUPPORTED, "route_plan: pad_multiple=%lld outside [1, 1024]",
+                     (long long)pad_multiple);
+  if (tokens > INT32_MAX / topk)
+    return set_error(MXGG_ERR_UNSUPPORTED, "route_plan: tokens * topk above 2^31");
+  const int64_t n = tokens * topk;
+  const int64_t need = n + num_experts * (pad_multiple - 1);
+  if (rows_cap < need)
+    return set_error(MXGG_ERR_SHAPE, "route_plan: rows_cap=%lld < tokens*topk + E*(pad-1) = %lld",
+                     (long long)rows_cap, (long long)need);
+  if (rows_cap > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "route_plan: rows_cap above 2^31");
+  if (!group_ends || !counts || (n > 0 && (!expert_idx || !perm)) || (rows_cap > 0 && !src))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "route_plan: null pointer");
+  return check_launch(launch_route_plan(expert_idx, n, (int)num_experts, (int)pad_multiple,
+                                        rows_cap, perm, src, group_ends, counts,
+                                        static_cast<hipStream_t>(stream)),
+                      "route_plan");
+}
+
+// Rows of 16-byte bf16 chunks: cols % 8 == 0, 16-byte aligned bases and strides.
+static int check_rows(const char* what, const void* a, int64_t lda, const void* b, int64_t ldb,
+                      int64_t cols) {
+  if (cols < 0 || cols % 8 != 0)
+    return set_error(MXGG_ERR_SHAPE, "%s: cols=%lld is not a non-negative multiple of 8", what,
+                     (long long)cols);
+  if (lda < cols || ldb < cols)
+    return set_error(MXGG_ERR_SHAPE, "%s: leading dimension smaller than the row", what);
+  if ((a && !aligned16(a)) || (b && !aligned16(b)) || lda % 8 != 0 || ldb % 8 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "%s: rows 16-byte aligned with leading dimensions multiples of 8", what);
+  return MXGG_OK;
+}
+
+int mxgg_gather_rows(const void* x, int64_t tokens, int64_t cols, int64_t ldx, const int32_t* src,
+                     int64_t topk, const float* row_scale, int64_t rows, void* out, int64_t ldo,
+                     void* stream) {
+  if (tokens < 0 || rows < 0 || topk < 1)
+    return set_error(MXGG_ERR_SHAPE, "gather_rows: tokens=%lld, rows=%lld, topk=%lld",
+                     (long long)tokens, (long long)rows, (long long)topk);
+  const int st = check_rows("gather_rows", x, ldx, out, ldo, cols);
+  if (st != MXGG_OK) return st;
+  if (rows == 0 || cols == 0) return MXGG_OK;
+  if (!src || !out || (tokens > 0 && !x))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "gather_rows: null pointer");
+  if (topk > INT32_MAX || rows > kMaxWaveRows)
+    return set_error(MXGG_ERR_UNSUPPORTED, "gather_rows: rows above %lld", (long long)kMaxWaveRows);
+  return check_launch(launch_gather_rows(static_cast<const uint16_t*>(x), ldx, tokens, src,
+                                         (int)topk, row_scale, rows, cols,
+                                         static_cast<uint16_t*>(out), ldo,
+                                         static_cast<hipStream_t>(stream)),
+                      "gather_rows");
+}
+
+int mxgg_gather_quant_dual(const void* x, int64_t tokens, int64_t cols, int64_t ldx,
+                           const int32_t* src, int64_t topk, const float* row_scale, int64_t rows,
+                           const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap,
+                           void* q, int64_t ldq, void* scales, int64_t lds, void* qt, int64_t ldqt,
+                           void* scales_t, int64_t ldst, int scale_layout,
+                           int32_t* group_ends_pad, int scale_mode, void* stream) {
+  if (tokens < 0 || topk < 1 || topk > INT32_MAX)
+    return set_error(MXGG_ERR_SHAPE, "gather_quant_dual: tokens=%lld, topk=%lld",
+                     (long long)tokens, (long long)topk);
+  const int st = check_dual("gather_quant_dual", x != nullptr || tokens == 0, rows, cols, ldx,
+                            group_ends, num_groups, rows_pad_cap, q, ldq, scales, lds, qt, ldqt,
+                            scales_t, ldst, scale_layout, group_ends_pad, scale_mode, x);
+  if (st != MXGG_OK || cols == 0 || rows_pad_cap == 0) return st;
+  if (rows > 0 && !src) return set_error(MXGG_ERR_INVALID_ARGUMENT, "gather_quant_dual: null src");
+  return check_launch(
+      launch_gather_quant_dual(static_cast<const uint16_t*>(x), tokens, ldx, src, (int)topk,
+                               row_scale, rows, cols, group_ends, group_ends ? num_groups : 1,
+                               rows_pad_cap, static_cast<uint8_t*>(q), ldq,
+                               static_cast<uint8_t*>(scales), lds, static_cast<uint8_t*>(qt), ldqt,
+                               static_cast<uint8_t*>(scales_t), ldst, scale_layout, group_ends_pad,
+                               scale_mode, static_cast<hipStream_t>(stream)),
+      "gather_quant_dual");
+}
+
+int mxgg_combine(const void* y, int64_t rows, int64_t cols, int64_t ldy, const int32_t* perm,
+                 const float* scores, int64_t tokens, int64_t topk, void* out, int64_t ldo,
+                 void* stream) {
+  if (rows < 0 || tokens < 0 || topk < 1 || topk > INT32_MAX)
+    return set_error(MXGG_ERR_SHAPE, "combine: rows=%lld, tokens=%lld, topk=%lld",
+                     (long long)rows, (long long)tokens, (long long)topk);
+  const int st = check_rows("combine", y, ldy, out, ldo, cols);
+  if (st != MXGG_OK) return st;
+  if (tokens == 0 || cols == 0) return MXGG_OK;
+  if (!perm || !out || (rows > 0 && !y))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "combine: null pointer");
+  if (tokens > kMaxWaveRows)
+    return set_error(MXGG_ERR_UNSUPPORTED, "combine: tokens above %lld", (long long)kMaxWaveRows);
+  return check_launch(launch_combine(static_cast<const uint16_t*>(y), ldy, rows, perm, scores,
+                                     tokens, (int)topk, cols, static_cast<uint16_t*>(out), ldo,
+                                     static_cast<hipStream_t>(stream)),
+                      "combine");
+}
+
+int mxgg_combine_score_grad(const void* grad_out, int64_t ldg, const void* y, int64_t rows,
+                            int64_t cols, int64_t ldy, const int32_t* perm, int64_t tokens,
+                            int64_t topk, float* grad_scores, void* stream) {
+  if (rows < 0 || tokens < 0 || topk < 1 || topk > INT32_MAX)
+    return set_error(MXGG_ERR_SHAPE, "combine_score_grad: rows=%lld, tokens=%lld, topk=%lld",
+                     (long long)rows, (long long)tokens, (long long)topk);
+  const int st = check_rows("combine_score_grad", grad_out, ldg, y, ldy, cols);
+  if (st != MXGG_OK) return st;
+  if (tokens == 0) return MXGG_OK;
+  if (!perm || !grad_scores || (cols > 0 && (!grad_out || (rows > 0 && !y))))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "combine_score_grad: null pointer");
+  if (tokens > kMaxWaveRows)
+    return set_error(MXGG_ERR_UNSUPPORTED, "combine_score_grad: tokens above %lld",
+                     (long long)kMaxWaveRows);
+  return check_launch(
+      launch_combine_score_grad(static_cast<const uint16_t*>(grad_out), ldg,
+                                static_cast<const uint16_t*>(y), ldy, rows, perm, tokens,
+                                (int)topk, cols, grad_scores, static_cast<hipStream_t>(stream)),
+      "combine_score_grad");
 }
 
 }  // extern "C"

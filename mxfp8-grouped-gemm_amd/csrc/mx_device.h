@@ -203,6 +203,14 @@ __device__ __forceinline__ void stage_group_tables(const int32_t* __restrict__ e
   }
 }
 
+// bf16(float(v_i) * sc) for the eight bf16 values of a 16-byte chunk (RNE).
+__device__ __forceinline__ uint4 scale_chunk(const uint4& v, float sc) {
+  return make_uint4(pack_bf16x2(bf16_lo(v.x) * sc, bf16_hi(v.x) * sc),
+                    pack_bf16x2(bf16_lo(v.y) * sc, bf16_hi(v.y) * sc),
+                    pack_bf16x2(bf16_lo(v.z) * sc, bf16_hi(v.z) * sc),
+                    pack_bf16x2(bf16_lo(v.w) * sc, bf16_hi(v.w) * sc));
+}
+
 // Padded token position P, the first of a run of `run` positions (run divides
 // 32, P a multiple of run, so the run never straddles two groups), to the
 // first real token tok0 and the number of real tokens ntok in the run.

@@ -48,6 +48,32 @@ hipError_t launch_quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int6
                              int64_t lds, uint8_t* qt, int64_t ldqt, uint8_t* st, int64_t ldst,
                              int layout, int32_t* group_ends_pad, int mode, hipStream_t stream);
 
+// The dual cast of rows gathered from token order: row r of the input is row
+// src[r] / topk of x (zero for src[r] < 0), times row_scale[src[r]] (rounded to
+// bf16) when row_scale is given; rows = rows of the routed layout.
+hipError_t launch_gather_quant_dual(const uint16_t* x, int64_t xrows, int64_t ldx,
+                                    const int32_t* src, int topk, const float* row_scale,
+                                    int64_t rows, int64_t cols, const int32_t* group_ends,
+                                    int64_t num_groups, int64_t rows_pad_cap, uint8_t* q,
+                                    int64_t ldq, uint8_t* s, int64_t lds, uint8_t* qt,
+                                    int64_t ldqt, uint8_t* st, int64_t ldst, int layout,
+                                    int32_t* group_ends_pad, int mode, hipStream_t stream);
+
+// Token routing (route.hip).
+hipError_t launch_route_plan(const int32_t* idx, int64_t n, int E, int pad, int64_t cap,
+                             int32_t* perm, int32_t* src, int32_t* ends, int32_t* counts,
+                             hipStream_t stream);
+hipError_t launch_gather_rows(const uint16_t* x, int64_t ldx, int64_t xrows, const int32_t* src,
+                              int topk, const float* row_scale, int64_t rows, int64_t cols,
+                              uint16_t* out, int64_t ldo, hipStream_t stream);
+hipError_t launch_combine(const uint16_t* y, int64_t ldy, int64_t yrows, const int32_t* perm,
+                          const float* scores, int64_t tokens, int topk, int64_t cols, uint16_t* out,
+                          int64_t ldo, hipStream_t stream);
+hipError_t launch_combine_score_grad(const uint16_t* dout, int64_t ldd, const uint16_t* y,
+                                     int64_t ldy, int64_t yrows, const int32_t* perm,
+                                     int64_t tokens, int topk, int64_t cols, float* dscore,
+                                     hipStream_t stream);
+
 // Padded cumulative group ends of the token-axis casts (one workgroup).
 hipError_t launch_pad_ends(const int32_t* group_ends, int64_t num_groups, int64_t rows,
                            int32_t* group_ends_pad, hipStream_t stream);

@@ -188,12 +188,23 @@ struct RowOut {
   int64_t ldq, s_row, s_blk;
 };
 
-template <int MODE, bool SW, bool ROW>
+// GATHER: row r of the cast's input is row src[r] / topk of x (zero when
+// src[r] < 0 or that token is not below xrows), optionally times
+// scale[src[r]] rounded to bf16: the routed layout of a top-k MoE layer read
+// straight from token order (the dispatch's gather, or the combine's backward).
+struct Gather {
+  const int32_t* src;
+  const float* scale;
+  int64_t xrows;
+  int topk;
+};
+
+template <int MODE, bool SW, bool ROW, bool GATHER>
 __global__ __launch_bounds__(256) void k_quant_dim1(
     const uint16_t* __restrict__ x, int64_t rows, int cols, int64_t ldx,
     const int32_t* __restrict__ ends, const int32_t* __restrict__ ends_pad, int E,
     int64_t rows_pad_cap, uint8_t* __restrict__ qt, int64_t ldqt, uint8_t* __restrict__ st,
-    int64_t st_row, int64_t st_blk, RowOut ro) {
+    int64_t st_row, int64_t st_blk, RowOut ro, Gather ga) {
   __shared__ int32_t ends_s[kMaxGroups];
   __shared__ int32_t pend_s[kMaxGroups];
   const int lane = threadIdx.x & 63;
@@ -215,10 +226,27 @@ __global__ __launch_bounds__(256) void k_quant_dim1(
   if (f >= cols) ntok = 0;
 
   uint4 v[16];
+  if (GATHER) {
+    int32_t sl[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    v[i] = i < ntok ? *reinterpret_cast<const uint4*>(x + (tok0 + i) * ldx + f)
-                    : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < 16; ++i) sl[i] = i < ntok ? ga.src[tok0 + i] : -1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t t = sl[i] >= 0 ? sl[i] / ga.topk : ga.xrows;
+      v[i] = t < ga.xrows ? *reinterpret_cast<const uint4*>(x + t * ldx + f)
+                          : make_uint4(0, 0, 0, 0);
+    }
+    if (ga.scale != nullptr) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (sl[i] >= 0 && sl[i] / ga.topk < ga.xrows) v[i] = scale_chunk(v[i], ga.scale[sl[i]]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      v[i] = i < ntok ? *reinterpret_cast<const uint4*>(x + (tok0 + i) * ldx + f)
+                      : make_uint4(0, 0, 0, 0);
+    }
   }
 
   if (ROW) {
@@ -304,19 +332,20 @@ hipError_t dim0_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
   return hipGetLastError();
 }
 
-template <int MODE, bool SW, bool ROW>
+template <int MODE, bool SW, bool ROW, bool GATHER>
 hipError_t dim1_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
                      const int32_t* ends, int64_t E, int64_t cap, uint8_t* qt, int64_t ldqt,
                      uint8_t* st, int64_t st_row, int64_t st_blk, int32_t* ends_pad,
-                     const RowOut& ro, hipStream_t stream) {
+                     const RowOut& ro, const Gather& ga, hipStream_t stream) {
   if (ends != nullptr) {
     hipLaunchKernelGGL(k_pad_ends, dim3(1), dim3(256), 0, stream, ends, (int)E, rows, ends_pad);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
   dim3 grid((unsigned)((cap + 127) / 128), (unsigned)((cols + 255) / 256));
-  hipLaunchKernelGGL((k_quant_dim1<MODE, SW, ROW>), grid, dim3(256), 0, stream, x, rows,
-                     (int)cols, ldx, ends, ends_pad, (int)E, cap, qt, ldqt, st, st_row, st_blk, ro);
+  hipLaunchKernelGGL((k_quant_dim1<MODE, SW, ROW, GATHER>), grid, dim3(256), 0, stream, x, rows,
+                     (int)cols, ldx, ends, ends_pad, (int)E, cap, qt, ldqt, st, st_row, st_blk, ro,
+                     ga);
   return hipGetLastError();
 }
 
@@ -366,11 +395,12 @@ hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int6
                            nullptr, 0, qt, ldqt, st, ldst, layout, group_ends_pad, mode, stream);
 }
 
-hipError_t launch_quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
-                             const int32_t* group_ends, int64_t num_groups,
-                             int64_t rows_pad_cap, uint8_t* q, int64_t ldq, uint8_t* s,
-                             int64_t lds, uint8_t* qt, int64_t ldqt, uint8_t* st, int64_t ldst,
-                             int layout, int32_t* group_ends_pad, int mode, hipStream_t stream) {
+template <bool GATHER>
+hipError_t quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                      const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap,
+                      uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, uint8_t* qt, int64_t ldqt,
+                      uint8_t* st, int64_t ldst, int layout, int32_t* group_ends_pad, int mode,
+                      const Gather& ga, hipStream_t stream) {
   if (cols == 0 || rows_pad_cap == 0) return hipSuccess;
   const bool sw = (mode & kCvtSoftwareFlag) != 0;
   const int m = mode & 0xFF;
@@ -383,9 +413,9 @@ hipError_t launch_quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int6
   ro.ldq = ldq;
   ro.s_row = bm ? 1 : lds;
   ro.s_blk = bm ? lds : 1;
-#define MXGG_DIM1(MODE, SWF, ROWF)                                                             \
-  dim1_impl<MODE, SWF, ROWF>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, qt, ldqt, \
-                             st, st_row, st_blk, group_ends_pad, ro, stream)
+#define MXGG_DIM1(MODE, SWF, ROWF)                                                           \
+  dim1_impl<MODE, SWF, ROWF, GATHER>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, \
+                                     qt, ldqt, st, st_row, st_blk, group_ends_pad, ro, ga, stream)
   if (q == nullptr) {
     if (m == kModeRceil)
       return sw ? MXGG_DIM1(kModeRceil, true, false) : MXGG_DIM1(kModeRceil, false, false);
@@ -395,6 +425,31 @@ hipError_t launch_quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int6
     return sw ? MXGG_DIM1(kModeRceil, true, true) : MXGG_DIM1(kModeRceil, false, true);
   return sw ? MXGG_DIM1(kModeFloor, true, true) : MXGG_DIM1(kModeFloor, false, true);
 #undef MXGG_DIM1
+}
+
+hipError_t launch_quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                             const int32_t* group_ends, int64_t num_groups,
+                             int64_t rows_pad_cap, uint8_t* q, int64_t ldq, uint8_t* s,
+                             int64_t lds, uint8_t* qt, int64_t ldqt, uint8_t* st, int64_t ldst,
+                             int layout, int32_t* group_ends_pad, int mode, hipStream_t stream) {
+  return quant_dual<false>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, q, ldq, s, lds,
+                           qt, ldqt, st, ldst, layout, group_ends_pad, mode, Gather{}, stream);
+}
+
+hipError_t launch_gather_quant_dual(const uint16_t* x, int64_t xrows, int64_t ldx,
+                                    const int32_t* src, int topk, const float* row_scale,
+                                    int64_t rows, int64_t cols, const int32_t* group_ends,
+                                    int64_t num_groups, int64_t rows_pad_cap, uint8_t* q,
+                                    int64_t ldq, uint8_t* s, int64_t lds, uint8_t* qt,
+                                    int64_t ldqt, uint8_t* st, int64_t ldst, int layout,
+                                    int32_t* group_ends_pad, int mode, hipStream_t stream) {
+  Gather ga;
+  ga.src = src;
+  ga.scale = row_scale;
+  ga.xrows = xrows;
+  ga.topk = topk;
+  return quant_dual<true>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, q, ldq, s, lds,
+                          qt, ldqt, st, ldst, layout, group_ends_pad, mode, ga, stream);
 }
 
 hipError_t launch_pad_ends(const int32_t* group_ends, int64_t num_groups, int64_t rows,

@@ -26,7 +26,23 @@ from .ops import (
     wgrad_prepare,
 )
 from .weight_cache import WeightCastCache
-from .autograd import MXFP8ExpertFFN, MXFP8GroupedMM, moe_ffn, moe_ffn_unfused, mxfp8_grouped_mm
+from .autograd import (
+    MXFP8ExpertFFN,
+    MXFP8GroupedMM,
+    MXFP8RoutedExpertFFN,
+    moe_ffn,
+    moe_ffn_unfused,
+    moe_routed_ffn,
+    mxfp8_grouped_mm,
+)
+from .routing import (
+    RoutePlan,
+    combine,
+    combine_score_grad,
+    gather_rows,
+    gather_to_mxfp8_dual,
+    route_plan,
+)
 from .torchao_compat import (
     apply,
     triton_mxfp8_grouped_mm,
@@ -46,4 +62,6 @@ __all__ = [
     "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",
     "WeightCastCache",
     "MXFP8GroupedMM", "mxfp8_grouped_mm", "MXFP8ExpertFFN", "moe_ffn", "moe_ffn_unfused",
+    "RoutePlan", "route_plan", "gather_rows", "gather_to_mxfp8_dual", "combine",
+    "combine_score_grad", "MXFP8RoutedExpertFFN", "moe_routed_ffn",
 ]

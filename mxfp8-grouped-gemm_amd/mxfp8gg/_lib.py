@@ -31,7 +31,7 @@ OUT_F32 = 1
 SCALES_ROW_MAJOR = 0
 SCALES_BLOCK_MAJOR = 1
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -71,6 +71,17 @@ SIGNATURES = {
     "mxgg_grouped_wgrad": (
         _I,
         [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I, _I64, _P],
+    ),
+    "mxgg_route_plan": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
+    "mxgg_gather_rows": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P]),
+    "mxgg_gather_quant_dual": (
+        _I,
+        [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64,
+         _P, _I64, _I, _P, _I, _P],
+    ),
+    "mxgg_combine": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P]),
+    "mxgg_combine_score_grad": (
+        _I, [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P],
     ),
 }
 

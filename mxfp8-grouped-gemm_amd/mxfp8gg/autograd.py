@@ -19,7 +19,7 @@ from __future__ import annotations
 
 import torch
 
-from . import ops
+from . import ops, routing
 
 
 class MXFP8GroupedMM(torch.autograd.Function):
@@ -153,7 +153,7 @@ def _check_ffn(x, w_gate_up, w_down, offs):
     E, F2, H = w_gate_up.shape
     if tuple(w_down.shape) != (E, H, F2 // 2) or x.shape[-1] != H:
         raise ValueError("shapes must be x [M, H], w_gate_up [E, 2F, H], w_down [E, H, F]")
-    return E, ops._group_ends(offs, E, x.device)
+    return E, (ops._group_ends(offs, E, x.device) if offs is not None else None)
 
 
 def _weight_dim0(w, scaling_mode, weight_cache):
@@ -197,3 +197,81 @@ def moe_ffn_unfused(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tens
     f = w_down.shape[2]
     a = torch.nn.functional.silu(h[:, :f]) * h[:, f:]
     return mxfp8_grouped_mm(a, w_down, offs, scaling_mode)
+
+
+class MXFP8RoutedExpertFFN(torch.autograd.Function):
+    """out = combine(FFN(gather(x)), scores): the expert FFN of MXFP8ExpertFFN
+    between the top-k dispatch and combine of a MoE layer on one GPU.
+
+    forward : route plan (device) -> both casts of the routed x read straight
+              from token order -> gate+up GEMM -> SwiGLU + cast -> down GEMM ->
+              combine (score-weighted, fp32 sum over k)
+    backward: the routed dY = bf16(dOut[t] * score[s]) is never written: its two
+              casts are gathered from dOut; then as MXFP8ExpertFFN; the routed
+              dX is summed back over k; d scores = dOut . routed output.
+    """
+
+    @staticmethod
+    def forward(ctx, x, expert_idx, scores, w_gate_up, w_down, pad_multiple=32,
+                scaling_mode="rceil", weight_cache=None):
+        E, _ = _check_ffn(x, w_gate_up, w_down, None)
+        plan = routing.route_plan(expert_idx, E, pad_multiple)
+        wcast = weight_cache.get if weight_cache is not None else ops.quant_weight_dual
+        xq, xs, xqt, xst, _ = routing.gather_to_mxfp8_dual(x, plan, scaling_mode)
+        (wq, ws), (wgt, wgts) = wcast(w_gate_up, scaling_mode)
+        h = ops.grouped_mm(xq, wq, plan.offs, xs, ws, out_dtype=torch.bfloat16)
+        aq, as_ = ops.swiglu_quant(h, scaling_mode)
+        (dq, ds), (wdt, wdts) = wcast(w_down, scaling_mode)
+        y = ops.grouped_mm(aq, dq, plan.offs, as_, ds, out_dtype=torch.bfloat16)
+        sc = scores.to(torch.float32).contiguous() if scores is not None else None
+        out = routing.combine(y, plan, sc)
+        ctx.save_for_backward(plan.perm, plan.src, plan.offs, plan.counts, h, xqt, xst, wgt, wgts,
+                              wdt, wdts, y, sc if sc is not None else torch.empty(0))
+        ctx.plan_meta = (plan.tokens, plan.topk, plan.num_experts, plan.pad_multiple)
+        ctx.has_scores = sc is not None
+        ctx.scaling_mode = scaling_mode
+        ctx.dtypes = (x.dtype, w_gate_up.dtype, w_down.dtype,
+                      scores.dtype if scores is not None else None)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        perm, src, offs, counts, h, xqt, xst, wgt, wgts, wdt, wdts, y, sc = ctx.saved_tensors
+        plan = routing.RoutePlan(perm, src, offs, counts, *ctx.plan_meta)
+        mode = ctx.scaling_mode
+        sc = sc if ctx.has_scores else None
+        dout = dout.to(torch.bfloat16)
+        if dout.stride(-1) != 1:
+            dout = dout.contiguous()
+        dx = dsc = dwgu = dwd = None
+        if ctx.has_scores and ctx.needs_input_grad[2]:
+            dsc = routing.combine_score_grad(dout, y, plan).to(ctx.dtypes[3])
+        dyq, dys, dyqt, dyst, _ = routing.gather_to_mxfp8_dual(dout, plan, mode, row_scale=sc)
+        da = ops.grouped_mm(dyq, wdt, offs, dys, wdts, out_dtype=torch.bfloat16)
+        act = ops.swiglu_backward_quant(h, da, offs, mode)
+        pad = act["offs_pad"]
+        if ctx.needs_input_grad[4]:
+            dwd = ops.grouped_wgrad(dyqt, act["a_qt"], pad, dyst, act["a_st"],
+                                    out_dtype=ctx.dtypes[2])
+        if ctx.needs_input_grad[0]:
+            dxr = ops.grouped_mm(act["dh_q"], wgt, offs, act["dh_s"], wgts,
+                                 out_dtype=torch.bfloat16)
+            dx = routing.combine(dxr, plan, None)
+        if ctx.needs_input_grad[3]:
+            dwgu = ops.grouped_wgrad(act["dh_qt"], xqt, pad, act["dh_st"], xst,
+                                     out_dtype=ctx.dtypes[1])
+        return dx, None, dsc, dwgu, dwd, None, None, None
+
+
+def moe_routed_ffn(x: torch.Tensor, expert_idx: torch.Tensor, scores: torch.Tensor | None,
+                   w_gate_up: torch.Tensor, w_down: torch.Tensor, pad_multiple: int = 32,
+                   scaling_mode: str = "rceil", weight_cache=None) -> torch.Tensor:
+    """The routed experts of one MoE layer on one GPU: every token t goes to the
+    experts expert_idx[t, :] (int [T, topk]; ids outside [0, E) are dropped),
+    through moe_ffn's MXFP8 expert FFN, and comes back as
+    sum_k scores[t, k] * expert_output (scores [T, topk] or None for a plain
+    sum).  x: bf16 [T, H]; w_gate_up [E, 2F, H]; w_down [E, H, F].  Each
+    expert's rows are padded to pad_multiple (the reference's dispatcher uses
+    32, port_mxfp8.py:214).  Differentiable in x, scores and both weights."""
+    return MXFP8RoutedExpertFFN.apply(x, expert_idx, scores, w_gate_up, w_down, pad_multiple,
+                                      scaling_mode, weight_cache)

@@ -92,6 +92,25 @@ def c5_sizes(seed=0):
     return zipf_sizes(131072, 32, 1.0, seed)
 
 
+def topk_routing(tokens: int, experts: int, topk: int, s: float, seed: int = 0):
+    """Top-k routing decisions of a MoE router: for every token, topk distinct
+    experts drawn with Zipf(s) preference p_i ~ 1/i^s (Gumbel top-k, i.e.
+    sampling without replacement), and softmax-normalised scores over them.
+    Returns (expert_idx int32 [tokens, topk], scores float32 [tokens, topk])."""
+    rng = np.random.default_rng(seed)
+    logp = -s * np.log(np.arange(1, experts + 1, dtype=np.float64))
+    keys = logp[None, :] + rng.gumbel(size=(tokens, experts))
+    idx = np.argsort(-keys, axis=1)[:, :topk].astype(np.int32)
+    logits = rng.standard_normal((tokens, topk))
+    w = np.exp(logits - logits.max(axis=1, keepdims=True))
+    return idx, (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def c5_routing(seed=0):
+    """C5's 131072 routed tokens as 16384 tokens x top-8 over 32 experts, Zipf(1.0)."""
+    return topk_routing(16384, 32, 8, 1.0, seed)
+
+
 def gemm_flops(tokens: int, n: int, k: int) -> int:
     """Algorithmic FLOPs of a grouped GEMM: 2 * M_total * N * K (fused_fwd.py:341)."""
     return 2 * int(tokens) * int(n) * int(k)

@@ -20,6 +20,13 @@ Pieces (reference paths under /root/reference):
     and its gradients in float32 with bf16 rounding after each op, the eager
     bf16 torch arithmetic of the reference's layer step (e2e_bench.py:56-61,
     85-100) with the textbook SiLU derivative sig * (1 + g * (1 - sig)).
+  * route_plan / gather_rows / combine / combine_score_grad: the token
+    dispatch and combine around the expert GEMMs that the reference takes
+    from torchtitan's token dispatcher with pad_multiple = 32
+    (port_mxfp8.py:214, 240): slots s = t * topk + k grouped by expert in
+    slot order (a sequential counting sort here), groups padded with empty
+    rows, routed input x[s // topk], combine = sum over k of the routed
+    output times its score (rounded to bf16), summed in float32 in k order.
 """
 from __future__ import annotations
 
@@ -264,3 +271,82 @@ def swiglu_bwd(g_bits: np.ndarray, u_bits: np.ndarray, d_bits: np.ndarray):
         du = bf16_round(d * s)
         a = bf16_round(s * u)
     return f32_to_bits(a), f32_to_bits(dg), f32_to_bits(du)
+
+
+# ---------------------------------------------------------------------------
+# Token routing of a top-k MoE layer (dispatch plan, gather, combine)
+# ---------------------------------------------------------------------------
+def route_plan(expert_idx: np.ndarray, num_experts: int, pad_multiple: int, rows_cap: int):
+    """Sequential counting sort of the slots s = t * topk + k by expert.
+
+    Returns (perm [n] int32: row of each slot, -1 for ids outside
+    [0, num_experts); src [rows_cap] int32: slot of each row, -1 for padding;
+    ends [E] int32: cumulative group ends, each group padded to a multiple of
+    pad_multiple; counts [E] int32)."""
+    idx = np.asarray(expert_idx, dtype=np.int64).reshape(-1)
+    E = int(num_experts)
+    counts = np.zeros(E, dtype=np.int64)
+    for e in idx:
+        if 0 <= e < E:
+            counts[e] += 1
+    padded = (counts + pad_multiple - 1) // pad_multiple * pad_multiple
+    ends = np.cumsum(padded)
+    nxt = ends - padded
+    perm = np.full(idx.size, -1, dtype=np.int32)
+    src = np.full(rows_cap, -1, dtype=np.int32)
+    for s, e in enumerate(idx):
+        if 0 <= e < E:
+            r = nxt[e]
+            nxt[e] += 1
+            perm[s] = r
+            src[r] = s
+    return perm, src, ends.astype(np.int32), counts.astype(np.int32)
+
+
+def gather_rows(x_bits: np.ndarray, src: np.ndarray, topk: int, row_scale=None) -> np.ndarray:
+    """Routed rows (bf16 bits): x[src // topk], times row_scale[src] rounded to
+    bf16 when given; zero rows where src < 0 or the token is out of range."""
+    x_bits = np.asarray(x_bits, dtype=np.uint16)
+    out = np.zeros((src.size, x_bits.shape[1]), dtype=np.uint16)
+    tok = np.where(src >= 0, src // topk, -1)
+    ok = (tok >= 0) & (tok < x_bits.shape[0])
+    rows = x_bits[tok[ok]]
+    if row_scale is not None:
+        sc = np.asarray(row_scale, dtype=np.float32).reshape(-1)[src[ok]]
+        rows = f32_to_bits(bf16_round(bits_to_f32(rows) * sc[:, None]))
+    out[ok] = rows
+    return out
+
+
+def combine(y_bits: np.ndarray, perm: np.ndarray, topk: int, scores=None) -> np.ndarray:
+    """out[t] = bf16(sum_k term_k) (bf16 bits) summed in float32, k = 0, 1, ...,
+    with term_k = bf16(float(y[perm[s]]) * score[s]) (the row itself without
+    scores); slots with perm < 0 add nothing."""
+    y_bits = np.asarray(y_bits, dtype=np.uint16)
+    p = np.asarray(perm).reshape(-1, topk)
+    T, H = p.shape[0], y_bits.shape[1]
+    acc = np.zeros((T, H), dtype=np.float32)
+    for k in range(topk):
+        r = p[:, k]
+        ok = (r >= 0) & (r < y_bits.shape[0])
+        term = np.zeros((T, H), dtype=np.float32)
+        term[ok] = bits_to_f32(y_bits[r[ok]])
+        if scores is not None:
+            sc = np.asarray(scores, dtype=np.float32).reshape(T, topk)[:, k]
+            term = bf16_round(term * sc[:, None])
+        acc = (acc + term).astype(np.float32)
+    return f32_to_bits(bf16_round(acc))
+
+
+def combine_score_grad(dout_bits: np.ndarray, y_bits: np.ndarray, perm: np.ndarray,
+                       topk: int) -> np.ndarray:
+    """d score[s] = sum_h dout[t][h] * y[perm[s]][h] (float64), 0 for dropped slots."""
+    d = bits_to_f32(np.asarray(dout_bits, dtype=np.uint16)).astype(np.float64)
+    y = bits_to_f32(np.asarray(y_bits, dtype=np.uint16)).astype(np.float64)
+    p = np.asarray(perm).reshape(-1, topk)
+    out = np.zeros(p.shape, dtype=np.float64)
+    for k in range(topk):
+        r = p[:, k]
+        ok = (r >= 0) & (r < y.shape[0])
+        out[ok, k] = np.einsum("th,th->t", d[ok], y[r[ok]])
+    return out

@@ -280,3 +280,116 @@ def test_swiglu_bwd_quant_empty_is_noop(lib):
 def test_python_maps_errors_to_exceptions(lib):
     with pytest.raises(ValueError, match="K=100"):
         _lib.check(_fwd(lib, K=100), "grouped_fwd")
+
+
+# ---------------------------------------------------------------------------
+# Token routing entry points
+# ---------------------------------------------------------------------------
+def _route(lib, **kw):
+    a = dict(idx=FAKE, T=64, K=2, E=4, pad=32, cap=128 + 4 * 31, perm=FAKE, src=FAKE, ends=FAKE,
+             counts=FAKE)
+    a.update(kw)
+    return lib.mxgg_route_plan(a["idx"], a["T"], a["K"], a["E"], a["pad"], a["cap"], a["perm"],
+                               a["src"], a["ends"], a["counts"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(E=0), _lib.ERR_UNSUPPORTED),
+    (dict(E=1025), _lib.ERR_UNSUPPORTED),
+    (dict(pad=0), _lib.ERR_UNSUPPORTED),
+    (dict(pad=2048), _lib.ERR_UNSUPPORTED),
+    (dict(K=0), _lib.ERR_SHAPE),
+    (dict(T=-1), _lib.ERR_SHAPE),
+    (dict(cap=128 + 4 * 31 - 1), _lib.ERR_SHAPE),      # below tokens*topk + E*(pad-1)
+    (dict(T=1 << 30, K=4, cap=1 << 31), _lib.ERR_UNSUPPORTED),
+    (dict(ends=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(src=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(idx=None), _lib.ERR_INVALID_ARGUMENT),
+])
+def test_route_plan_rejects(lib, kw, status):
+    assert _route(lib, **kw) == status
+
+
+def _gather(lib, **kw):
+    a = dict(x=FAKE, T=16, cols=64, ldx=64, src=FAKE, K=2, scale=None, rows=40, out=FAKE, ldo=64)
+    a.update(kw)
+    return lib.mxgg_gather_rows(a["x"], a["T"], a["cols"], a["ldx"], a["src"], a["K"], a["scale"],
+                                a["rows"], a["out"], a["ldo"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(cols=60), _lib.ERR_SHAPE),
+    (dict(ldo=56), _lib.ERR_SHAPE),
+    (dict(K=0), _lib.ERR_SHAPE),
+    (dict(x=FAKE + 8), _lib.ERR_ALIGNMENT),
+    (dict(ldx=72 + 4), _lib.ERR_ALIGNMENT),
+    (dict(src=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(rows=1 << 27), _lib.ERR_UNSUPPORTED),
+])
+def test_gather_rows_rejects(lib, kw, status):
+    assert _gather(lib, **kw) == status
+
+
+def test_gather_rows_empty_is_noop(lib):
+    assert _gather(lib, rows=0) == _lib.OK
+
+
+def _gather_dual(lib, **kw):
+    a = dict(x=FAKE, T=32, cols=64, ldx=64, src=FAKE, K=2, scale=None, rows=64, ends=FAKE, E=2,
+             cap=128, q=FAKE, ldq=64, s=FAKE, lds=64, qt=FAKE, ldqt=128, st=FAKE, ldst=64,
+             layout=BM, pad=FAKE, mode=0)
+    a.update(kw)
+    return lib.mxgg_gather_quant_dual(
+        a["x"], a["T"], a["cols"], a["ldx"], a["src"], a["K"], a["scale"], a["rows"], a["ends"],
+        a["E"], a["cap"], a["q"], a["ldq"], a["s"], a["lds"], a["qt"], a["ldqt"], a["st"],
+        a["ldst"], a["layout"], a["pad"], a["mode"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(K=0), _lib.ERR_SHAPE),
+    (dict(cols=48), _lib.ERR_SHAPE),
+    (dict(cap=96), _lib.ERR_SHAPE),                   # below rows + 31 * groups
+    (dict(src=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(mode=9), _lib.ERR_INVALID_ARGUMENT),
+    (dict(x=FAKE + 4), _lib.ERR_ALIGNMENT),
+    (dict(E=0), _lib.ERR_UNSUPPORTED),
+])
+def test_gather_quant_dual_rejects(lib, kw, status):
+    assert _gather_dual(lib, **kw) == status
+
+
+def _combine(lib, **kw):
+    a = dict(y=FAKE, rows=64, cols=64, ldy=64, perm=FAKE, scores=None, T=16, K=2, out=FAKE, ldo=64)
+    a.update(kw)
+    return lib.mxgg_combine(a["y"], a["rows"], a["cols"], a["ldy"], a["perm"], a["scores"],
+                            a["T"], a["K"], a["out"], a["ldo"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(cols=12), _lib.ERR_SHAPE),
+    (dict(K=0), _lib.ERR_SHAPE),
+    (dict(ldy=32), _lib.ERR_SHAPE),
+    (dict(out=FAKE + 2), _lib.ERR_ALIGNMENT),
+    (dict(perm=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(T=1 << 27), _lib.ERR_UNSUPPORTED),
+])
+def test_combine_rejects(lib, kw, status):
+    assert _combine(lib, **kw) == status
+
+
+def test_combine_empty_is_noop(lib):
+    assert _combine(lib, T=0) == _lib.OK
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(cols=12), _lib.ERR_SHAPE),
+    (dict(K=0), _lib.ERR_SHAPE),
+    (dict(y=FAKE + 8), _lib.ERR_ALIGNMENT),
+    (dict(perm=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(grad=None), _lib.ERR_INVALID_ARGUMENT),
+])
+def test_combine_score_grad_rejects(lib, kw, status):
+    a = dict(d=FAKE, ldd=64, y=FAKE, rows=64, cols=64, ldy=64, perm=FAKE, T=16, K=2, grad=FAKE)
+    a.update(kw)
+    assert lib.mxgg_combine_score_grad(a["d"], a["ldd"], a["y"], a["rows"], a["cols"], a["ldy"],
+                                       a["perm"], a["T"], a["K"], a["grad"], None) == status

@@ -10,6 +10,9 @@ Each check is independent of the oracle's own formulas:
     :310, :391), against pure-Python loops on tiny inputs, and the exact
     power-of-two scaling invariant;
   * dim1: against the transposed dim0 cast of each zero-padded group.
+  * routing: against a hand-worked plan, torch's stable argsort of the expert
+    ids (the dispatcher's own formula), torch's index ops for the gather and
+    combine, and torch autograd for the combine's score gradient.
 """
 import json
 import math
@@ -416,3 +419,88 @@ def test_swiglu_special_points():
     assert abs(a[2]) < 1e-7 and abs(dg[2]) < 1e-6
     assert a[3] == np.inf and np.isnan(a[4])                   # -inf / (1 + inf) = NaN
     assert np.isnan(a[5]) and np.isnan(dg[5]) and np.isnan(du[5])
+
+
+# ---------------------------------------------------------------------------
+# Token routing (dispatch plan, gather, combine)
+# ---------------------------------------------------------------------------
+def test_route_plan_known_answer():
+    # slots 0..5 go to experts 2,0,0,1,2,2; groups padded to 4 rows
+    perm, src, ends, counts = O.route_plan(np.array([[2, 0], [0, 1], [2, 2]]), 3, 4, 16)
+    assert perm.tolist() == [8, 0, 1, 4, 9, 10]
+    assert src.tolist() == [1, 2, -1, -1, 3, -1, -1, -1, 0, 4, 5, -1, -1, -1, -1, -1]
+    assert ends.tolist() == [4, 8, 12] and counts.tolist() == [2, 1, 3]
+
+
+@pytest.mark.parametrize("T,K,E,pad,seed", [(50, 1, 4, 1, 0), (300, 8, 32, 1, 1), (97, 3, 7, 32, 2),
+                                            (64, 8, 256, 128, 3), (5, 2, 1, 32, 4)])
+def test_route_plan_is_torch_stable_argsort(T, K, E, pad, seed):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randint(0, E, (T, K), generator=g)
+    perm, src, ends, counts = O.route_plan(idx.numpy(), E, pad, T * K + E * (pad - 1))
+    order = torch.argsort(idx.reshape(-1), stable=True).numpy()   # torchtitan's dispatch order
+    assert np.array_equal(src[src >= 0], order)
+    assert np.array_equal(perm[src[src >= 0]], np.flatnonzero(src >= 0))
+    assert np.array_equal(counts, torch.bincount(idx.reshape(-1), minlength=E).numpy())
+    padded = -(-counts // pad) * pad
+    assert np.array_equal(ends, np.cumsum(padded))
+    for e in range(E):   # each group: its slots first, then empty rows
+        lo = ends[e] - padded[e]
+        assert np.all(src[lo:lo + counts[e]] >= 0) and np.all(src[lo + counts[e]:ends[e]] == -1)
+    assert np.all(src[ends[-1]:] == -1)
+
+
+def test_route_plan_drops_out_of_range_ids():
+    idx = np.array([[0, 5], [-1, 1], [1, 0]])
+    perm, src, ends, counts = O.route_plan(idx, 2, 1, 6)
+    assert perm.tolist() == [0, -1, -1, 2, 3, 1]
+    assert counts.tolist() == [2, 2] and ends.tolist() == [2, 4]
+    assert src.tolist() == [0, 5, 3, 4, -1, -1]
+
+
+def _bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def test_gather_and_combine_match_torch_index_ops():
+    g = torch.Generator().manual_seed(5)
+    T, K, E, H = 40, 4, 6, 24
+    idx = torch.randint(0, E, (T, K), generator=g)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    sc = torch.rand(T, K, generator=g)
+    perm, src, ends, _ = O.route_plan(idx.numpy(), E, 1, T * K)
+    order = torch.argsort(idx.reshape(-1), stable=True)
+    # gather: the dispatcher's routed input x[sorted // topk], and its scaled form
+    assert np.array_equal(O.gather_rows(_bf16_bits(x), src, K), _bf16_bits(x[order // K]))
+    scaled = (x[order // K].float() * sc.reshape(-1)[order][:, None]).to(torch.bfloat16)
+    assert np.array_equal(O.gather_rows(_bf16_bits(x), src, K, sc.numpy()), _bf16_bits(scaled))
+    # combine with topk = 1 puts every routed row back in place
+    perm1, src1, _, _ = O.route_plan(idx[:, :1].numpy(), E, 1, T)
+    y1 = O.gather_rows(_bf16_bits(x), src1, 1)
+    assert np.array_equal(O.combine(y1, perm1, 1), _bf16_bits(x))
+    # combine: the dispatcher's scaled scatter-add, summed exactly (float64)
+    y = torch.randn(T * K, H, generator=g).to(torch.bfloat16)
+    terms = (y[torch.from_numpy(perm).long()].float() * sc.reshape(-1)[:, None]).to(torch.bfloat16)
+    exact = torch.zeros(T, H, dtype=torch.float64).index_add_(
+        0, torch.arange(T).repeat_interleave(K), terms.double())
+    got = O.bits_to_f32(O.combine(_bf16_bits(y), perm, K, sc.numpy())).astype(np.float64)
+    ref = exact.to(torch.bfloat16).float().numpy().astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))) - 7)
+    assert np.all(np.abs(got - ref) <= ulp)                # at most one bf16 ulp (fp32 sum order)
+    assert np.mean(got != ref) < 0.01
+
+
+def test_combine_score_grad_matches_torch_autograd():
+    g = torch.Generator().manual_seed(6)
+    T, K, E, H = 16, 2, 3, 32
+    idx = torch.randint(0, E, (T, K), generator=g)
+    perm, _, _, _ = O.route_plan(idx.numpy(), E, 1, T * K)
+    y = torch.randn(T * K, H, generator=g).to(torch.bfloat16)
+    d = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    sc = torch.rand(T, K, generator=g, dtype=torch.float64).requires_grad_(True)
+    # the combine as torch ops (rounding steps are identity for autograd)
+    terms = y[torch.from_numpy(perm).long()].double().reshape(T, K, H) * sc[:, :, None]
+    out = terms.sum(1)
+    out.backward(d.double())
+    got = O.combine_score_grad(_bf16_bits(d), _bf16_bits(y), perm, K)
+    assert np.allclose(got, sc.grad.numpy(), rtol=1e-12, atol=1e-12)
