@@ -13,7 +13,8 @@ forward, the C4 weight gradient (fp32 dW), the bf16->MXFP8 casts, and the
 reference's CPU path (dequantise + per-group fp32 matmul with torch on the
 host cores) on a bounded sample of C2.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only fwd|wgrad|copy|ref8|c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                      [--only fwd|wgrad|copy|ref8|c5|routing]
 """
 import argparse
 import json
@@ -146,6 +147,61 @@ def layer_step_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     return out
 
 
+def routing_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
+    """C5 as a routed MoE layer: 16384 tokens x top-8 over 32 experts (Zipf(1.0)
+    preference), hidden 7168, intermediate 2048.  Times the device dispatch
+    plan, the dual MXFP8 cast gathered from token order (against the gather
+    and the plain dual cast of the routed rows it replaces), the score-weighted
+    combine and its score gradient, and the whole routed layer step (plan,
+    casts, six GEMMs, SwiGLU, combine; forward + backward) through
+    mxfp8gg.moe_routed_ffn.  Bytes are algorithmic: bf16 rows read and
+    written, 1 + 1/32 bytes per element of each MXFP8 cast."""
+    idx_np, sc_np = workloads.c5_routing()
+    T, K = idx_np.shape
+    H, F, E = 7168, 2048, 32
+    idx = torch.from_numpy(idx_np).to(dev)
+    sc = torch.from_numpy(sc_np).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16)
+    plan = mxfp8gg.route_plan(idx, E)
+    rows, slots, cast = plan.rows, T * K, 1 + 1 / 32
+    ms_plan = time_launches(lambda: mxfp8gg.route_plan(idx, E), 20, 3, torch)
+    ms_gd = time_launches(lambda: mxfp8gg.gather_to_mxfp8_dual(x, plan), 10, 3, torch)
+    ms_g = time_launches(lambda: mxfp8gg.gather_rows(x, plan), 10, 3, torch)
+    xr = mxfp8gg.gather_rows(x, plan)
+    ms_d = time_launches(lambda: mxfp8gg.to_mxfp8_dual(xr, plan.offs), 10, 3, torch)
+    del xr
+    b_dual = rows * H * (2 + 2 * cast)
+    y = torch.randn((rows, H), generator=gen, device=dev).to(torch.bfloat16)
+    d = torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16)
+    ms_c = time_launches(lambda: mxfp8gg.combine(y, plan, sc), 10, 3, torch)
+    ms_sg = time_launches(lambda: mxfp8gg.combine_score_grad(d, y, plan), 10, 3, torch)
+    del y
+    b_comb = slots * H * 2 + T * H * 2
+    out = {"tokens": T, "topk": K, "routed_rows": slots, "layout_rows": rows,
+           "route_plan_us": round(ms_plan * 1e3, 1),
+           "gather_dual_cast": {"ms": round(ms_gd, 4), "GBps": round(b_dual / ms_gd / 1e6, 1)},
+           "gather_then_dual_cast_ms": round(ms_g + ms_d, 4),
+           "combine": {"ms": round(ms_c, 4), "GBps": round(b_comb / ms_c / 1e6, 1)},
+           "combine_score_grad": {"ms": round(ms_sg, 4), "GBps": round(b_comb / ms_sg / 1e6, 1)}}
+    wgu = (torch.randn((E, 2 * F, H), generator=gen, device=dev) * 0.006).to(torch.bfloat16)
+    wd = (torch.randn((E, H, F), generator=gen, device=dev) * 0.006).to(torch.bfloat16)
+    leaves = [t.requires_grad_(True) for t in (x, sc, wgu, wd)]
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        mxfp8gg.moe_routed_ffn(x, idx, sc, wgu, wd).backward(d)
+
+    ms = time_launches(step, steps, warmup, torch)
+    flops = 18 * slots * F * H
+    out["layer_step"] = {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 1),
+                         "frac_of_peak": round(flops / ms / 1e9 / PEAK_MXFP8_TFLOPS, 4)}
+    for t in leaves:
+        t.grad = None
+    return out
+
+
 def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, budget_s=12.0):
     """The reference's CPU path on a bounded sample of the workload: whole
     experts of C2, in order, until `budget_s` of CPU work has run."""
@@ -187,11 +243,12 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "c5"], default="all",
+    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "c5", "routing"],
+                    default="all",
                     help="fwd / wgrad: time only that GEMM (for profiler runs); copy: a plain "
                          "1 GiB device-to-device copy, the reference for HBM byte counters; "
                          "ref8: the reference's 8 equal-group shapes only; c5: the full "
-                         "expert-FFN layer step only")
+                         "expert-FFN layer step only; routing: C5 as a routed top-8 layer")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the MXFP8 grouped GEMM shards by expert and "
@@ -209,6 +266,9 @@ def main():
 
     if args.only == "c5":
         print(json.dumps(layer_step_c5(torch, mxfp8gg, workloads, dev)), flush=True)
+        return
+    if args.only == "routing":
+        print(json.dumps(routing_c5(torch, mxfp8gg, workloads, dev)), flush=True)
         return
     if args.only == "ref8":
         print(json.dumps(ref_equal_shapes(torch, mxfp8gg, workloads, dev)), flush=True)
@@ -309,6 +369,8 @@ def main():
         components["ref_equal_shapes"] = ref_equal_shapes(torch, mxfp8gg, workloads, dev)
         log("C5: expert-FFN layer step (forward + backward)")
         components["layer_step_c5"] = layer_step_c5(torch, mxfp8gg, workloads, dev)
+        log("C5 as a routed top-8 layer (dispatch, combine)")
+        components["routing_c5"] = routing_c5(torch, mxfp8gg, workloads, dev)
 
     traffic = None
     tfile = ROOT / "profiles" / "traffic_grouped_fwd_c2.json"
