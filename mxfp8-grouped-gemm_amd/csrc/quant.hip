@@ -188,10 +188,12 @@ struct RowOut {
   int64_t ldq, s_row, s_blk;
 };
 
-// GATHER: row r of the cast's input is row src[r] / topk of x (zero when
-// src[r] < 0 or that token is not below xrows), optionally times
-// scale[src[r]] rounded to bf16: the routed layout of a top-k MoE layer read
-// straight from token order (the dispatch's gather, or the combine's backward).
+// GATHER (1, or 2 with row factors): row r of the cast's input is row
+// src[r] / topk of x (zero when src[r] < 0 or that token is not below xrows),
+// with GATHER 2 times scale[src[r]] rounded to bf16: the routed layout of a
+// top-k MoE layer read straight from token order (the dispatch's gather, or
+// the combine's backward).  Separate instantiations keep the plain gather's
+// registers free of the factors.
 struct Gather {
   const int32_t* src;
   const float* scale;
@@ -199,7 +201,7 @@ struct Gather {
   int topk;
 };
 
-template <int MODE, bool SW, bool ROW, bool GATHER>
+template <int MODE, bool SW, bool ROW, int GATHER>
 __global__ __launch_bounds__(256) void k_quant_dim1(
     const uint16_t* __restrict__ x, int64_t rows, int cols, int64_t ldx,
     const int32_t* __restrict__ ends, const int32_t* __restrict__ ends_pad, int E,
@@ -226,7 +228,8 @@ __global__ __launch_bounds__(256) void k_quant_dim1(
   if (f >= cols) ntok = 0;
 
   uint4 v[16];
-  if (GATHER) {
+  if (GATHER == 1) {
+    // all 16 row indices first, then all 16 rows: two load latencies, not 16
     int32_t sl[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) sl[i] = i < ntok ? ga.src[tok0 + i] : -1;
@@ -236,11 +239,26 @@ __global__ __launch_bounds__(256) void k_quant_dim1(
       v[i] = t < ga.xrows ? *reinterpret_cast<const uint4*>(x + t * ldx + f)
                           : make_uint4(0, 0, 0, 0);
     }
-    if (ga.scale != nullptr) {
+  } else if (GATHER == 2) {
+    // the row factors are loaded together with the rows so that their
+    // latency overlaps
+    int32_t sl[16], t[16];
+    float sc[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (sl[i] >= 0 && sl[i] / ga.topk < ga.xrows) v[i] = scale_chunk(v[i], ga.scale[sl[i]]);
+    for (int i = 0; i < 16; ++i) sl[i] = i < ntok ? ga.src[tok0 + i] : -1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t ti = sl[i] >= 0 ? sl[i] / ga.topk : ga.xrows;
+      t[i] = ti < ga.xrows ? (int32_t)ti : -1;
+      sc[i] = t[i] >= 0 ? ga.scale[sl[i]] : 0.0f;
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      v[i] = t[i] >= 0 ? *reinterpret_cast<const uint4*>(x + (int64_t)t[i] * ldx + f)
+                       : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (t[i] >= 0) v[i] = scale_chunk(v[i], sc[i]);
   } else {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -332,7 +350,7 @@ hipError_t dim0_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
   return hipGetLastError();
 }
 
-template <int MODE, bool SW, bool ROW, bool GATHER>
+template <int MODE, bool SW, bool ROW, int GATHER>
 hipError_t dim1_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
                      const int32_t* ends, int64_t E, int64_t cap, uint8_t* qt, int64_t ldqt,
                      uint8_t* st, int64_t st_row, int64_t st_blk, int32_t* ends_pad,
@@ -395,7 +413,7 @@ hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int6
                            nullptr, 0, qt, ldqt, st, ldst, layout, group_ends_pad, mode, stream);
 }
 
-template <bool GATHER>
+template <int GATHER>
 hipError_t quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
                       const int32_t* group_ends, int64_t num_groups, int64_t rows_pad_cap,
                       uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, uint8_t* qt, int64_t ldqt,
@@ -432,8 +450,8 @@ hipError_t launch_quant_dual(const uint16_t* x, int64_t rows, int64_t cols, int6
                              int64_t rows_pad_cap, uint8_t* q, int64_t ldq, uint8_t* s,
                              int64_t lds, uint8_t* qt, int64_t ldqt, uint8_t* st, int64_t ldst,
                              int layout, int32_t* group_ends_pad, int mode, hipStream_t stream) {
-  return quant_dual<false>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, q, ldq, s, lds,
-                           qt, ldqt, st, ldst, layout, group_ends_pad, mode, Gather{}, stream);
+  return quant_dual<0>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, q, ldq, s, lds,
+                       qt, ldqt, st, ldst, layout, group_ends_pad, mode, Gather{}, stream);
 }
 
 hipError_t launch_gather_quant_dual(const uint16_t* x, int64_t xrows, int64_t ldx,
@@ -448,8 +466,11 @@ hipError_t launch_gather_quant_dual(const uint16_t* x, int64_t xrows, int64_t ld
   ga.scale = row_scale;
   ga.xrows = xrows;
   ga.topk = topk;
-  return quant_dual<true>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, q, ldq, s, lds,
-                          qt, ldqt, st, ldst, layout, group_ends_pad, mode, ga, stream);
+  if (row_scale != nullptr)
+    return quant_dual<2>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, q, ldq, s, lds,
+                         qt, ldqt, st, ldst, layout, group_ends_pad, mode, ga, stream);
+  return quant_dual<1>(x, rows, cols, ldx, group_ends, num_groups, rows_pad_cap, q, ldq, s, lds,
+                       qt, ldqt, st, ldst, layout, group_ends_pad, mode, ga, stream);
 }
 
 hipError_t launch_pad_ends(const int32_t* group_ends, int64_t num_groups, int64_t rows,
