@@ -153,15 +153,54 @@ __global__ __launch_bounds__(256) void k_gather_rows(
 
 // One wave per token.  out[t] = bf16(sum_k term_k), term_k =
 // float(bf16(float(y[perm[s]]) * score[s])) (or the row itself without scores).
+// Up to 8 slots per token: the slots' rows and factors are read once (they
+// are the same for the whole wave) and every chunk's 8 row loads go out
+// together; the sum stays in k order.  More slots take the general loop.
+constexpr int kCombineSlots = 8;
+
 template <bool SCORES>
 __global__ __launch_bounds__(256) void k_combine(
     const uint16_t* __restrict__ y, int64_t ldy, int64_t yrows, const int32_t* __restrict__ perm,
     const float* __restrict__ scores, int64_t tokens, int topk, int chunks,
     uint16_t* __restrict__ out, int64_t ldo) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t t = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (t >= tokens) return;
   const int32_t* pt = perm + t * topk;
+  uint16_t* o = out + t * ldo;
+  if (topk <= kCombineSlots) {
+    int32_t r[kCombineSlots];
+    float sc[kCombineSlots];
+#pragma unroll
+    for (int k = 0; k < kCombineSlots; ++k) {
+      const int32_t rk = k < topk ? pt[k] : -1;
+      r[k] = rk >= 0 && rk < yrows ? rk : -1;
+      sc[k] = SCORES && k < topk ? scores[t * topk + k] : 1.0f;
+    }
+    for (int c = lane; c < chunks; c += 64) {
+      uint4 v[kCombineSlots];
+#pragma unroll
+      for (int k = 0; k < kCombineSlots; ++k)
+        v[k] = r[k] >= 0 ? *reinterpret_cast<const uint4*>(y + (int64_t)r[k] * ldy + 8 * c)
+                         : make_uint4(0, 0, 0, 0);
+      float acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kCombineSlots; ++k) {
+        if (r[k] < 0) continue;
+        const uint4 w = SCORES ? scale_chunk(v[k], sc[k]) : v[k];
+        acc[0] += bf16_lo(w.x); acc[1] += bf16_hi(w.x);
+        acc[2] += bf16_lo(w.y); acc[3] += bf16_hi(w.y);
+        acc[4] += bf16_lo(w.z); acc[5] += bf16_hi(w.z);
+        acc[6] += bf16_lo(w.w); acc[7] += bf16_hi(w.w);
+      }
+      *reinterpret_cast<uint4*>(o + 8 * c) =
+          make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
+                     pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7]));
+    }
+    return;
+  }
   for (int c = lane; c < chunks; c += 64) {
     float acc[8];
 #pragma unroll
@@ -176,42 +215,59 @@ __global__ __launch_bounds__(256) void k_combine(
       acc[4] += bf16_lo(v.z); acc[5] += bf16_hi(v.z);
       acc[6] += bf16_lo(v.w); acc[7] += bf16_hi(v.w);
     }
-    *reinterpret_cast<uint4*>(out + t * ldo + 8 * c) =
+    *reinterpret_cast<uint4*>(o + 8 * c) =
         make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
                    pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7]));
   }
 }
 
+__device__ __forceinline__ float dot_chunk(const uint4& d, const uint4& v, float acc) {
+  acc = __builtin_fmaf(bf16_lo(d.x), bf16_lo(v.x), acc);
+  acc = __builtin_fmaf(bf16_hi(d.x), bf16_hi(v.x), acc);
+  acc = __builtin_fmaf(bf16_lo(d.y), bf16_lo(v.y), acc);
+  acc = __builtin_fmaf(bf16_hi(d.y), bf16_hi(v.y), acc);
+  acc = __builtin_fmaf(bf16_lo(d.z), bf16_lo(v.z), acc);
+  acc = __builtin_fmaf(bf16_hi(d.z), bf16_hi(v.z), acc);
+  acc = __builtin_fmaf(bf16_lo(d.w), bf16_lo(v.w), acc);
+  return __builtin_fmaf(bf16_hi(d.w), bf16_hi(v.w), acc);
+}
+
 // One wave per token: d_score[s] = sum_h float(dout[t][h]) * float(y[perm[s]][h]),
-// 0 for a dropped slot.
+// 0 for a dropped slot.  Up to 8 slots per token share one read of dout.
 __global__ __launch_bounds__(256) void k_combine_score_grad(
     const uint16_t* __restrict__ dout, int64_t ldd, const uint16_t* __restrict__ y, int64_t ldy,
     int64_t yrows, const int32_t* __restrict__ perm, int64_t tokens, int topk, int chunks,
     float* __restrict__ dscore) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t t = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (t >= tokens) return;
-  for (int k = 0; k < topk; ++k) {
-    const int32_t r = perm[t * topk + k];
-    const bool ok = r >= 0 && r < yrows;
-    float acc = 0.0f;
-    if (ok) {
-      for (int c = lane; c < chunks; c += 64) {
-        const uint4 d = *reinterpret_cast<const uint4*>(dout + t * ldd + 8 * c);
-        const uint4 v = *reinterpret_cast<const uint4*>(y + (int64_t)r * ldy + 8 * c);
-        acc = __builtin_fmaf(bf16_lo(d.x), bf16_lo(v.x), acc);
-        acc = __builtin_fmaf(bf16_hi(d.x), bf16_hi(v.x), acc);
-        acc = __builtin_fmaf(bf16_lo(d.y), bf16_lo(v.y), acc);
-        acc = __builtin_fmaf(bf16_hi(d.y), bf16_hi(v.y), acc);
-        acc = __builtin_fmaf(bf16_lo(d.z), bf16_lo(v.z), acc);
-        acc = __builtin_fmaf(bf16_hi(d.z), bf16_hi(v.z), acc);
-        acc = __builtin_fmaf(bf16_lo(d.w), bf16_lo(v.w), acc);
-        acc = __builtin_fmaf(bf16_hi(d.w), bf16_hi(v.w), acc);
-      }
+  const uint16_t* dr = dout + t * ldd;
+  for (int k0 = 0; k0 < topk; k0 += kCombineSlots) {
+    int32_t r[kCombineSlots];
+#pragma unroll
+    for (int k = 0; k < kCombineSlots; ++k) {
+      const int32_t rk = k0 + k < topk ? perm[t * topk + k0 + k] : -1;
+      r[k] = rk >= 0 && rk < yrows ? rk : -1;
+    }
+    float acc[kCombineSlots];
+#pragma unroll
+    for (int k = 0; k < kCombineSlots; ++k) acc[k] = 0.0f;
+    for (int c = lane; c < chunks; c += 64) {
+      const uint4 d = *reinterpret_cast<const uint4*>(dr + 8 * c);
+      uint4 v[kCombineSlots];
+#pragma unroll
+      for (int k = 0; k < kCombineSlots; ++k)
+        v[k] = r[k] >= 0 ? *reinterpret_cast<const uint4*>(y + (int64_t)r[k] * ldy + 8 * c)
+                         : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int k = 0; k < kCombineSlots; ++k) acc[k] = dot_chunk(d, v[k], acc[k]);
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-    if (lane == 0) dscore[t * topk + k] = ok ? acc : 0.0f;
+    for (int k = 0; k < kCombineSlots; ++k) {
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) acc[k] += __shfl_xor(acc[k], off);
+      if (lane == 0 && k0 + k < topk) dscore[t * topk + k0 + k] = r[k] >= 0 ? acc[k] : 0.0f;
+    }
   }
 }
 

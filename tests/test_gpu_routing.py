@@ -104,7 +104,8 @@ def test_gather_to_mxfp8_dual_equals_cast_of_gathered_rows(gpu, mode_name, mode,
 
 
 @pytest.mark.parametrize("scaled", [False, True])
-@pytest.mark.parametrize("T,K,E,H", [(257, 8, 32, 64), (40, 1, 3, 24), (1, 2, 2, 8)])
+@pytest.mark.parametrize("T,K,E,H", [(257, 8, 32, 64), (40, 1, 3, 24), (1, 2, 2, 8),
+                                     (50, 10, 16, 40)])   # top-10: the general slot loop
 def test_combine_matches_oracle(gpu, scaled, T, K, E, H):
     idx = _idx(gpu, T, K, E, 8, drop=True)
     plan = mxfp8gg.route_plan(idx, E, 32)
@@ -124,7 +125,7 @@ def test_combine_inverts_gather_for_top1(gpu):
     assert torch.equal(mxfp8gg.combine(mxfp8gg.gather_rows(x, plan), plan), x)
 
 
-@pytest.mark.parametrize("T,K,E,H", [(130, 4, 9, 256), (16, 8, 32, 7168)])
+@pytest.mark.parametrize("T,K,E,H", [(130, 4, 9, 256), (16, 8, 32, 7168), (33, 11, 12, 64)])
 def test_combine_score_grad_matches_oracle(gpu, T, K, E, H):
     idx = _idx(gpu, T, K, E, 11, drop=True)
     plan = mxfp8gg.route_plan(idx, E, 32)
