@@ -35,6 +35,7 @@ namespace {
 
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanWaves = kPlanThreads / 64;
+constexpr int kPlanPrefetch = 8;  // 64-slot chunks whose ids are loaded together
 
 // Lanes of the wave whose key equals this lane's (keys < 2^nbits).
 __device__ __forceinline__ uint64_t match_key(uint32_t key, int nbits) {
@@ -64,12 +65,17 @@ __global__ __launch_bounds__(kPlanThreads) void k_route_plan(
   const int64_t beg = std::min<int64_t>((int64_t)w * per, n);
   const int64_t end = std::min<int64_t>(beg + per, n);
   int32_t* h = hist + w * E;
-  for (int64_t c0 = beg; c0 < end; c0 += 64) {
-    const int64_t s = c0 + lane;
-    if (s < end) {
-      const int32_t e = idx[s];
-      if (e >= 0 && e < E) atomicAdd(&h[e], 1);
+  // the ids of 8 chunks are loaded together, so 8 loads are in flight
+  for (int64_t b0 = beg; b0 < end; b0 += 64 * kPlanPrefetch) {
+    int32_t ev[kPlanPrefetch];
+#pragma unroll
+    for (int j = 0; j < kPlanPrefetch; ++j) {
+      const int64_t s = b0 + 64 * j + lane;
+      ev[j] = s < end ? idx[s] : -1;
     }
+#pragma unroll
+    for (int j = 0; j < kPlanPrefetch; ++j)
+      if (ev[j] >= 0 && ev[j] < E) atomicAdd(&h[ev[j]], 1);
   }
   __syncthreads();
 
@@ -105,23 +111,32 @@ __global__ __launch_bounds__(kPlanThreads) void k_route_plan(
 
   // Ranks: keys 0..E-1 are experts, E marks a dropped or absent slot.
   const int nbits = 32 - __builtin_clz((unsigned)E);
-  for (int64_t c0 = beg; c0 < end; c0 += 64) {
-    const int64_t s = c0 + lane;
-    const bool active = s < end;
-    const int32_t e = active ? idx[s] : -1;
-    const bool valid = active && e >= 0 && e < E;
-    const uint32_t key = valid ? (uint32_t)e : (uint32_t)E;
-    const uint64_t peers = match_key(key, nbits);
-    const uint64_t below = (1ull << lane) - 1ull;
-    const uint64_t upto = (2ull << lane) - 1ull;  // lane 63: all lanes
-    if (valid) {
-      const int32_t base = h[e];
-      const int32_t dest = base + __popcll(peers & below);
-      perm[s] = dest;
-      if (dest < cap) src[dest] = (int32_t)s;  // always true: dest < group end <= cap
-      if ((peers & ~upto) == 0) h[e] = base + __popcll(peers);  // last lane of the group
-    } else if (active) {
-      perm[s] = -1;
+  for (int64_t b0 = beg; b0 < end; b0 += 64 * kPlanPrefetch) {
+    int32_t ev[kPlanPrefetch];
+#pragma unroll
+    for (int j = 0; j < kPlanPrefetch; ++j) {
+      const int64_t s = b0 + 64 * j + lane;
+      ev[j] = s < end ? idx[s] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kPlanPrefetch; ++j) {
+      const int64_t s = b0 + 64 * j + lane;
+      const bool active = s < end;
+      const int32_t e = ev[j];
+      const bool valid = active && e >= 0 && e < E;
+      const uint32_t key = valid ? (uint32_t)e : (uint32_t)E;
+      const uint64_t peers = match_key(key, nbits);
+      const uint64_t below = (1ull << lane) - 1ull;
+      const uint64_t upto = (2ull << lane) - 1ull;  // lane 63: all lanes
+      if (valid) {
+        const int32_t base = h[e];
+        const int32_t dest = base + __popcll(peers & below);
+        perm[s] = dest;
+        if (dest < cap) src[dest] = (int32_t)s;  // always true: dest < group end <= cap
+        if ((peers & ~upto) == 0) h[e] = base + __popcll(peers);  // last lane of the group
+      } else if (active) {
+        perm[s] = -1;
+      }
     }
   }
 }
