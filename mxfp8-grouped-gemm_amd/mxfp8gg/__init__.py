@@ -1,9 +1,11 @@
 """mxfp8gg — MXFP8 grouped GEMM for AMD MI355X (gfx950).
 
 bf16 -> MXFP8 casts, a forward grouped GEMM and a weight-gradient grouped GEMM
-over ragged expert groups, all as hand-written HIP kernels in libmxgg.so
-behind a C ABI (include/mxgg.h).  This package is the host side: it takes
-torch tensors, allocates outputs, and calls the library on the current stream.
+over ragged expert groups, the expert FFN's fused SwiGLU casts, and the token
+routing (dispatch plan, gather, combine) around them, all as hand-written HIP
+kernels in libmxgg.so behind a C ABI (include/mxgg.h).  This package is the
+host side: it takes torch tensors, allocates outputs, and calls the library on
+the current stream.
 """
 from ._lib import MxggError, load as load_library
 from .ops import (
