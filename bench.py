@@ -154,7 +154,8 @@ def routing_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     and the plain dual cast of the routed rows it replaces), the score-weighted
     combine and its score gradient, and the whole routed layer step (plan,
     casts, six GEMMs, SwiGLU, combine; forward + backward) through
-    mxfp8gg.moe_routed_ffn.  Bytes are algorithmic: bf16 rows read and
+    mxfp8gg.moe_routed_ffn, and its forward-only pass (no autograd, weight
+    casts cached: the inference step).  Bytes are algorithmic: bf16 rows read and
     written, 1 + 1/32 bytes per element of each MXFP8 cast."""
     idx_np, sc_np = workloads.c5_routing()
     T, K = idx_np.shape
@@ -171,7 +172,9 @@ def routing_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     xr = mxfp8gg.gather_rows(x, plan)
     ms_d = time_launches(lambda: mxfp8gg.to_mxfp8_dual(xr, plan.offs), 10, 3, torch)
     del xr
+    ms_g0 = time_launches(lambda: mxfp8gg.gather_to_mxfp8_dim0(x, plan), 10, 3, torch)
     b_dual = rows * H * (2 + 2 * cast)
+    b_dim0 = rows * H * (2 + cast)
     y = torch.randn((rows, H), generator=gen, device=dev).to(torch.bfloat16)
     d = torch.randn((T, H), generator=gen, device=dev).to(torch.bfloat16)
     ms_c = time_launches(lambda: mxfp8gg.combine(y, plan, sc), 10, 3, torch)
@@ -182,6 +185,7 @@ def routing_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
            "route_plan_us": round(ms_plan * 1e3, 1),
            "gather_dual_cast": {"ms": round(ms_gd, 4), "GBps": round(b_dual / ms_gd / 1e6, 1)},
            "gather_then_dual_cast_ms": round(ms_g + ms_d, 4),
+           "gather_dim0_cast": {"ms": round(ms_g0, 4), "GBps": round(b_dim0 / ms_g0 / 1e6, 1)},
            "combine": {"ms": round(ms_c, 4), "GBps": round(b_comb / ms_c / 1e6, 1)},
            "combine_score_grad": {"ms": round(ms_sg, 4), "GBps": round(b_comb / ms_sg / 1e6, 1)}}
     wgu = (torch.randn((E, 2 * F, H), generator=gen, device=dev) * 0.006).to(torch.bfloat16)
@@ -197,6 +201,18 @@ def routing_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     flops = 18 * slots * F * H
     out["layer_step"] = {"ms": round(ms, 3), "tflops": round(flops / ms / 1e9, 1),
                          "frac_of_peak": round(flops / ms / 1e9 / PEAK_MXFP8_TFLOPS, 4)}
+    cache = mxfp8gg.WeightCastCache()
+
+    def fwd():
+        with torch.no_grad():
+            mxfp8gg.moe_routed_ffn(x, idx, sc, wgu, wd, weight_cache=cache)
+
+    ms_f = time_launches(fwd, steps, warmup, torch)
+    flops_f = 6 * slots * F * H
+    out["forward_only_cached_weights"] = {
+        "ms": round(ms_f, 3), "tflops": round(flops_f / ms_f / 1e9, 1),
+        "frac_of_peak": round(flops_f / ms_f / 1e9 / PEAK_MXFP8_TFLOPS, 4)}
+    del cache
     for t in leaves:
         t.grad = None
     return out

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 6
+#define MXGG_ABI_VERSION 7
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -309,6 +309,18 @@ int mxgg_gather_quant_dual(const void* x, int64_t tokens, int64_t cols, int64_t 
                            void* q, int64_t ldq, void* scales, int64_t lds, void* qt, int64_t ldqt,
                            void* scales_t, int64_t ldst, int scale_layout,
                            int32_t* group_ends_pad, int scale_mode, void* stream);
+
+/*
+ * mxgg_quant_dim0 of the routed rows (as mxgg_gather_rows would write them
+ * without row_scale), read straight from token order: the MXFP8 expert input
+ * of a forward-only pass, which needs no token-axis cast.  rows = rows of the
+ * routed layout (every row is written; padding rows as zero blocks); every
+ * other argument as mxgg_quant_dim0.
+ */
+int mxgg_gather_quant_dim0(const void* x, int64_t tokens, int64_t cols, int64_t ldx,
+                           const int32_t* src, int64_t topk, int64_t rows, void* q, int64_t ldq,
+                           void* scales, int64_t lds, int scale_layout, int scale_mode,
+                           void* stream);
 
 /*
  * Combine: out[t] = bf16(sum over k of float(bf16(float(y[perm[s]]) *

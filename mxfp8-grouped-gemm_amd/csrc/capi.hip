@@ -84,30 +84,38 @@ static bool valid_layout(int layout) {
   return layout == MXGG_SCALES_ROW_MAJOR || layout == MXGG_SCALES_BLOCK_MAJOR;
 }
 
-int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx, void* q, int64_t ldq,
-                    void* scales, int64_t lds, int scale_layout, int scale_mode, void* stream) {
+static int check_dim0(const char* what, const void* x, int64_t rows, int64_t cols, int64_t ldx,
+                      const void* q, int64_t ldq, const void* scales, int64_t lds,
+                      int scale_layout, int scale_mode) {
   const int mode = scale_mode & 0xFF;
   if (mode != MXGG_SCALE_RCEIL && mode != MXGG_SCALE_FLOOR)
-    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim0: unknown scale_mode %d", scale_mode);
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "%s: unknown scale_mode %d", what, scale_mode);
   if (!valid_layout(scale_layout))
-    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim0: unknown scale_layout %d",
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "%s: unknown scale_layout %d", what,
                      scale_layout);
   if (rows < 0 || cols < 0)
-    return set_error(MXGG_ERR_SHAPE, "quant_dim0: negative size rows=%lld cols=%lld",
+    return set_error(MXGG_ERR_SHAPE, "%s: negative size rows=%lld cols=%lld", what,
                      (long long)rows, (long long)cols);
   if (cols % 32 != 0)
-    return set_error(MXGG_ERR_SHAPE, "quant_dim0: cols=%lld is not a multiple of 32",
+    return set_error(MXGG_ERR_SHAPE, "%s: cols=%lld is not a multiple of 32", what,
                      (long long)cols);
   if (rows == 0 || cols == 0) return MXGG_OK;
-  if (!x || !q || !scales)
-    return set_error(MXGG_ERR_INVALID_ARGUMENT, "quant_dim0: null pointer");
+  if (!x || !q || !scales) return set_error(MXGG_ERR_INVALID_ARGUMENT, "%s: null pointer", what);
   if (ldx < cols || ldq < cols ||
       lds < (scale_layout == MXGG_SCALES_BLOCK_MAJOR ? rows : cols / 32))
-    return set_error(MXGG_ERR_SHAPE, "quant_dim0: leading dimension smaller than the row");
+    return set_error(MXGG_ERR_SHAPE, "%s: leading dimension smaller than the row", what);
   if (!aligned16(x) || !aligned16(q) || ldx % 8 != 0 || ldq % 8 != 0 ||
       (reinterpret_cast<uintptr_t>(q) & 7u) != 0)
     return set_error(MXGG_ERR_ALIGNMENT,
-                     "quant_dim0: x and q must be 16-byte aligned, ldx and ldq multiples of 8");
+                     "%s: x and q must be 16-byte aligned, ldx and ldq multiples of 8", what);
+  return MXGG_OK;
+}
+
+int mxgg_quant_dim0(const void* x, int64_t rows, int64_t cols, int64_t ldx, void* q, int64_t ldq,
+                    void* scales, int64_t lds, int scale_layout, int scale_mode, void* stream) {
+  const int st = check_dim0("quant_dim0", x, rows, cols, ldx, q, ldq, scales, lds, scale_layout,
+                            scale_mode);
+  if (st != MXGG_OK || rows == 0 || cols == 0) return st;
   return check_launch(launch_quant_dim0(static_cast<const uint16_t*>(x), rows, cols, ldx,
                                         static_cast<uint8_t*>(q), ldq,
                                         static_cast<uint8_t*>(scales), lds, scale_layout,
@@ -627,6 +635,26 @@ int mxgg_gather_quant_dual(const void* x, int64_t tokens, int64_t cols, int64_t 
                                static_cast<uint8_t*>(scales_t), ldst, scale_layout, group_ends_pad,
                                scale_mode, static_cast<hipStream_t>(stream)),
       "gather_quant_dual");
+}
+
+int mxgg_gather_quant_dim0(const void* x, int64_t tokens, int64_t cols, int64_t ldx,
+                           const int32_t* src, int64_t topk, int64_t rows, void* q, int64_t ldq,
+                           void* scales, int64_t lds, int scale_layout, int scale_mode,
+                           void* stream) {
+  if (tokens < 0 || topk < 1 || topk > INT32_MAX)
+    return set_error(MXGG_ERR_SHAPE, "gather_quant_dim0: tokens=%lld, topk=%lld",
+                     (long long)tokens, (long long)topk);
+  // x may be empty (no tokens): the check then needs a stand-in address
+  const void* xv = (x == nullptr && tokens == 0) ? q : x;
+  const int st = check_dim0("gather_quant_dim0", xv, rows, cols, ldx, q, ldq, scales, lds,
+                            scale_layout, scale_mode);
+  if (st != MXGG_OK || rows == 0 || cols == 0) return st;
+  if (!src) return set_error(MXGG_ERR_INVALID_ARGUMENT, "gather_quant_dim0: null src");
+  return check_launch(
+      launch_gather_quant_dim0(static_cast<const uint16_t*>(x), tokens, ldx, src, (int)topk, rows,
+                               cols, static_cast<uint8_t*>(q), ldq, static_cast<uint8_t*>(scales),
+                               lds, scale_layout, scale_mode, static_cast<hipStream_t>(stream)),
+      "gather_quant_dim0");
 }
 
 int mxgg_combine(const void* y, int64_t rows, int64_t cols, int64_t ldy, const int32_t* perm,

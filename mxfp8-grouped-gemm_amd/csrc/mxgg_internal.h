@@ -59,6 +59,13 @@ hipError_t launch_gather_quant_dual(const uint16_t* x, int64_t xrows, int64_t ld
                                     int64_t ldqt, uint8_t* st, int64_t ldst, int layout,
                                     int32_t* group_ends_pad, int mode, hipStream_t stream);
 
+// The row-wise cast of rows gathered from token order (row r = row
+// src[r] / topk of x, zero for src[r] < 0); rows = rows of the routed layout.
+hipError_t launch_gather_quant_dim0(const uint16_t* x, int64_t xrows, int64_t ldx,
+                                    const int32_t* src, int topk, int64_t rows, int64_t cols,
+                                    uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int layout,
+                                    int mode, hipStream_t stream);
+
 // Token routing (route.hip).
 hipError_t launch_route_plan(const int32_t* idx, int64_t n, int E, int pad, int64_t cap,
                              int32_t* perm, int32_t* src, int32_t* ends, int32_t* counts,

@@ -17,6 +17,19 @@ namespace {
 // of a quad hold one 32-element block and combine their amax with two xor
 // shuffles.  Each wave handles 4 rows per trip, a block 16 rows.
 // ---------------------------------------------------------------------------
+// GATHER (1, or 2 with row factors): row r of the cast's input is row
+// src[r] / topk of x (zero when src[r] < 0 or that token is not below xrows),
+// with GATHER 2 times scale[src[r]] rounded to bf16: the routed layout of a
+// top-k MoE layer read straight from token order (the dispatch's gather, or
+// the combine's backward).  Separate instantiations keep the plain gather's
+// registers free of the factors.
+struct Gather {
+  const int32_t* src;
+  const float* scale;
+  int64_t xrows;
+  int topk;
+};
+
 template <int MODE, bool SW, bool ANY>
 __device__ __forceinline__ void dim0_store(const uint4 (&v)[4], const uint32_t (&b)[4], uint8_t* q,
                                            int64_t ldq, uint8_t* s, int64_t s_row, int64_t s_blk,
@@ -33,25 +46,40 @@ __device__ __forceinline__ void dim0_store(const uint4 (&v)[4], const uint32_t (
   }
 }
 
-template <int MODE, bool SW>
+// GATHER: the rows are gathered from token order as in k_quant_dim1 (no row
+// factors): the row-wise cast of the routed layout for a forward-only pass.
+template <int MODE, bool SW, bool GATHER>
 __global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__ x, int64_t rows,
                                                     int cols8, int64_t ldx,
                                                     uint8_t* __restrict__ q, int64_t ldq,
                                                     uint8_t* __restrict__ s, int64_t s_row,
-                                                    int64_t s_blk) {
+                                                    int64_t s_blk, Gather ga) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int cc = blockIdx.x * 64 + lane;  // chunk column
   const bool col_ok = cc < cols8;         // whole quads share col_ok (cols8 % 4 == 0)
   for (int64_t r0 = (int64_t)blockIdx.y * 16 + wave * 4; r0 < rows; r0 += (int64_t)gridDim.y * 16) {
     uint4 v[4];
+    if (GATHER) {
+      int32_t sl[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t r = r0 + u;
-      if (col_ok && r < rows) {
-        v[u] = *reinterpret_cast<const uint4*>(x + r * ldx + (int64_t)cc * 8);
-      } else {
-        v[u] = make_uint4(0, 0, 0, 0);
+      for (int u = 0; u < 4; ++u) sl[u] = r0 + u < rows ? ga.src[r0 + u] : -1;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t t = sl[u] >= 0 ? sl[u] / ga.topk : ga.xrows;
+        v[u] = col_ok && t < ga.xrows
+                   ? *reinterpret_cast<const uint4*>(x + t * ldx + (int64_t)cc * 8)
+                   : make_uint4(0, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t r = r0 + u;
+        if (col_ok && r < rows) {
+          v[u] = *reinterpret_cast<const uint4*>(x + r * ldx + (int64_t)cc * 8);
+        } else {
+          v[u] = make_uint4(0, 0, 0, 0);
+        }
       }
     }
     uint32_t b[4];
@@ -186,19 +214,6 @@ struct RowOut {
   uint8_t* q;     // [rows, cols] row-wise payload
   uint8_t* s;     // scale bytes, byte (r, b) at s[r * s_row + b * s_blk]
   int64_t ldq, s_row, s_blk;
-};
-
-// GATHER (1, or 2 with row factors): row r of the cast's input is row
-// src[r] / topk of x (zero when src[r] < 0 or that token is not below xrows),
-// with GATHER 2 times scale[src[r]] rounded to bf16: the routed layout of a
-// top-k MoE layer read straight from token order (the dispatch's gather, or
-// the combine's backward).  Separate instantiations keep the plain gather's
-// registers free of the factors.
-struct Gather {
-  const int32_t* src;
-  const float* scale;
-  int64_t xrows;
-  int topk;
 };
 
 template <int MODE, bool SW, bool ROW, int GATHER>
@@ -340,13 +355,14 @@ __global__ __launch_bounds__(256) void k_quant_dim1(
   }
 }
 
-template <int MODE, bool SW>
+template <int MODE, bool SW, bool GATHER>
 hipError_t dim0_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx, uint8_t* q,
-                     int64_t ldq, uint8_t* s, int64_t s_row, int64_t s_blk, hipStream_t stream) {
+                     int64_t ldq, uint8_t* s, int64_t s_row, int64_t s_blk, const Gather& ga,
+                     hipStream_t stream) {
   const int cols8 = (int)(cols / 8);
   dim3 grid((cols8 + 63) / 64, (unsigned)std::min<int64_t>((rows + 15) / 16, 65535));
-  hipLaunchKernelGGL((k_quant_dim0<MODE, SW>), grid, dim3(256), 0, stream, x, rows, cols8, ldx, q,
-                     ldq, s, s_row, s_blk);
+  hipLaunchKernelGGL((k_quant_dim0<MODE, SW, GATHER>), grid, dim3(256), 0, stream, x, rows, cols8,
+                     ldx, q, ldq, s, s_row, s_blk, ga);
   return hipGetLastError();
 }
 
@@ -389,19 +405,42 @@ __global__ __launch_bounds__(256) void k_scales_to_block_major(
 
 }  // namespace
 
-hipError_t launch_quant_dim0(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
-                             uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int layout,
-                             int mode, hipStream_t stream) {
+template <bool GATHER>
+hipError_t quant_dim0(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx, uint8_t* q,
+                      int64_t ldq, uint8_t* s, int64_t lds, int layout, int mode,
+                      const Gather& ga, hipStream_t stream) {
   if (rows == 0 || cols == 0) return hipSuccess;
   const bool sw = (mode & kCvtSoftwareFlag) != 0;
   const int m = mode & 0xFF;
   const int64_t s_row = layout == MXGG_SCALES_BLOCK_MAJOR ? 1 : lds;
   const int64_t s_blk = layout == MXGG_SCALES_BLOCK_MAJOR ? lds : 1;
   if (m == kModeRceil)
-    return sw ? dim0_impl<kModeRceil, true>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk, stream)
-              : dim0_impl<kModeRceil, false>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk, stream);
-  return sw ? dim0_impl<kModeFloor, true>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk, stream)
-            : dim0_impl<kModeFloor, false>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk, stream);
+    return sw ? dim0_impl<kModeRceil, true, GATHER>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk,
+                                                    ga, stream)
+              : dim0_impl<kModeRceil, false, GATHER>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk,
+                                                     ga, stream);
+  return sw ? dim0_impl<kModeFloor, true, GATHER>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk,
+                                                  ga, stream)
+            : dim0_impl<kModeFloor, false, GATHER>(x, rows, cols, ldx, q, ldq, s, s_row, s_blk,
+                                                   ga, stream);
+}
+
+hipError_t launch_quant_dim0(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
+                             uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int layout,
+                             int mode, hipStream_t stream) {
+  return quant_dim0<false>(x, rows, cols, ldx, q, ldq, s, lds, layout, mode, Gather{}, stream);
+}
+
+hipError_t launch_gather_quant_dim0(const uint16_t* x, int64_t xrows, int64_t ldx,
+                                    const int32_t* src, int topk, int64_t rows, int64_t cols,
+                                    uint8_t* q, int64_t ldq, uint8_t* s, int64_t lds, int layout,
+                                    int mode, hipStream_t stream) {
+  Gather ga;
+  ga.src = src;
+  ga.scale = nullptr;
+  ga.xrows = xrows;
+  ga.topk = topk;
+  return quant_dim0<true>(x, rows, cols, ldx, q, ldq, s, lds, layout, mode, ga, stream);
 }
 
 hipError_t launch_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,

@@ -43,6 +43,7 @@ from .routing import (
     combine_score_grad,
     gather_rows,
     gather_to_mxfp8_dual,
+    gather_to_mxfp8_dim0,
     route_plan,
 )
 from .torchao_compat import (
@@ -64,6 +65,7 @@ __all__ = [
     "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",
     "WeightCastCache",
     "MXFP8GroupedMM", "mxfp8_grouped_mm", "MXFP8ExpertFFN", "moe_ffn", "moe_ffn_unfused",
-    "RoutePlan", "route_plan", "gather_rows", "gather_to_mxfp8_dual", "combine",
+    "RoutePlan", "route_plan", "gather_rows", "gather_to_mxfp8_dual", "gather_to_mxfp8_dim0",
+    "combine",
     "combine_score_grad", "MXFP8RoutedExpertFFN", "moe_routed_ffn",
 ]

@@ -31,7 +31,7 @@ OUT_F32 = 1
 SCALES_ROW_MAJOR = 0
 SCALES_BLOCK_MAJOR = 1
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -78,6 +78,9 @@ SIGNATURES = {
         _I,
         [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P, _I64,
          _P, _I64, _I, _P, _I, _P],
+    ),
+    "mxgg_gather_quant_dim0": (
+        _I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _I, _I, _P],
     ),
     "mxgg_combine": (_I, [_P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I64, _P]),
     "mxgg_combine_score_grad": (

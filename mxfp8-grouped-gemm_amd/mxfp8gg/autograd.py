@@ -263,6 +263,19 @@ class MXFP8RoutedExpertFFN(torch.autograd.Function):
         return dx, None, dsc, dwgu, dwd, None, None, None
 
 
+def _routed_forward_only(x, expert_idx, scores, w_gate_up, w_down, pad_multiple, scaling_mode,
+                         weight_cache=None):
+    E, _ = _check_ffn(x, w_gate_up, w_down, None)
+    plan = routing.route_plan(expert_idx, E, pad_multiple)
+    xq, xs = routing.gather_to_mxfp8_dim0(x, plan, scaling_mode)
+    wq, ws = _weight_dim0(w_gate_up, scaling_mode, weight_cache)
+    h = ops.grouped_mm(xq, wq, plan.offs, xs, ws, out_dtype=torch.bfloat16)
+    aq, as_ = ops.swiglu_quant(h, scaling_mode)
+    dq, ds = _weight_dim0(w_down, scaling_mode, weight_cache)
+    y = ops.grouped_mm(aq, dq, plan.offs, as_, ds, out_dtype=torch.bfloat16)
+    return routing.combine(y, plan, scores)
+
+
 def moe_routed_ffn(x: torch.Tensor, expert_idx: torch.Tensor, scores: torch.Tensor | None,
                    w_gate_up: torch.Tensor, w_down: torch.Tensor, pad_multiple: int = 32,
                    scaling_mode: str = "rceil", weight_cache=None) -> torch.Tensor:
@@ -272,6 +285,12 @@ def moe_routed_ffn(x: torch.Tensor, expert_idx: torch.Tensor, scores: torch.Tens
     sum_k scores[t, k] * expert_output (scores [T, topk] or None for a plain
     sum).  x: bf16 [T, H]; w_gate_up [E, 2F, H]; w_down [E, H, F].  Each
     expert's rows are padded to pad_multiple (the reference's dispatcher uses
-    32, port_mxfp8.py:214).  Differentiable in x, scores and both weights."""
+    32, port_mxfp8.py:214).  Differentiable in x, scores and both weights;
+    without autograd (no_grad, or nothing requiring grad) only the row-wise
+    casts are made and nothing is kept for backward."""
+    if not torch.is_grad_enabled() or not any(
+            t is not None and t.requires_grad for t in (x, scores, w_gate_up, w_down)):
+        return _routed_forward_only(x, expert_idx, scores, w_gate_up, w_down, pad_multiple,
+                                    scaling_mode, weight_cache)
     return MXFP8RoutedExpertFFN.apply(x, expert_idx, scores, w_gate_up, w_down, pad_multiple,
                                       scaling_mode, weight_cache)

@@ -28,8 +28,8 @@ from . import _lib
 from .ops import (_FP8, _block_major_buffer, _mode, _need_gpu, _stream_ptr,
                   padded_token_capacity)
 
-__all__ = ["RoutePlan", "route_plan", "gather_rows", "gather_to_mxfp8_dual", "combine",
-           "combine_score_grad"]
+__all__ = ["RoutePlan", "route_plan", "gather_rows", "gather_to_mxfp8_dual",
+           "gather_to_mxfp8_dim0", "combine", "combine_score_grad"]
 
 
 class RoutePlan(NamedTuple):
@@ -148,6 +148,28 @@ def gather_to_mxfp8_dual(x: torch.Tensor, plan: RoutePlan, scaling_mode="rceil",
         "gather_quant_dual",
     )
     return q, sbuf[:, :M].t(), qt, stbuf[:, :C].t(), ends_pad
+
+
+def gather_to_mxfp8_dim0(x: torch.Tensor, plan: RoutePlan, scaling_mode="rceil"):
+    """The row-wise MXFP8 cast of the routed rows (gather_rows(x, plan)), read
+    straight from token order: the expert input of a forward-only pass.
+    Returns (q [plan.rows, H], s) like to_mxfp8_dim0(gather_rows(x, plan))."""
+    _need_gpu(x, "x")
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] % 32 != 0:
+        raise TypeError("x must be a 2-D bfloat16 tensor [tokens, H] with H % 32 == 0")
+    x2 = _rows_ok(x)
+    M, C = plan.rows, x.shape[1]
+    q = torch.empty((M, C), dtype=_FP8, device=x.device)
+    sbuf = _block_major_buffer(M, C // 32, x.device)
+    lib = _lib.load()
+    _lib.check(
+        lib.mxgg_gather_quant_dim0(
+            x2.data_ptr(), x2.shape[0], C, x2.stride(0), plan.src.data_ptr(), plan.topk, M,
+            q.data_ptr(), C, sbuf.data_ptr(), sbuf.stride(0), _lib.SCALES_BLOCK_MAJOR,
+            _mode(scaling_mode), _stream_ptr(x)),
+        "gather_quant_dim0",
+    )
+    return q, sbuf[:, :M].t()
 
 
 def combine(y: torch.Tensor, plan: RoutePlan, scores: torch.Tensor | None = None):

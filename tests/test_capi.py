@@ -358,6 +358,37 @@ def test_gather_quant_dual_rejects(lib, kw, status):
     assert _gather_dual(lib, **kw) == status
 
 
+def _gather_dim0(lib, **kw):
+    a = dict(x=FAKE, T=32, cols=64, ldx=64, src=FAKE, K=2, rows=64, q=FAKE, ldq=64, s=FAKE,
+             lds=64, layout=BM, mode=0)
+    a.update(kw)
+    return lib.mxgg_gather_quant_dim0(a["x"], a["T"], a["cols"], a["ldx"], a["src"], a["K"],
+                                      a["rows"], a["q"], a["ldq"], a["s"], a["lds"], a["layout"],
+                                      a["mode"], None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(K=0), _lib.ERR_SHAPE),
+    (dict(T=-1), _lib.ERR_SHAPE),
+    (dict(cols=48), _lib.ERR_SHAPE),
+    (dict(lds=63), _lib.ERR_SHAPE),                    # block-major: lds >= rows
+    (dict(ldx=32), _lib.ERR_SHAPE),
+    (dict(src=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(x=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(mode=9), _lib.ERR_INVALID_ARGUMENT),
+    (dict(layout=7), _lib.ERR_INVALID_ARGUMENT),
+    (dict(x=FAKE + 4), _lib.ERR_ALIGNMENT),
+    (dict(q=FAKE + 8), _lib.ERR_ALIGNMENT),
+])
+def test_gather_quant_dim0_rejects(lib, kw, status):
+    assert _gather_dim0(lib, **kw) == status
+
+
+def test_gather_quant_dim0_empty_is_noop(lib):
+    assert _gather_dim0(lib, rows=0) == _lib.OK
+    assert _gather_dim0(lib, cols=0) == _lib.OK
+
+
 def _combine(lib, **kw):
     a = dict(y=FAKE, rows=64, cols=64, ldy=64, perm=FAKE, scores=None, T=16, K=2, out=FAKE, ldo=64)
     a.update(kw)

@@ -103,6 +103,31 @@ def test_gather_to_mxfp8_dual_equals_cast_of_gathered_rows(gpu, mode_name, mode,
     assert np.array_equal(u8(qt), rqt) and np.array_equal(u8(st), rst)
 
 
+@pytest.mark.parametrize("mode_name,mode", [("rceil", O.RCEIL), ("floor", O.FLOOR)])
+@pytest.mark.parametrize("T,K,E,H,pad", [(700, 4, 6, 128, 32), (1, 1, 1, 32, 1),
+                                         (333, 10, 40, 7168, 32), (0, 2, 3, 64, 32)])
+def test_gather_to_mxfp8_dim0_matches_oracle(gpu, mode_name, mode, T, K, E, H, pad):
+    # every routed row (padding rows included) is the row-wise cast of the
+    # oracle's gathered row, and equals the cast of the bf16 gathered copy
+    idx = _idx(gpu, T, K, E, 14, drop=True)
+    g = torch.Generator(device=gpu).manual_seed(15)
+    x = (torch.randn(T, H, generator=g, device=gpu) *
+         torch.exp2(torch.randint(-30, 30, (T, 1), generator=g, device=gpu).float())
+         ).to(torch.bfloat16)
+    if T > 9:
+        x[9, 5] = float("nan")
+        x[2, H - 1] = float("-inf")
+    plan = mxfp8gg.route_plan(idx, E, pad)
+    q, s = mxfp8gg.gather_to_mxfp8_dim0(x, plan, mode_name)
+    assert q.shape == (plan.rows, H) and s.shape == (plan.rows, H // 32)
+    xr = O.gather_rows(bits(x), plan.src.cpu().numpy(), K, None)
+    rq, rs = O.quant_dim0(xr, mode)
+    assert np.array_equal(u8(q), rq) and np.array_equal(u8(s), rs)
+    q2, s2 = mxfp8gg.to_mxfp8_dim0(mxfp8gg.gather_rows(x, plan), mode_name)
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8))
+    assert torch.equal(s.contiguous(), s2.contiguous())
+
+
 @pytest.mark.parametrize("scaled", [False, True])
 @pytest.mark.parametrize("T,K,E,H", [(257, 8, 32, 64), (40, 1, 3, 24), (1, 2, 2, 8),
                                      (50, 10, 16, 40)])   # top-10: the general slot loop
@@ -159,6 +184,24 @@ def test_routed_ffn_forward_is_gather_ffn_combine(gpu):
     plan = mxfp8gg.route_plan(idx, E, 32)
     y = mxfp8gg.moe_ffn(mxfp8gg.gather_rows(x, plan), wgu, wd, plan.offs)
     assert torch.equal(out, mxfp8gg.combine(y, plan, sc))
+
+
+@pytest.mark.parametrize("scored", [True, False])
+def test_routed_ffn_forward_only_equals_training_forward(gpu, scored):
+    # the no-grad path (row-wise casts only) and the autograd path (dual casts,
+    # saved state) give the same bits
+    x, idx, sc, wgu, wd = _routed_layer(gpu, T=300, K=6, E=12, seed=16)
+    sc = sc if scored else None
+    with torch.no_grad():
+        a = mxfp8gg.moe_routed_ffn(x, idx, sc, wgu, wd)
+    b = mxfp8gg.moe_routed_ffn(x.clone().requires_grad_(True), idx, sc, wgu, wd)
+    assert b.requires_grad
+    assert torch.equal(a, b.detach())
+    cache = mxfp8gg.WeightCastCache()
+    with torch.no_grad():
+        c = mxfp8gg.moe_routed_ffn(x, idx, sc, wgu, wd, weight_cache=cache)
+        d = mxfp8gg.moe_routed_ffn(x, idx, sc, wgu, wd, weight_cache=cache)
+    assert torch.equal(a, c) and torch.equal(a, d)
 
 
 def test_routed_ffn_gradients(gpu):
