@@ -99,6 +99,8 @@ static int check_dim0(const char* what, const void* x, int64_t rows, int64_t col
   if (cols % 32 != 0)
     return set_error(MXGG_ERR_SHAPE, "%s: cols=%lld is not a multiple of 32", what,
                      (long long)cols);
+  if (cols > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "%s: cols above 2^31", what);
   if (rows == 0 || cols == 0) return MXGG_OK;
   if (!x || !q || !scales) return set_error(MXGG_ERR_INVALID_ARGUMENT, "%s: null pointer", what);
   if (ldx < cols || ldq < cols ||
@@ -163,8 +165,8 @@ int mxgg_quant_dim1(const void* x, int64_t rows, int64_t cols, int64_t ldx,
   if ((x && !aligned16(x)) || !aligned16(qt) || ldx % 8 != 0 || ldqt % 16 != 0)
     return set_error(MXGG_ERR_ALIGNMENT,
                      "quant_dim1: x and qt must be 16-byte aligned, ldx % 8 == 0, ldqt % 16 == 0");
-  if (rows > INT32_MAX || rows_pad_cap > INT32_MAX)
-    return set_error(MXGG_ERR_UNSUPPORTED, "quant_dim1: more than 2^31 rows");
+  if (rows > INT32_MAX || rows_pad_cap > INT32_MAX || cols > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "quant_dim1: more than 2^31 rows or columns");
   return check_launch(
       launch_quant_dim1(static_cast<const uint16_t*>(x), rows, cols, ldx, group_ends, groups,
                         rows_pad_cap, static_cast<uint8_t*>(qt), ldqt,
@@ -220,8 +222,8 @@ static int check_dual(const char* what, bool have_x, int64_t rows, int64_t cols,
                      "%s: x 16-byte aligned with ldx %% 8 == 0, q 8-byte aligned with ldq "
                      "%% 8 == 0, qt 16-byte aligned with ldqt %% 16 == 0",
                      what);
-  if (rows > INT32_MAX || rows_pad_cap > INT32_MAX)
-    return set_error(MXGG_ERR_UNSUPPORTED, "%s: more than 2^31 rows", what);
+  if (rows > INT32_MAX || rows_pad_cap > INT32_MAX || cols > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "%s: more than 2^31 rows or columns", what);
   return MXGG_OK;
 }
 
@@ -259,6 +261,8 @@ int mxgg_swiglu_quant_dim0(const void* gate, const void* up, int64_t ldh, int64_
   if (cols % 32 != 0)
     return set_error(MXGG_ERR_SHAPE, "swiglu_quant_dim0: cols=%lld is not a multiple of 32",
                      (long long)cols);
+  if (cols > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "swiglu_quant_dim0: cols above 2^31");
   if (rows == 0 || cols == 0) return MXGG_OK;
   if (!gate || !up || !q || !scales)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "swiglu_quant_dim0: null pointer");
@@ -585,6 +589,7 @@ static int check_rows(const char* what, const void* a, int64_t lda, const void* 
   if (cols < 0 || cols % 8 != 0)
     return set_error(MXGG_ERR_SHAPE, "%s: cols=%lld is not a non-negative multiple of 8", what,
                      (long long)cols);
+  if (cols > INT32_MAX) return set_error(MXGG_ERR_UNSUPPORTED, "%s: cols above 2^31", what);
   if (lda < cols || ldb < cols)
     return set_error(MXGG_ERR_SHAPE, "%s: leading dimension smaller than the row", what);
   if ((a && !aligned16(a)) || (b && !aligned16(b)) || lda % 8 != 0 || ldb % 8 != 0)

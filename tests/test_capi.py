@@ -384,6 +384,14 @@ def test_gather_quant_dim0_rejects(lib, kw, status):
     assert _gather_dim0(lib, **kw) == status
 
 
+def test_column_counts_above_int32_are_rejected(lib):
+    big = 1 << 31   # a multiple of 32; the kernels index columns with 32-bit ints
+    assert _gather_dim0(lib, cols=big, ldx=big, ldq=big) == _lib.ERR_UNSUPPORTED
+    assert lib.mxgg_quant_dim0(FAKE, 4, big, big, FAKE, big, FAKE, 4, BM, 0, None) == \
+        _lib.ERR_UNSUPPORTED
+    assert _combine(lib, cols=big, ldy=big, ldo=big) == _lib.ERR_UNSUPPORTED
+
+
 def test_gather_quant_dim0_empty_is_noop(lib):
     assert _gather_dim0(lib, rows=0) == _lib.OK
     assert _gather_dim0(lib, cols=0) == _lib.OK
