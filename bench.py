@@ -87,6 +87,46 @@ def ref_equal_shapes(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
             "vs_reference_unscaled": round(gu / REF_GEOMEAN_UNSCALED, 3)}
 
 
+def dense_c2_shape(torch, mxfp8gg, dev, steps=10, warmup=3):
+    """C2's GEMM as one dense group (M=65536, N=4096, K=7168): this library's
+    kernel with and without E8M0 scales, and the vendor library through
+    torch._scaled_mm (hipBLASLt) at the same shape, tensorwise fp8 and MX
+    block-scaled, for reference.  Separates the kernel's own ceiling from what
+    C2's ragged groups cost (partial m-tiles, a last round of tiles)."""
+    M, N, K = 65536, 4096, 7168
+    gen = torch.Generator(device=dev).manual_seed(0)
+    xq, xs = mxfp8gg.to_mxfp8_dim0(torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16))
+    wq, ws = mxfp8gg.to_mxfp8_dim0(
+        (torch.randn((1, N, K), generator=gen, device=dev) * 0.006).to(torch.bfloat16))
+    ends = torch.tensor([M], dtype=torch.int32, device=dev)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    fl = 2 * M * N * K
+
+    one = torch.ones((), device=dev)
+    e8 = torch.float8_e8m0fnu
+    sa, sb = xs.contiguous().view(e8), ws[0].contiguous().view(e8)
+    cases = {
+        "mxgg_scaled_tflops": lambda: mxfp8gg.grouped_mm(xq, wq, ends, xs, ws, out=out),
+        "mxgg_unscaled_tflops": lambda: mxfp8gg.grouped_mm(xq, wq, ends, out=out),
+        "hipblaslt_fp8_tensorwise_tflops":
+            lambda: torch._scaled_mm(xq, wq[0].t(), one, one, out_dtype=torch.bfloat16),
+        "hipblaslt_mxfp8_tflops":
+            lambda: torch._scaled_mm(xq, wq[0].t(), sa, sb, out_dtype=torch.bfloat16)}
+    res = {"M": M, "N": N, "K": K, "note": "best of 3 interleaved rounds"}
+    best = {}
+    for _ in range(3):   # interleaved, so clock and thermal drift hit every case alike
+        for name, fn in cases.items():
+            if isinstance(best.get(name), str):
+                continue
+            try:
+                t = round(fl / time_launches(fn, steps, warmup, torch) / 1e9, 1)
+                best[name] = max(best.get(name, 0.0), t)
+            except Exception as ex:  # the vendor paths are a comparison only
+                best[name] = "unavailable: " + str(ex)[:120]
+    res.update(best)
+    return res
+
+
 def layer_step_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     """one DSv3 expert-FFN layer step on one GPU --
     131072 routed tokens, Zipf(1.0) over 32 experts, hidden 7168, intermediate
@@ -259,12 +299,14 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "c5", "routing"],
+    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "c5", "routing",
+                                       "dense"],
                     default="all",
                     help="fwd / wgrad: time only that GEMM (for profiler runs); copy: a plain "
                          "1 GiB device-to-device copy, the reference for HBM byte counters; "
                          "ref8: the reference's 8 equal-group shapes only; c5: the full "
-                         "expert-FFN layer step only; routing: C5 as a routed top-8 layer")
+                         "expert-FFN layer step only; routing: C5 as a routed top-8 layer; "
+                         "dense: C2's shape as one dense GEMM, with hipBLASLt beside it")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the MXFP8 grouped GEMM shards by expert and "
@@ -285,6 +327,9 @@ def main():
         return
     if args.only == "routing":
         print(json.dumps(routing_c5(torch, mxfp8gg, workloads, dev)), flush=True)
+        return
+    if args.only == "dense":
+        print(json.dumps(dense_c2_shape(torch, mxfp8gg, dev)), flush=True)
         return
     if args.only == "ref8":
         print(json.dumps(ref_equal_shapes(torch, mxfp8gg, workloads, dev)), flush=True)
@@ -383,6 +428,8 @@ def main():
         del go, gos, ia, ias, dw
         log("reference's 8 equal-group shapes")
         components["ref_equal_shapes"] = ref_equal_shapes(torch, mxfp8gg, workloads, dev)
+        log("C2's shape as one dense GEMM (kernel ceiling, vendor library beside it)")
+        components["dense_c2_shape"] = dense_c2_shape(torch, mxfp8gg, dev)
         log("C5: expert-FFN layer step (forward + backward)")
         components["layer_step_c5"] = layer_step_c5(torch, mxfp8gg, workloads, dev)
         log("C5 as a routed top-8 layer (dispatch, combine)")
