@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 7
+#define MXGG_ABI_VERSION 8
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -219,6 +219,29 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
                      const int32_t* group_ends, int64_t num_groups,
                      int64_t M, int64_t N, int64_t K,
                      void* out, int64_t ldo, int out_dtype, void* stream);
+
+/*
+ * mxgg_grouped_fwd with a caller-owned workspace of at least
+ * mxgg_grouped_fwd_workspace_bytes() bytes (16-byte aligned; contents need no
+ * initialisation and are scratch after the call).  When the tiles of the
+ * last round would leave at least half of the compute units idle (and for
+ * launches with fewer tiles than compute units), those tiles are cut along K
+ * into up to 16 ranges over the idle units; their fp32 partial tiles go to the
+ * workspace and a second kernel on the same stream adds them in a fixed order
+ * and writes the output.  Deterministic; results can differ from
+ * mxgg_grouped_fwd in the last bit of those tiles (fp32 summation order).
+ * Replaces the same reference interface as mxgg_grouped_fwd
+ * (fused_fwd.py:172-229); the reference has no counterpart of the workspace.
+ * Calls that share a workspace must be ordered on one stream.
+ */
+int64_t mxgg_grouped_fwd_workspace_bytes(void);
+int mxgg_grouped_fwd_split(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                           const void* w, int64_t w_group_stride, int64_t ldw,
+                           const void* w_scales, int64_t ws_group_stride, int64_t ldws,
+                           const int32_t* group_ends, int64_t num_groups,
+                           int64_t M, int64_t N, int64_t K,
+                           void* out, int64_t ldo, int out_dtype,
+                           void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Weight-gradient grouped GEMM, contracting over the ragged token dimension:

@@ -398,11 +398,11 @@ int mxgg_scales_to_block_major(const void* src, int64_t batch, int64_t rows, int
       "scales_to_block_major");
 }
 
-int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
-                     const void* w, int64_t w_group_stride, int64_t ldw, const void* w_scales,
-                     int64_t ws_group_stride, int64_t ldws, const int32_t* group_ends,
-                     int64_t num_groups, int64_t M, int64_t N, int64_t K, void* out, int64_t ldo,
-                     int out_dtype, void* stream) {
+static int grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                       const void* w, int64_t w_group_stride, int64_t ldw, const void* w_scales,
+                       int64_t ws_group_stride, int64_t ldws, const int32_t* group_ends,
+                       int64_t num_groups, int64_t M, int64_t N, int64_t K, void* out,
+                       int64_t ldo, int out_dtype, void* workspace, void* stream) {
   if (out_dtype != MXGG_OUT_BF16 && out_dtype != MXGG_OUT_F32)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd: unknown out_dtype %d", out_dtype);
   if (M < 0 || N < 0 || K < 0)
@@ -471,7 +471,37 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
   args.E = (int32_t)E;
   args.out_f32 = out_dtype == MXGG_OUT_F32;
   args.scaled = scaled;
+  args.split_ws = static_cast<float*>(workspace);
   return check_launch(launch_grouped_fwd(args, static_cast<hipStream_t>(stream)), "grouped_fwd");
+}
+
+int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                     const void* w, int64_t w_group_stride, int64_t ldw, const void* w_scales,
+                     int64_t ws_group_stride, int64_t ldws, const int32_t* group_ends,
+                     int64_t num_groups, int64_t M, int64_t N, int64_t K, void* out, int64_t ldo,
+                     int out_dtype, void* stream) {
+  return grouped_fwd(a, lda, a_scales, ldas, w, w_group_stride, ldw, w_scales, ws_group_stride,
+                     ldws, group_ends, num_groups, M, N, K, out, ldo, out_dtype, nullptr, stream);
+}
+
+int64_t mxgg_grouped_fwd_workspace_bytes(void) { return fwd_split_workspace_bytes(); }
+
+int mxgg_grouped_fwd_split(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                           const void* w, int64_t w_group_stride, int64_t ldw,
+                           const void* w_scales, int64_t ws_group_stride, int64_t ldws,
+                           const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t N,
+                           int64_t K, void* out, int64_t ldo, int out_dtype, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+  if (!workspace)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd_split: null workspace");
+  if (workspace_bytes < fwd_split_workspace_bytes())
+    return set_error(MXGG_ERR_SHAPE, "grouped_fwd_split: workspace_bytes=%lld < %lld",
+                     (long long)workspace_bytes, (long long)fwd_split_workspace_bytes());
+  if (!aligned16(workspace))
+    return set_error(MXGG_ERR_ALIGNMENT, "grouped_fwd_split: workspace must be 16-byte aligned");
+  return grouped_fwd(a, lda, a_scales, ldas, w, w_group_stride, ldw, w_scales, ws_group_stride,
+                     ldws, group_ends, num_groups, M, N, K, out, ldo, out_dtype, workspace,
+                     stream);
 }
 
 int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, int64_t ldgos,

@@ -46,6 +46,12 @@ constexpr uint32_t kOpBytes = 256u * kStageK;          // one operand of one sta
 constexpr uint32_t kScaleOff = 2u * kOpBytes;          // scale rows after P and Q data
 constexpr uint32_t kStageBytes = kScaleOff + 4u * 512u;  // + [4 blocks][P, Q][256]
 constexpr uint32_t kOobOffset = 0x80000000u;           // beyond every num_records we create
+// Split-K of the forward's last round: at most this many K-ranges per tile;
+// workspace = a header (tail tile count, split count, then q0, p0, group
+// begin and end of every split tile) and one fp32 256x256 partial per split.
+constexpr uint32_t kMaxSplit = 16;
+constexpr int64_t kSplitHdrBytes = 16384;
+constexpr int64_t kPartialBytes = 256 * 256 * 4;
 
 struct __align__(16) Smem {
   uint8_t ring[2][kStageBytes];
@@ -643,12 +649,37 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
   const uint32_t n_tiles = ((uint32_t)args.N + kTileP - 1) / kTileP;
   const uint32_t total = m_tiles * n_tiles;
   const uint32_t K = (uint32_t)args.K;
+  // With a workspace, a last round of tiles that would leave at least half of
+  // the workgroups idle is cut along K into S ranges (whole stages), one work
+  // item each; k_fwd_split_reduce adds the S partials in a fixed order.
+  const uint32_t G = gridDim.x;
+  const uint32_t full = total / G * G;
+  const uint32_t rem = total - full;
+  const uint32_t nst = (K + kStageK - 1) / kStageK;
+  uint32_t S = 1, chunk = nst;
+  if (args.split_ws != nullptr && rem > 0 && rem <= G / 2 && nst > 1) {
+    S = min(min(G / rem, nst), kMaxSplit);
+    chunk = (nst + S - 1) / S;
+    S = (nst + chunk - 1) / chunk;
+  }
+  int32_t* hdr = reinterpret_cast<int32_t*>(args.split_ws);
+  if (hdr != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    hdr[0] = S > 1 ? (int32_t)rem : 0;
+    hdr[1] = (int32_t)S;
+  }
+  const uint32_t items = S > 1 ? full + rem * S : total;
 
-  for (uint32_t base = 0;; base += gridDim.x) {
+  for (uint32_t base = 0;; base += G) {
     const uint32_t lid = xcd_slice(base);
-    if (lid >= total) break;
+    if (lid >= items) break;
+    uint32_t tile = lid, split = 0;
+    const bool part = S > 1 && lid >= full;
+    if (part) {
+      tile = full + (lid - full) / S;
+      split = (lid - full) % S;
+    }
     uint32_t mt, nt;
-    band_decode(lid, m_tiles, n_tiles, gm, mt, nt);
+    band_decode(tile, m_tiles, n_tiles, gm, mt, nt);
     // group of m-tile mt: last g with sched[g] <= mt
     int lo = 0, hi = E - 1;
     while (lo < hi) {
@@ -677,10 +708,92 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
       Q.lds = (uint32_t)args.ldas;
     }
     v16f acc[4][4];
-    mainloop<SCALED>(sm, P, Q, 0u, K, acc);
-    const int64_t ldo_bytes = args.ldo * (F32 ? 4 : 2);
-    epilogue<F32>(sm, acc, reinterpret_cast<char*>(args.out), ldo_bytes, q0, (uint32_t)gb,
-                  (uint32_t)ge, p0, (uint32_t)args.N);
+    if (part) {
+      const uint32_t klo = split * chunk * kStageK;
+      mainloop<SCALED>(sm, P, Q, klo, min(K, klo + chunk * kStageK), acc);
+      const uint32_t t = tile - full;
+      if (split == 0 && threadIdx.x == 0) {
+        hdr[4 + 4 * t] = (int32_t)q0;
+        hdr[5 + 4 * t] = (int32_t)p0;
+        hdr[6 + 4 * t] = gb;
+        hdr[7 + 4 * t] = ge;
+      }
+      // the whole 256x256 fp32 partial, rows and columns unmasked
+      char* slot = reinterpret_cast<char*>(args.split_ws) + kSplitHdrBytes +
+                   (int64_t)(t * S + split) * kPartialBytes;
+      epilogue<true>(sm, acc, slot, 1024, 0u, 0u, 256u, 0u, 256u);
+    } else {
+      mainloop<SCALED>(sm, P, Q, 0u, K, acc);
+      const int64_t ldo_bytes = args.ldo * (F32 ? 4 : 2);
+      epilogue<F32>(sm, acc, reinterpret_cast<char*>(args.out), ldo_bytes, q0, (uint32_t)gb,
+                    (uint32_t)ge, p0, (uint32_t)args.N);
+    }
+  }
+}
+
+// Sum of the split partials of the forward's last round, in split order (the
+// first partial is the starting value), stored inside the tile's group and
+// columns.  Each thread takes 4 (tile, row, 4-column) items a grid-stride
+// apart and issues all their loads before adding, so the sums are bound by
+// bandwidth, not by one load latency per partial.  Exits at once when the
+// forward did not split (header count 0).
+constexpr int kReduceItems = 4;
+
+__global__ __launch_bounds__(256) void k_fwd_split_reduce(const float* __restrict__ ws,
+                                                          void* __restrict__ out, int64_t ldo,
+                                                          int32_t N, int32_t out_f32) {
+  const int32_t* hdr = reinterpret_cast<const int32_t*>(ws);
+  const int32_t n = hdr[0], S = hdr[1];
+  const float* part = ws + kSplitHdrBytes / 4;
+  const int64_t work = (int64_t)n * 256 * 64;  // (tile, row, group of 4 columns)
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x; i0 < work;
+       i0 += kReduceItems * stride) {
+    v4f acc[kReduceItems];
+    int64_t dsto[kReduceItems];
+    int32_t pcol[kReduceItems];
+#pragma unroll
+    for (int u = 0; u < kReduceItems; ++u) {
+      const int64_t i = i0 + u * stride;
+      dsto[u] = -1;
+      pcol[u] = 0;
+      acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
+      if (i >= work) continue;
+      const int32_t t = (int32_t)(i >> 14), r = (int32_t)((i >> 6) & 255),
+                    c = (int32_t)(i & 63) * 4;
+      const int32_t* th = hdr + 4 + 4 * t;
+      const int32_t q = th[0] + r, p = th[1] + c;
+      if (q < th[2] || q >= th[3] || p >= N) continue;
+      dsto[u] = (int64_t)q * ldo + p;
+      pcol[u] = p;
+      const float* src = part + (int64_t)t * S * 65536 + r * 256 + c;
+      acc[u] = *reinterpret_cast<const v4f*>(src);
+      for (int32_t sp = 1; sp < S; ++sp)
+        acc[u] += *reinterpret_cast<const v4f*>(src + (int64_t)sp * 65536);
+    }
+#pragma unroll
+    for (int u = 0; u < kReduceItems; ++u) {
+      if (dsto[u] < 0) continue;
+      const int32_t p = pcol[u];
+      if (out_f32) {
+        float* dst = reinterpret_cast<float*>(out) + dsto[u];
+        if (p + 4 <= N)
+          *reinterpret_cast<v4f*>(dst) = acc[u];
+        else
+          for (int32_t k = 0; p + k < N; ++k) dst[k] = acc[u][k];
+      } else {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(out) + dsto[u];
+        if (p + 4 <= N) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(acc[u][0], acc[u][1]),
+                                                      pack_bf16x2(acc[u][2], acc[u][3]));
+        } else {
+          for (int32_t k = 0; p + k < N; ++k) {
+            const __bf16 h = (__bf16)acc[u][k];
+            dst[k] = *reinterpret_cast<const uint16_t*>(&h);
+          }
+        }
+      }
+    }
   }
 }
 
@@ -793,6 +906,10 @@ int persistent_grid() {
 
 }  // namespace
 
+int64_t fwd_split_workspace_bytes() {
+  return kSplitHdrBytes + (int64_t)persistent_grid() * kPartialBytes;
+}
+
 hipError_t launch_grouped_fwd(const FwdArgs& a, hipStream_t stream) {
   if (a.M == 0 || a.N == 0) return hipSuccess;
   const dim3 grid(persistent_grid()), block(kThreads);
@@ -804,6 +921,11 @@ hipError_t launch_grouped_fwd(const FwdArgs& a, hipStream_t stream) {
     if (a.out_f32) MXGG_FWD(false, true); else MXGG_FWD(false, false);
   }
 #undef MXGG_FWD
+  if (a.split_ws == nullptr) return hipGetLastError();
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(k_fwd_split_reduce, dim3(4 * grid.x), dim3(256), 0, stream, a.split_ws,
+                     a.out, a.ldo, a.N, a.out_f32);
   return hipGetLastError();
 }
 

@@ -125,8 +125,12 @@ struct FwdArgs {
   int32_t M, N, K, E;
   int32_t out_f32;
   int32_t scaled;
+  // Optional workspace of fwd_split_workspace_bytes(): the tiles of a last,
+  // sparse round of tiles are then split along K over the idle CUs.
+  float* split_ws;
 };
 hipError_t launch_grouped_fwd(const FwdArgs& args, hipStream_t stream);
+int64_t fwd_split_workspace_bytes();
 
 struct WgradArgs {
   const uint8_t* go;   // [N, M] token-contiguous

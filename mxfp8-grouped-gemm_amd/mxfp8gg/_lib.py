@@ -31,7 +31,7 @@ OUT_F32 = 1
 SCALES_ROW_MAJOR = 0
 SCALES_BLOCK_MAJOR = 1
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -67,6 +67,12 @@ SIGNATURES = {
         _I,
         [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
          _P, _I64, _I, _P],
+    ),
+    "mxgg_grouped_fwd_workspace_bytes": (_I64, []),
+    "mxgg_grouped_fwd_split": (
+        _I,
+        [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
+         _P, _I64, _I, _P, _I64, _P],
     ),
     "mxgg_grouped_wgrad": (
         _I,

@@ -414,15 +414,51 @@ def swiglu_backward_quant(h: torch.Tensor, grad_a: torch.Tensor, offs: torch.Ten
 # ---------------------------------------------------------------------------
 # forward grouped GEMM
 # ---------------------------------------------------------------------------
+_SPLIT_WS_BYTES: dict = {}
+
+
+def _split_workspace_bytes(device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _SPLIT_WS_BYTES.get(idx)
+    if n is None:
+        with torch.cuda.device(idx):
+            n = int(_lib.load().mxgg_grouped_fwd_workspace_bytes())
+        _SPLIT_WS_BYTES[idx] = n
+    return n
+
+
+def _split_workspace(device) -> torch.Tensor:
+    """Scratch for mxgg_grouped_fwd_split, from the caching allocator (stream
+    ordered, so it can be released as soon as the launch is queued)."""
+    return torch.empty(_split_workspace_bytes(device), dtype=torch.uint8, device=device)
+
+
+def _small_launch(M: int, N: int, E: int, device) -> bool:
+    """True when the forward has at most half a round of 256x256 tiles for any
+    group sizes: expert g needs ceil((m_g + 3) / 256) m-tiles at most (its
+    tiles start up to 3 rows early; the first expert's start at row 0), and
+    the sum of those ceilings is at most floor((M + 3(E-1) + 255 E) / 256)."""
+    units = (_split_workspace_bytes(device) - 16384) // (256 * 256 * 4)
+    m_tiles = (M + 3 * (E - 1) + 255 * E) // 256
+    return m_tiles * ((N + 255) // 256) <= units // 2
+
+
 def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
                a_scales: torch.Tensor | None = None, w_scales: torch.Tensor | None = None,
-               out_dtype: torch.dtype = torch.bfloat16, out: torch.Tensor | None = None):
+               out_dtype: torch.dtype = torch.bfloat16, out: torch.Tensor | None = None,
+               split_tail: bool | None = None):
     """out[rows of g] = dequant(a[rows of g]) @ dequant(w[g])^T, fp32 accumulate.
 
     a: e4m3 [M, K]; w: e4m3 [E, N, K]; offs: int32 group ends ([E] or [E+1]
     with leading 0) or None for a single group; scales: E8M0 bytes
     [M, K/32] and [E, N, K/32], both or neither (neither = scale 1.0).
-    Rows after the last group end are left untouched.
+    Rows after the last group end are left untouched.  split_tail: run a
+    launch whose tiles fill at most half of the compute units split along K
+    over the idle units (mxgg_grouped_fwd_split; deterministic, equal to the
+    unsplit result up to fp32 summation order).  None (default): only when
+    the launch is that small whatever the group sizes are; True: always take
+    the split entry point (it splits a sparse last round of any launch);
+    False: never.
     """
     _need_gpu(a, "a")
     _need_gpu(w, "w")
@@ -450,17 +486,20 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
     elif out.shape != (M, N) or out.dtype != out_dtype or out.stride(-1) != 1:
         raise ValueError("out must be a row-major [M, N] tensor of out_dtype")
     lib = _lib.load()
-    _lib.check(
-        lib.mxgg_grouped_fwd(
-            a8.data_ptr(), a8.stride(0),
+    args = (a8.data_ptr(), a8.stride(0),
             sa.data_ptr() if sa is not None else None, ldas,
             w8.data_ptr(), w8.stride(0), w8.stride(1),
             sw.data_ptr() if sw is not None else None, wsg, ldws,
             ends.data_ptr() if ends is not None else None, E,
-            M, N, K, out.data_ptr(), out.stride(0), _out_code(out_dtype), _stream_ptr(a),
-        ),
-        "grouped_fwd",
-    )
+            M, N, K, out.data_ptr(), out.stride(0), _out_code(out_dtype))
+    if split_tail is None:
+        split_tail = _small_launch(M, N, E, a.device)
+    if split_tail and M > 0 and N > 0:
+        ws = _split_workspace(a.device)
+        _lib.check(lib.mxgg_grouped_fwd_split(*args, ws.data_ptr(), ws.numel(), _stream_ptr(a)),
+                   "grouped_fwd_split")
+    else:
+        _lib.check(lib.mxgg_grouped_fwd(*args, _stream_ptr(a)), "grouped_fwd")
     return out
 
 

@@ -57,6 +57,37 @@ def _fwd(lib, **kw):
                                 args["out"], args["ldo"], args["dt"], None)
 
 
+def _fwd_split(lib, ws=FAKE, nbytes=None, **kw):
+    args = dict(a=FAKE, lda=256, a_s=None, ldas=0, w=FAKE, wg=512 * 256, ldw=256, w_s=None,
+                wsg=0, ldws=0, ends=None, E=1, M=64, N=512, K=256, out=FAKE, ldo=512,
+                dt=_lib.OUT_BF16)
+    args.update(kw)
+    if nbytes is None:
+        nbytes = lib.mxgg_grouped_fwd_workspace_bytes()
+    return lib.mxgg_grouped_fwd_split(args["a"], args["lda"], args["a_s"], args["ldas"],
+                                      args["w"], args["wg"], args["ldw"], args["w_s"],
+                                      args["wsg"], args["ldws"], args["ends"], args["E"],
+                                      args["M"], args["N"], args["K"], args["out"], args["ldo"],
+                                      args["dt"], ws, nbytes, None)
+
+
+def test_split_workspace_size_covers_one_partial_per_unit(lib):
+    # header + one 256x256 fp32 partial per workgroup of the persistent grid
+    n = lib.mxgg_grouped_fwd_workspace_bytes()
+    assert n >= 16384 + 8 * 256 * 256 * 4 and (n - 16384) % (256 * 256 * 4) == 0
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(ws=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(nbytes=16384), _lib.ERR_SHAPE),
+    (dict(ws=FAKE + 8), _lib.ERR_ALIGNMENT),
+    (dict(K=100), _lib.ERR_SHAPE),                     # then the forward's own checks
+    (dict(a=None), _lib.ERR_INVALID_ARGUMENT),
+])
+def test_grouped_fwd_split_rejects(lib, kw, status):
+    assert _fwd_split(lib, **kw) == status
+
+
 @pytest.mark.parametrize("kw,status", [
     (dict(K=100), _lib.ERR_SHAPE),                     # K % 32
     (dict(K=0), _lib.ERR_SHAPE),
