@@ -5,7 +5,9 @@ bars as the fixed-case tests:
 
   * casts, routing plans, gathers and combines: bit for bit;
   * grouped GEMMs: tests/_helpers.assert_close_to_oracle (every element within
-    2^-7 |ref| + 2^-12 max|ref| of the float64 dequantise-then-matmul value).
+    2^-7 |ref| + 2^-12 max|ref| of the float64 dequantise-then-matmul value);
+    split forwards also within 2^-14 max|y| (fp32) or 2^-7 max|y| (bf16) of
+    the unsplit entry point.
 
 Shapes stay small enough for the numpy oracle (a few seconds for the file).
 """
@@ -65,6 +67,40 @@ def test_random_grouped_fwd(gpu, sizes, N, K, scaled, f32, seed):
     ref = O.grouped_fwd(u8(a_q), u8(a_s) if scaled else None, u8(w_q),
                         u8(w_s) if scaled else None, ends)
     assert_close_to_oracle(y, ref)
+
+
+def _split_cases(n=12, seed=150):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        E = int(rng.integers(1, 9))
+        M = int(rng.integers(1, 1500))
+        out.append((_sizes(rng, E, M), 8 * int(rng.integers(1, 76)), 32 * int(rng.integers(1, 129)),
+                    bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), int(rng.integers(0, 2**31))))
+    return out
+
+
+@pytest.mark.parametrize("sizes,N,K,scaled,f32,seed", _split_cases())
+def test_random_split_forward(gpu, sizes, N, K, scaled, f32, seed):
+    # small launches split along K (mxgg_grouped_fwd_split) against the oracle
+    # and against the unsplit entry point (fp32 summation order only)
+    E, M = len(sizes), sum(sizes)
+    a_q, a_s = _rand_q((max(M, 1), K), gpu, seed)
+    w_q, w_s = _rand_q((E, N, K), gpu, seed + 1)
+    a_q, a_s = a_q[:M], a_s[:M]
+    ends = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    dt = torch.float32 if f32 else torch.bfloat16
+    args = (a_q.view(torch.float8_e4m3fn), w_q.view(torch.float8_e4m3fn), ends,
+            a_s if scaled else None, w_s if scaled else None)
+    y1 = ops.grouped_mm(*args, out_dtype=dt, split_tail=True)
+    y0 = ops.grouped_mm(*args, out_dtype=dt, split_tail=False)
+    if M == 0:
+        return
+    ref = O.grouped_fwd(u8(a_q), u8(a_s) if scaled else None, u8(w_q),
+                        u8(w_s) if scaled else None, workloads.ends_of(sizes))
+    assert_close_to_oracle(y1, ref)
+    mag = y0.float().abs().max().item()
+    assert (y1.float() - y0.float()).abs().max().item() <= (2.0 ** -14 if f32 else 2.0 ** -7) * mag
 
 
 def _wgrad_cases(n=10, seed=200):
