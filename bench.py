@@ -52,7 +52,7 @@ def time_launches(fn, steps, warmup, torch):
 
 # The reference's published forward numbers on MI355X are geometric means over
 # these 8 equal-group DeepSeek-V3 shapes (fused_fwd.py:323-333): 1501 TFLOPS
-# with E8M0 scales, 1864 without (BASELINE.md).
+# with E8M0 scales, 1864 without.
 REF_GEOMEAN_SCALED = 1501.0
 REF_GEOMEAN_UNSCALED = 1864.0
 
