@@ -443,6 +443,17 @@ def _small_launch(M: int, N: int, E: int, device) -> bool:
     return m_tiles * ((N + 255) // 256) <= units // 2
 
 
+_MAX_OPERAND_BYTES = 0x7FFFFFF0   # the C ABI's bound on (rows - 1) * ld + K
+
+
+def _rows_per_launch(lda: int, K: int, M: int) -> int:
+    """Rows of A one forward launch may take: all M when A fits the 32-bit
+    buffer range, else the largest multiple of 256 that does."""
+    if M == 0 or (M - 1) * lda + K <= _MAX_OPERAND_BYTES:
+        return max(M, 1)
+    return max(256, ((_MAX_OPERAND_BYTES - K) // lda + 1) // 256 * 256)
+
+
 def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
                a_scales: torch.Tensor | None = None, w_scales: torch.Tensor | None = None,
                out_dtype: torch.dtype = torch.bfloat16, out: torch.Tensor | None = None,
@@ -486,20 +497,33 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
     elif out.shape != (M, N) or out.dtype != out_dtype or out.stride(-1) != 1:
         raise ValueError("out must be a row-major [M, N] tensor of out_dtype")
     lib = _lib.load()
-    args = (a8.data_ptr(), a8.stride(0),
-            sa.data_ptr() if sa is not None else None, ldas,
-            w8.data_ptr(), w8.stride(0), w8.stride(1),
-            sw.data_ptr() if sw is not None else None, wsg, ldws,
-            ends.data_ptr() if ends is not None else None, E,
-            M, N, K, out.data_ptr(), out.stride(0), _out_code(out_dtype))
-    if split_tail is None:
-        split_tail = _small_launch(M, N, E, a.device)
-    if split_tail and M > 0 and N > 0:
-        ws = _split_workspace(a.device)
-        _lib.check(lib.mxgg_grouped_fwd_split(*args, ws.data_ptr(), ws.numel(), _stream_ptr(a)),
-                   "grouped_fwd_split")
-    else:
-        _lib.check(lib.mxgg_grouped_fwd(*args, _stream_ptr(a)), "grouped_fwd")
+    stream = _stream_ptr(a)
+    esz = out.element_size()
+    rows = _rows_per_launch(a8.stride(0), K, M)
+    for r0 in range(0, max(M, 1), rows):
+        # Operands are read through 32-bit buffer ranges (< 2 GiB): a larger
+        # activation matrix runs as row chunks (multiples of 256 rows), each
+        # with the group ends shifted to the chunk and clamped to it (on the
+        # device, no host sync).  Every output row still comes from one
+        # full-K accumulation, so the chunked result is the same.
+        m = min(rows, M - r0)
+        e = ends
+        if e is not None and rows < M:
+            e = torch.clamp(ends - r0, 0, m)
+        args = (a8.data_ptr() + r0 * a8.stride(0), a8.stride(0),
+                sa.data_ptr() + r0 if sa is not None else None, ldas,
+                w8.data_ptr(), w8.stride(0), w8.stride(1),
+                sw.data_ptr() if sw is not None else None, wsg, ldws,
+                e.data_ptr() if e is not None else None, E,
+                m, N, K, out.data_ptr() + r0 * out.stride(0) * esz, out.stride(0),
+                _out_code(out_dtype))
+        split = _small_launch(m, N, E, a.device) if split_tail is None else split_tail
+        if split and m > 0 and N > 0:
+            ws = _split_workspace(a.device)
+            _lib.check(lib.mxgg_grouped_fwd_split(*args, ws.data_ptr(), ws.numel(), stream),
+                       "grouped_fwd_split")
+        else:
+            _lib.check(lib.mxgg_grouped_fwd(*args, stream), "grouped_fwd")
     return out
 
 

@@ -232,6 +232,42 @@ def test_torchao_named_forward(gpu):
     assert torch.equal(y1, y2) and torch.equal(y1, y3)
 
 
+def test_forward_above_2gib_runs_in_row_chunks(gpu):
+    # A is 360000 x 7168 e4m3 = 2.58 GB, past the 32-bit buffer range of one
+    # launch: grouped_mm runs it as row chunks of 299520 rows with shifted
+    # group ends.  The C ABI refuses the whole matrix in one launch; rows at
+    # the chunk boundary, at group boundaries and at both ends match the
+    # oracle, and one group straddles the chunk boundary.
+    M, N, K = 360000, 256, 7168
+    sizes = [100000, 250000, 10000]
+    g = torch.Generator(device=gpu).manual_seed(51)
+    a = torch.randint(0, 0x7E, (M, K), generator=g, device=gpu, dtype=torch.uint8)
+    a |= torch.randint(0, 2, (M, K), generator=g, device=gpu, dtype=torch.uint8) << 7
+    a_s = torch.randint(120, 134, (M, K // 32), generator=g, device=gpu, dtype=torch.uint8)
+    w = torch.randint(0, 0x7E, (3, N, K), generator=g, device=gpu, dtype=torch.uint8)
+    w_s = torch.randint(120, 134, (3, N, K // 32), generator=g, device=gpu, dtype=torch.uint8)
+    assert ops._rows_per_launch(K, K, M) == 299520
+    ends = torch.tensor(np.cumsum(sizes), dtype=torch.int32, device=gpu)
+    f8 = torch.float8_e4m3fn
+    y = ops.grouped_mm(a.view(f8), w.view(f8), ends, a_s, w_s)
+    lib = mxfp8gg.load_library()
+    assert lib.mxgg_grouped_fwd(a.data_ptr(), K, None, 0, w.data_ptr(), N * K, K, None, 0, 0,
+                                ends.data_ptr(), 3, M, N, K, y.data_ptr(), N, 0,
+                                None) == mxfp8gg._lib.ERR_UNSUPPORTED
+    rows = np.r_[0:8, 99990:100010, 299500:299540, 349990:350010, M - 8:M]
+    ri = torch.from_numpy(rows).to(gpu)
+    grp = np.searchsorted(np.cumsum(sizes), rows, side="right")
+    for e in range(3):
+        sel = rows[grp == e]
+        if sel.size == 0:
+            continue
+        si = torch.from_numpy(sel).to(gpu)
+        ref = O.grouped_fwd(u8(a[si]), u8(a_s[si]), u8(w[e:e + 1]), u8(w_s[e:e + 1]),
+                            np.array([sel.size]))
+        assert_close_to_oracle(y[si], ref)
+    assert not torch.isnan(y[ri].float()).any()
+
+
 @pytest.mark.parametrize("cfg", ["c2", "c3"])
 def test_full_size_forward_sampled_rows(gpu, cfg):
     x, w, sizes = getattr(workloads, cfg)(gpu)
