@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 8
+#define MXGG_ABI_VERSION 9
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -276,6 +276,28 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
                        const int32_t* group_ends, int64_t num_groups,
                        int64_t M, int64_t N, int64_t K,
                        void* dw, int out_dtype, int64_t split_tokens, void* stream);
+
+/*
+ * mxgg_grouped_wgrad with split_tokens > 0 and a caller-owned workspace of at
+ * least mxgg_grouped_wgrad_workspace_bytes(M, N, K, num_groups, split_tokens)
+ * bytes (16-byte aligned, no initialisation): the fp32 partial tiles of
+ * experts cut into several chunks go to the workspace and a second kernel on
+ * the same stream adds them in chunk order and writes dW (bf16 or fp32).
+ * Deterministic, and dW needs no zeroing (experts without tokens are written
+ * as zeros).  Same reference interface as mxgg_grouped_wgrad
+ * (wgrad_fused.py:22-112); the reference does not split.  Calls that share a
+ * workspace must be ordered on one stream.  The size query returns -1 for
+ * invalid arguments.
+ */
+int64_t mxgg_grouped_wgrad_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t num_groups,
+                                           int64_t split_tokens);
+int mxgg_grouped_wgrad_split(const void* go_t, int64_t ldgo, const void* go_scales_t,
+                             int64_t ldgos, const void* ia_t, int64_t ldia,
+                             const void* ia_scales_t, int64_t ldias,
+                             const int32_t* group_ends, int64_t num_groups,
+                             int64_t M, int64_t N, int64_t K,
+                             void* dw, int out_dtype, int64_t split_tokens,
+                             void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Token routing of a top-k MoE layer on one GPU (the layer's dispatch and

@@ -504,10 +504,11 @@ int mxgg_grouped_fwd_split(const void* a, int64_t lda, const void* a_scales, int
                      stream);
 }
 
-int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, int64_t ldgos,
-                       const void* ia_t, int64_t ldia, const void* ia_scales_t, int64_t ldias,
-                       const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t N,
-                       int64_t K, void* dw, int out_dtype, int64_t split_tokens, void* stream) {
+static int grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, int64_t ldgos,
+                         const void* ia_t, int64_t ldia, const void* ia_scales_t, int64_t ldias,
+                         const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t N,
+                         int64_t K, void* dw, int out_dtype, int64_t split_tokens,
+                         void* workspace, void* stream) {
   if (out_dtype != MXGG_OUT_BF16 && out_dtype != MXGG_OUT_F32)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: unknown out_dtype %d", out_dtype);
   if (M < 0 || N < 0 || K < 0)
@@ -528,7 +529,7 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
     return set_error(MXGG_ERR_INVALID_ARGUMENT,
                      "grouped_wgrad: split_tokens=%lld must be 0 or a positive multiple of 128",
                      (long long)split_tokens);
-  if (split_tokens > 0 && out_dtype != MXGG_OUT_F32)
+  if (split_tokens > 0 && out_dtype != MXGG_OUT_F32 && workspace == nullptr)
     return set_error(MXGG_ERR_UNSUPPORTED,
                      "grouped_wgrad: split-K accumulates with fp32 atomics (out_dtype F32 only)");
   if (N == 0 || K == 0) return MXGG_OK;
@@ -577,8 +578,48 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
   args.split = (int32_t)split_tokens;
   args.out_f32 = out_dtype == MXGG_OUT_F32;
   args.scaled = scaled;
+  args.split_ws = static_cast<float*>(workspace);
   return check_launch(launch_grouped_wgrad(args, static_cast<hipStream_t>(stream)),
                       "grouped_wgrad");
+}
+
+int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, int64_t ldgos,
+                       const void* ia_t, int64_t ldia, const void* ia_scales_t, int64_t ldias,
+                       const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t N,
+                       int64_t K, void* dw, int out_dtype, int64_t split_tokens, void* stream) {
+  return grouped_wgrad(go_t, ldgo, go_scales_t, ldgos, ia_t, ldia, ia_scales_t, ldias,
+                       group_ends, num_groups, M, N, K, dw, out_dtype, split_tokens, nullptr,
+                       stream);
+}
+
+int64_t mxgg_grouped_wgrad_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t num_groups,
+                                           int64_t split_tokens) {
+  if (M < 0 || N < 0 || K < 0 || num_groups < 1 || split_tokens < 128) return -1;
+  return wgrad_split_workspace_bytes(M, N, K, num_groups, split_tokens);
+}
+
+int mxgg_grouped_wgrad_split(const void* go_t, int64_t ldgo, const void* go_scales_t,
+                             int64_t ldgos, const void* ia_t, int64_t ldia,
+                             const void* ia_scales_t, int64_t ldias, const int32_t* group_ends,
+                             int64_t num_groups, int64_t M, int64_t N, int64_t K, void* dw,
+                             int out_dtype, int64_t split_tokens, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+  if (split_tokens <= 0 || split_tokens % 128 != 0 || split_tokens > INT32_MAX)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT,
+                     "grouped_wgrad_split: split_tokens=%lld must be a positive multiple of 128",
+                     (long long)split_tokens);
+  if (!workspace)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad_split: null workspace");
+  if (num_groups >= 1 && num_groups <= kMaxGroupsAbi && M >= 0 && N >= 0 && K >= 0 &&
+      workspace_bytes < wgrad_split_workspace_bytes(M, N, K, num_groups, split_tokens))
+    return set_error(MXGG_ERR_SHAPE, "grouped_wgrad_split: workspace_bytes=%lld < %lld",
+                     (long long)workspace_bytes,
+                     (long long)wgrad_split_workspace_bytes(M, N, K, num_groups, split_tokens));
+  if (!aligned16(workspace))
+    return set_error(MXGG_ERR_ALIGNMENT, "grouped_wgrad_split: workspace must be 16-byte aligned");
+  return grouped_wgrad(go_t, ldgo, go_scales_t, ldgos, ia_t, ldia, ia_scales_t, ldias,
+                       group_ends, num_groups, M, N, K, dw, out_dtype, split_tokens, workspace,
+                       stream);
 }
 
 // ---------------------------------------------------------------------------

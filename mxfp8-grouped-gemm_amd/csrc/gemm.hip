@@ -52,6 +52,10 @@ constexpr uint32_t kOobOffset = 0x80000000u;           // beyond every num_recor
 constexpr uint32_t kMaxSplit = 16;
 constexpr int64_t kSplitHdrBytes = 16384;
 constexpr int64_t kPartialBytes = 256 * 256 * 4;
+// Wgrad split with a workspace: header = E, items per expert, tile counts,
+// band width, then (expert, first item, chunks) of every rank; partial of
+// work item i at kWgHdrBytes + i * kPartialBytes.
+constexpr int64_t kWgHdrBytes = 32768;
 
 struct __align__(16) Smem {
   uint8_t ring[2][kStageBytes];
@@ -839,6 +843,22 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
   __syncthreads();
   scan_counts(sm, sm.sched, sm.items, E);
   const uint32_t total = (uint32_t)sm.items[E];
+  const bool staged = split > 0 && args.split_ws != nullptr;
+  if (staged && blockIdx.x == 0) {
+    int32_t* hdr = reinterpret_cast<int32_t*>(args.split_ws);
+    if (threadIdx.x == 0) {
+      hdr[0] = E;
+      hdr[1] = (int32_t)per_expert;
+      hdr[2] = (int32_t)n_tiles;
+      hdr[3] = (int32_t)k_tiles;
+      hdr[4] = (int32_t)gm;
+    }
+    for (int r = threadIdx.x; r < E; r += kThreads) {
+      hdr[8 + 4 * r] = sm.order[r];
+      hdr[9 + 4 * r] = sm.items[r];
+      hdr[10 + 4 * r] = sm.chunks[r];
+    }
+  }
 
   for (uint32_t base = 0;; base += gridDim.x) {
     const uint32_t lid = xcd_slice(base);
@@ -891,10 +911,88 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
     } else {
       mainloop<SCALED>(sm, P, Q, (uint32_t)cb, (uint32_t)ce, acc);
     }
+    if (staged && sm.chunks[rank] > 1) {
+      // one of several partials of this tile: the whole fp32 256x256 block
+      char* slot = reinterpret_cast<char*>(args.split_ws) + kWgHdrBytes +
+                   (int64_t)lid * kPartialBytes;
+      epilogue<true>(sm, acc, slot, 1024, 0u, 0u, 256u, 0u, 256u);
+      continue;
+    }
     char* out = reinterpret_cast<char*>(args.dw) +
                 (int64_t)g * args.N * args.K * (F32 ? 4 : 2);
     epilogue<F32>(sm, acc, out, (int64_t)args.K * (F32 ? 4 : 2), q0, 0u, (uint32_t)args.N, p0,
-                  (uint32_t)args.K, F32 && split > 0);
+                  (uint32_t)args.K, F32 && split > 0 && !staged);
+  }
+}
+
+// dW tiles of experts whose tokens were cut into several chunks: the chunks'
+// fp32 partials added in chunk order (the first is the starting value);
+// experts without tokens (no work items) written as zeros; experts with one
+// chunk were written by the GEMM itself.  Items are (rank, tile, row,
+// 4-column group), 4 per thread a grid-stride apart, loads before adds.
+__global__ __launch_bounds__(256) void k_wgrad_split_reduce(const float* __restrict__ ws,
+                                                            void* __restrict__ dw, int32_t N,
+                                                            int32_t K, int32_t out_f32) {
+  const int32_t* hdr = reinterpret_cast<const int32_t*>(ws);
+  const int32_t E = hdr[0], per_expert = hdr[1], n_tiles = hdr[2], k_tiles = hdr[3];
+  const uint32_t gm = (uint32_t)hdr[4];
+  const float* part = ws + kWgHdrBytes / 4;
+  const int64_t per_rank = (int64_t)per_expert * 16384;
+  const int64_t work = (int64_t)E * per_rank;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i0 = (int64_t)blockIdx.x * 256 + threadIdx.x; i0 < work;
+       i0 += kReduceItems * stride) {
+    v4f acc[kReduceItems];
+    int64_t dsto[kReduceItems];
+    int32_t pcol[kReduceItems];
+#pragma unroll
+    for (int u = 0; u < kReduceItems; ++u) {
+      const int64_t i = i0 + u * stride;
+      dsto[u] = -1;
+      pcol[u] = 0;
+      acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
+      if (i >= work) continue;
+      const int32_t r = (int32_t)(i / per_rank);
+      const int32_t t = (int32_t)((i >> 14) % per_expert);
+      const int32_t row = (int32_t)((i >> 6) & 255), c = (int32_t)(i & 63) * 4;
+      const int32_t* rh = hdr + 8 + 4 * r;
+      const int32_t chunks = rh[2];
+      if (chunks == 1) continue;
+      uint32_t nt, kt;
+      band_decode((uint32_t)t, (uint32_t)n_tiles, (uint32_t)k_tiles, gm, nt, kt);
+      const int32_t n = (int32_t)nt * 256 + row, k = (int32_t)kt * 256 + c;
+      if (n >= N || k >= K) continue;
+      dsto[u] = ((int64_t)rh[0] * N + n) * K + k;
+      pcol[u] = k;
+      if (chunks == 0) continue;
+      const float* src = part + ((int64_t)rh[1] + t) * 65536 + row * 256 + c;
+      acc[u] = *reinterpret_cast<const v4f*>(src);
+      for (int32_t ch = 1; ch < chunks; ++ch)
+        acc[u] += *reinterpret_cast<const v4f*>(src + (int64_t)ch * per_expert * 65536);
+    }
+#pragma unroll
+    for (int u = 0; u < kReduceItems; ++u) {
+      if (dsto[u] < 0) continue;
+      const int32_t k = pcol[u];
+      if (out_f32) {
+        float* dst = reinterpret_cast<float*>(dw) + dsto[u];
+        if (k + 4 <= K)
+          *reinterpret_cast<v4f*>(dst) = acc[u];
+        else
+          for (int32_t j = 0; k + j < K; ++j) dst[j] = acc[u][j];
+      } else {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(dw) + dsto[u];
+        if (k + 4 <= K) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16x2(acc[u][0], acc[u][1]),
+                                                      pack_bf16x2(acc[u][2], acc[u][3]));
+        } else {
+          for (int32_t j = 0; k + j < K; ++j) {
+            const __bf16 h = (__bf16)acc[u][j];
+            dst[j] = *reinterpret_cast<const uint16_t*>(&h);
+          }
+        }
+      }
+    }
   }
 }
 
@@ -905,6 +1003,12 @@ int persistent_grid() {
 }
 
 }  // namespace
+
+int64_t wgrad_split_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t E, int64_t split) {
+  // sum over experts of ceil(tokens / split) <= M / split + E
+  const int64_t tiles = ((N + 255) / 256) * ((K + 255) / 256);
+  return kWgHdrBytes + (M / split + E) * tiles * kPartialBytes;
+}
 
 int64_t fwd_split_workspace_bytes() {
   return kSplitHdrBytes + (int64_t)persistent_grid() * kPartialBytes;
@@ -940,6 +1044,11 @@ hipError_t launch_grouped_wgrad(const WgradArgs& a, hipStream_t stream) {
     if (a.out_f32) MXGG_WG(false, true); else MXGG_WG(false, false);
   }
 #undef MXGG_WG
+  if (a.split <= 0 || a.split_ws == nullptr) return hipGetLastError();
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(k_wgrad_split_reduce, dim3(4 * grid.x), dim3(256), 0, stream, a.split_ws,
+                     a.dw, a.N, a.K, a.out_f32);
   return hipGetLastError();
 }
 

@@ -144,7 +144,12 @@ struct WgradArgs {
   int32_t split;       // tokens per split-K chunk (multiple of 128), 0 = whole groups
   int32_t out_f32;
   int32_t scaled;
+  // With split > 0: workspace of wgrad_split_workspace_bytes() for the fp32
+  // partials, added in chunk order by a second kernel (deterministic, any
+  // output dtype); nullptr = fp32 atomics into the zeroed output.
+  float* split_ws;
 };
 hipError_t launch_grouped_wgrad(const WgradArgs& args, hipStream_t stream);
+int64_t wgrad_split_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t E, int64_t split);
 
 }  // namespace mxgg

@@ -31,7 +31,7 @@ OUT_F32 = 1
 SCALES_ROW_MAJOR = 0
 SCALES_BLOCK_MAJOR = 1
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -77,6 +77,12 @@ SIGNATURES = {
     "mxgg_grouped_wgrad": (
         _I,
         [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I, _I64, _P],
+    ),
+    "mxgg_grouped_wgrad_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64, _I64]),
+    "mxgg_grouped_wgrad_split": (
+        _I,
+        [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I, _I64, _P,
+         _I64, _P],
     ),
     "mxgg_route_plan": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
     "mxgg_gather_rows": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P]),

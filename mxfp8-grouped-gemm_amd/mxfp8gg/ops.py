@@ -575,18 +575,19 @@ def _cu_count(device) -> int:
 def wgrad_split_tokens(M: int, N: int, K: int, E: int, cus: int) -> int:
     """Split-K chunk (tokens) for a weight-gradient call, from shapes only.
 
-    The partial sums of a split are added with fp32 atomics, which move about
-    0.5 TB/s, so splitting pays only when most compute units would otherwise
-    idle: with at most cus/4 output tiles (E * ceil(N/256) * ceil(K/256)), the
-    tokens are cut into at most cus/tiles (<= 8) chunks of at least 4096
-    tokens (one round of work items), assuming the M tokens spread evenly over
-    the experts (group sizes live on the device and are not read back).
-    Returns 0 for no split."""
+    With at most cus/2 output tiles (E * ceil(N/256) * ceil(K/256)) most
+    compute units would idle, so each expert's tokens are cut into up to
+    min(16, cus/tiles) chunks of at least 4096 tokens: about one round of
+    work items, each writing an fp32 partial tile that a second kernel adds in
+    chunk order (measured best on 32, 64 and 128 tiles; with more tiles the
+    partials cost more than the idle units).  The M tokens are assumed to
+    spread evenly over the experts (group sizes live on the device and are not
+    read back).  Returns 0 for no split."""
     tiles = E * ((N + 255) // 256) * ((K + 255) // 256)
-    if tiles == 0 or M == 0 or 4 * tiles > cus:
+    if tiles == 0 or M == 0 or 2 * tiles > cus:
         return 0
     per_expert = max(1, M // max(E, 1))
-    splits = min(8, cus // tiles)
+    splits = min(16, cus // tiles)
     chunk = max(4096, (per_expert + splits - 1) // splits)
     chunk = (chunk + 127) // 128 * 128
     return 0 if chunk >= per_expert else chunk
@@ -604,9 +605,10 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
     group end must be a multiple of 32 (the layout to_mxfp8_dim1 produces).
     Empty groups yield zeros.
     split_tokens: split-K chunk in tokens (multiple of 128), 0 for none, None
-    to choose from the shapes (wgrad_split_tokens) for fp32 output.  Split-K
-    adds fp32 partial sums atomically into a zeroed output, so the result can
-    differ from the unsplit one in the last bits (summation order).
+    to choose from the shapes (wgrad_split_tokens).  A split call writes the
+    fp32 partial tiles to a workspace and adds them in chunk order
+    (mxgg_grouped_wgrad_split): deterministic, any output dtype, equal to the
+    unsplit result up to fp32 summation order.
     """
     _need_gpu(go, "go")
     _need_gpu(ia, "ia")
@@ -627,27 +629,26 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
     E = offs.numel()
     ends = _group_ends(offs, E, go.device)
     if split_tokens is None:
-        split_tokens = (wgrad_split_tokens(M, N, K, E, _cu_count(go.device))
-                        if out_dtype == torch.float32 else 0)
+        split_tokens = wgrad_split_tokens(M, N, K, E, _cu_count(go.device))
     if out is None:
-        alloc = torch.zeros if split_tokens else torch.empty
-        out = alloc((E, N, K), dtype=out_dtype, device=go.device)
+        out = torch.empty((E, N, K), dtype=out_dtype, device=go.device)
     elif out.shape != (E, N, K) or out.dtype != out_dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous [E, N, K] tensor of out_dtype")
-    elif split_tokens:
-        out.zero_()
     lib = _lib.load()
-    _lib.check(
-        lib.mxgg_grouped_wgrad(
-            g8.data_ptr(), g8.stride(0),
+    args = (g8.data_ptr(), g8.stride(0),
             sg.data_ptr() if sg is not None else None, ldgs,
             i8.data_ptr(), i8.stride(0),
             si.data_ptr() if si is not None else None, ldis,
-            ends.data_ptr(), E, M, N, K, out.data_ptr(), _out_code(out_dtype), int(split_tokens),
-            _stream_ptr(go),
-        ),
-        "grouped_wgrad",
-    )
+            ends.data_ptr(), E, M, N, K, out.data_ptr(), _out_code(out_dtype), int(split_tokens))
+    if split_tokens:
+        nbytes = int(lib.mxgg_grouped_wgrad_workspace_bytes(M, N, K, E, int(split_tokens)))
+        if nbytes < 0:
+            raise ValueError(f"split_tokens={split_tokens} must be a positive multiple of 128")
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=go.device)
+        _lib.check(lib.mxgg_grouped_wgrad_split(*args, ws.data_ptr(), nbytes, _stream_ptr(go)),
+                   "grouped_wgrad_split")
+    else:
+        _lib.check(lib.mxgg_grouped_wgrad(*args, _stream_ptr(go)), "grouped_wgrad")
     return out
 
 

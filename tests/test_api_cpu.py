@@ -98,8 +98,12 @@ def test_apply_without_torchao_raises():
 def test_wgrad_split_choice():
     # enough tiles for every compute unit: no split
     assert ops.wgrad_split_tokens(65536, 4096, 7168, 32, 256) == 0
-    # 128 tiles on 256 units: atomics would cost what the idle half saves
-    assert ops.wgrad_split_tokens(65536, 2048, 1024, 4, 256) == 0
+    # 128 tiles on 256 units: 2 chunks per expert fill the other half
+    assert ops.wgrad_split_tokens(65536, 2048, 1024, 4, 256) == 8192
+    # 512 tiles: the partials would cost more than the idle units
+    assert ops.wgrad_split_tokens(65536, 2048, 2048, 8, 256) == 0
+    # 8 tiles: at most 16 chunks, none shorter than 4096 tokens
+    assert ops.wgrad_split_tokens(131072, 512, 512, 2, 256) == 4096
     # 2 experts x 4 x 4 tiles = 32 on 256 units: 8 chunks of 4096 tokens
     assert ops.wgrad_split_tokens(65536, 1024, 1024, 2, 256) == 4096
     # 1 expert x 8 x 8 tiles = 64: 4 chunks

@@ -71,6 +71,37 @@ def _fwd_split(lib, ws=FAKE, nbytes=None, **kw):
                                       args["dt"], ws, nbytes, None)
 
 
+def test_wgrad_split_workspace_bound(lib):
+    # header + one 256x256 fp32 partial per work item, with at most
+    # M / split + E chunks over all experts; -1 for invalid arguments
+    assert lib.mxgg_grouped_wgrad_workspace_bytes(65536, 1024, 1024, 2, 4096) == \
+        32768 + (16 + 2) * 16 * 256 * 256 * 4
+    assert lib.mxgg_grouped_wgrad_workspace_bytes(65536, 1024, 1024, 2, 0) == -1
+    assert lib.mxgg_grouped_wgrad_workspace_bytes(65536, 1024, 1024, 0, 4096) == -1
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(split=0), _lib.ERR_INVALID_ARGUMENT),
+    (dict(split=200), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ws=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(nbytes=32768), _lib.ERR_SHAPE),
+    (dict(ws=FAKE + 4), _lib.ERR_ALIGNMENT),
+    (dict(M=100), _lib.ERR_SHAPE),                     # then the wgrad's own checks
+])
+def test_grouped_wgrad_split_rejects(lib, kw, status):
+    a = dict(go=FAKE, ldgo=4096, gs=None, ldgs=0, ia=FAKE, ldia=4096, is_=None, ldis=0,
+             ends=FAKE, E=2, M=4096, N=256, K=256, dw=FAKE, dt=_lib.OUT_F32, split=1024,
+             ws=FAKE, nbytes=None)
+    a.update(kw)
+    if a["nbytes"] is None:
+        a["nbytes"] = max(0, lib.mxgg_grouped_wgrad_workspace_bytes(a["M"], a["N"], a["K"],
+                                                                    a["E"], 1024))
+    assert lib.mxgg_grouped_wgrad_split(a["go"], a["ldgo"], a["gs"], a["ldgs"], a["ia"],
+                                        a["ldia"], a["is_"], a["ldis"], a["ends"], a["E"],
+                                        a["M"], a["N"], a["K"], a["dw"], a["dt"], a["split"],
+                                        a["ws"], a["nbytes"], None) == status
+
+
 def test_split_workspace_size_covers_one_partial_per_unit(lib):
     # header + one 256x256 fp32 partial per workgroup of the persistent grid
     n = lib.mxgg_grouped_fwd_workspace_bytes()

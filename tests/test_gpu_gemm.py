@@ -396,6 +396,45 @@ def test_wgrad_split_k_matches_oracle(gpu, sizes, split):
             assert (dw[g] - whole[g]).abs().max() <= 2.0 ** -12 * whole[g].abs().max()
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_wgrad_staged_split_deterministic_any_dtype(gpu, out_dtype):
+    # the workspace split (mxgg_grouped_wgrad_split): bf16 output too, no
+    # zeroing of dW (a NaN-filled output comes back with zeros for the empty
+    # expert), bit-equal repeat calls, the unsplit result up to fp32 summation
+    # order, and the fp32-atomics split of mxgg_grouped_wgrad within the same
+    # bound
+    sizes = [1024, 0, 2976, 96, 352]
+    M, N, K = sum(sizes), 288, 320
+    go_q, go_s = _rand_q((N, M), gpu, 61)
+    ia_q, ia_s = _rand_q((K, M), gpu, 62)
+    ends = workloads.ends_of(sizes)
+    offs = torch.from_numpy(ends).to(gpu)
+    go8, ia8 = go_q.view(torch.float8_e4m3fn), ia_q.view(torch.float8_e4m3fn)
+    E = len(sizes)
+    out = torch.full((E, N, K), float("nan"), dtype=out_dtype, device=gpu)
+    dw = ops.grouped_wgrad(go8, ia8, offs, go_s, ia_s, out_dtype=out_dtype, out=out,
+                           split_tokens=256)
+    dw2 = ops.grouped_wgrad(go8, ia8, offs, go_s, ia_s, out_dtype=out_dtype, split_tokens=256)
+    assert torch.equal(dw.view(torch.uint8), dw2.view(torch.uint8))
+    assert torch.all(dw[1] == 0)
+    whole = ops.grouped_wgrad(go8, ia8, offs, go_s, ia_s, out_dtype=out_dtype, split_tokens=0)
+    ref = O.grouped_wgrad(u8(go_q), u8(go_s), u8(ia_q), u8(ia_s), ends)
+    tol = 2.0 ** -12 if out_dtype == torch.float32 else 2.0 ** -7
+    for g in (0, 2, 3, 4):
+        assert_close_to_oracle(dw[g], ref[g])
+        assert (dw[g].float() - whole[g].float()).abs().max() <= tol * whole[g].float().abs().max()
+    if out_dtype == torch.float32:
+        sg, ldg = ops._scales_2d(go_s, N, M // 32, "go_s")
+        si, ldi = ops._scales_2d(ia_s, K, M // 32, "ia_s")
+        at = torch.zeros((E, N, K), dtype=torch.float32, device=gpu)
+        lib = mxfp8gg.load_library()
+        assert lib.mxgg_grouped_wgrad(
+            go_q.data_ptr(), M, sg.data_ptr(), ldg, ia_q.data_ptr(), M, si.data_ptr(), ldi,
+            offs.data_ptr(), E, M, N, K, at.data_ptr(), mxfp8gg._lib.OUT_F32, 256,
+            torch.cuda.current_stream(gpu).cuda_stream) == 0
+        assert (at - dw).abs().max() <= 2.0 ** -12 * dw.abs().max()
+
+
 def test_wgrad_split_k_chosen_for_few_tiles(gpu):
     # 2 experts x 2 x 2 output tiles: far fewer than compute units, so the
     # call splits the 16384 tokens of each expert on its own
