@@ -127,6 +127,49 @@ def dense_c2_shape(torch, mxfp8gg, dev, steps=10, warmup=3):
     return res
 
 
+def small_launches(torch, mxfp8gg, dev, steps=10, warmup=3):
+    """Calls with fewer output tiles than compute units, split along K over the
+    idle units or not: forward (one expert, K=7168; 16 and 128 tiles) and
+    weight gradient (fp32 dW; 32, 64 and 128 tiles, 65536 or 32768 tokens
+    spread evenly).  Split forwards/wgrads write fp32 partials to a workspace
+    and a second kernel adds them in a fixed order."""
+    from mxfp8gg import ops
+    res = {"forward": [], "wgrad": []}
+    gen = torch.Generator(device=dev).manual_seed(2)
+    for M, N in ((512, 2048), (2048, 4096)):
+        K = 7168
+        xq, xs = mxfp8gg.to_mxfp8_dim0(torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16))
+        wq, ws = mxfp8gg.to_mxfp8_dim0(
+            (torch.randn((1, N, K), generator=gen, device=dev) * 0.006).to(torch.bfloat16))
+        ends = torch.tensor([M], dtype=torch.int32, device=dev)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        fl = 2 * M * N * K
+        row = {"M": M, "N": N, "K": K, "tiles": (M // 256) * (N // 256)}
+        for name, sp in (("unsplit_tflops", False), ("split_tflops", True)):
+            row[name] = round(fl / time_launches(
+                lambda sp=sp: ops.grouped_mm(xq, wq, ends, xs, ws, out=out, split_tail=sp),
+                steps, warmup, torch) / 1e9, 1)
+        res["forward"].append(row)
+    for E, M, N, K in ((2, 65536, 1024, 1024), (1, 32768, 2048, 2048), (4, 65536, 2048, 1024)):
+        dy = torch.randn((M, N), generator=gen, device=dev).to(torch.bfloat16)
+        x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+        offs = torch.arange(1, E + 1, dtype=torch.int32, device=dev) * (M // E)
+        go, gos, pad = mxfp8gg.to_mxfp8_dim1(dy, offs)
+        ia, ias, _ = mxfp8gg.to_mxfp8_dim1(x, offs)
+        del dy, x
+        out = torch.empty((E, N, K), dtype=torch.float32, device=dev)
+        split = ops.wgrad_split_tokens(go.shape[1], N, K, E, ops._cu_count(dev))
+        fl = 2 * M * N * K
+        row = {"E": E, "tokens": M, "N": N, "K": K, "tiles": E * (N // 256) * (K // 256),
+               "split_tokens": split}
+        for name, sp in (("unsplit_tflops", 0), ("split_tflops", split)):
+            row[name] = round(fl / time_launches(
+                lambda sp=sp: ops.grouped_wgrad(go, ia, pad, gos, ias, out=out, split_tokens=sp),
+                steps, warmup, torch) / 1e9, 1)
+        res["wgrad"].append(row)
+    return res
+
+
 def layer_step_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     """one DSv3 expert-FFN layer step on one GPU --
     131072 routed tokens, Zipf(1.0) over 32 experts, hidden 7168, intermediate
@@ -300,13 +343,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "c5", "routing",
-                                       "dense"],
+                                       "dense", "small"],
                     default="all",
                     help="fwd / wgrad: time only that GEMM (for profiler runs); copy: a plain "
                          "1 GiB device-to-device copy, the reference for HBM byte counters; "
                          "ref8: the reference's 8 equal-group shapes only; c5: the full "
                          "expert-FFN layer step only; routing: C5 as a routed top-8 layer; "
-                         "dense: C2's shape as one dense GEMM, with hipBLASLt beside it")
+                         "dense: C2's shape as one dense GEMM, with hipBLASLt beside it; "
+                         "small: launches with fewer tiles than compute units, split or not")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the MXFP8 grouped GEMM shards by expert and "
@@ -327,6 +371,9 @@ def main():
         return
     if args.only == "routing":
         print(json.dumps(routing_c5(torch, mxfp8gg, workloads, dev)), flush=True)
+        return
+    if args.only == "small":
+        print(json.dumps(small_launches(torch, mxfp8gg, dev)), flush=True)
         return
     if args.only == "dense":
         print(json.dumps(dense_c2_shape(torch, mxfp8gg, dev)), flush=True)
@@ -430,6 +477,8 @@ def main():
         components["ref_equal_shapes"] = ref_equal_shapes(torch, mxfp8gg, workloads, dev)
         log("C2's shape as one dense GEMM (kernel ceiling, vendor library beside it)")
         components["dense_c2_shape"] = dense_c2_shape(torch, mxfp8gg, dev)
+        log("small launches split along K")
+        components["small_launches"] = small_launches(torch, mxfp8gg, dev)
         log("C5: expert-FFN layer step (forward + backward)")
         components["layer_step_c5"] = layer_step_c5(torch, mxfp8gg, workloads, dev)
         log("C5 as a routed top-8 layer (dispatch, combine)")
