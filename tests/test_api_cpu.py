@@ -95,6 +95,18 @@ def test_apply_without_torchao_raises():
         patch_kernels.apply()
 
 
+def test_forward_rows_per_launch_stay_under_the_buffer_range():
+    # one launch reads A through a 32-bit buffer range: (rows - 1) * lda + K
+    # must stay below 0x7FFFFFF0; larger A runs in chunks of whole 256-row tiles
+    assert ops._rows_per_launch(7168, 7168, 1000) == 1000
+    assert ops._rows_per_launch(7168, 7168, 0) == 1
+    r = ops._rows_per_launch(7168, 7168, 360000)
+    assert r == 299520 and r % 256 == 0 and (r - 1) * 7168 + 7168 <= 0x7FFFFFF0
+    assert (r + 256 - 1) * 7168 + 7168 > 0x7FFFFFF0      # the next multiple would not fit
+    lda = 1 << 23   # the largest row stride the C ABI accepts
+    assert ops._rows_per_launch(lda, 4096, 1000) == 256
+
+
 def test_wgrad_split_choice():
     # enough tiles for every compute unit: no split
     assert ops.wgrad_split_tokens(65536, 4096, 7168, 32, 256) == 0
