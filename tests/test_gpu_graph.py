@@ -72,3 +72,37 @@ def test_graph_replays_match_eager(gpu):
         assert torch.equal(g_out.view(torch.int16), e_out.view(torch.int16))
         assert torch.equal(g_dw.view(torch.int16), e_dw.view(torch.int16))
         assert torch.isfinite(e_out.float()).all()
+
+
+def test_graph_of_routed_forward_only(gpu):
+    # the whole forward-only routed layer captured as one graph
+    # (plan, gathered cast, weight casts, two GEMMs, SwiGLU cast, combine)
+    T, K, E, H, F = 64, 8, 16, 256, 128
+    gen = torch.Generator(device=gpu).manual_seed(72)
+    x = torch.empty((T, H), dtype=torch.bfloat16, device=gpu)
+    wgu = torch.empty((E, 2 * F, H), dtype=torch.bfloat16, device=gpu)
+    wd = torch.empty((E, H, F), dtype=torch.bfloat16, device=gpu)
+    _fill(gen, x, wgu, wd)
+    idx_np, sc_np = workloads.topk_routing(T, E, K, 1.0, 72)
+    idx = torch.from_numpy(idx_np).to(gpu)
+    sc = torch.from_numpy(sc_np).to(gpu)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mxfp8gg.moe_routed_ffn(x, idx, sc, wgu, wd)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        g_out = mxfp8gg.moe_routed_ffn(x, idx, sc, wgu, wd)
+    for r in range(3):
+        _fill(gen, x)
+        i2, s2 = workloads.topk_routing(T, E, K, 1.0, 100 + r)
+        idx.copy_(torch.from_numpy(i2).to(gpu))
+        sc.copy_(torch.from_numpy(s2).to(gpu))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        e_out = mxfp8gg.moe_routed_ffn(x, idx, sc, wgu, wd)
+        torch.cuda.synchronize()
+        assert torch.equal(g_out.view(torch.int16), e_out.view(torch.int16))
