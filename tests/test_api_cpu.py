@@ -163,3 +163,16 @@ def test_weight_cache_distinguishes_tensors_and_evicts_lru():
     assert len(calls) == 4                          # evicted earlier, cast again
     cache.clear()
     assert len(cache) == 0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    # one GPU's expert share is the measured unit: --gpus 2 exits with a message
+    # before touching a device
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
