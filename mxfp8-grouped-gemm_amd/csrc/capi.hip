@@ -547,8 +547,10 @@ static int grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t
                      "grouped_wgrad: scale bases and strides must be multiples of 4");
   if (scaled && ((M / 32) * ldgos > kMaxBufferBytes || (M / 32) * ldias > kMaxBufferBytes))
     return set_error(MXGG_ERR_UNSUPPORTED, "grouped_wgrad: scale array larger than 2 GiB");
-  if ((go_t && !aligned16(go_t)) || (ia_t && !aligned16(ia_t)) || ldgo % 16 != 0 ||
-      ldia % 16 != 0)
+  // No tokens (M == 0): the operands are never read and every expert's dW is
+  // written as zeros, so their layout does not matter.
+  if (M > 0 && ((go_t && !aligned16(go_t)) || (ia_t && !aligned16(ia_t)) || ldgo % 16 != 0 ||
+                ldia % 16 != 0))
     return set_error(MXGG_ERR_ALIGNMENT,
                      "grouped_wgrad: operands must be 16-byte aligned with ld % 16 == 0");
   const int esz = out_dtype == MXGG_OUT_F32 ? 4 : 2;

@@ -435,6 +435,23 @@ def test_wgrad_staged_split_deterministic_any_dtype(gpu, out_dtype):
         assert (at - dw).abs().max() <= 2.0 ** -12 * dw.abs().max()
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("split", [0, 128])
+def test_wgrad_without_tokens_is_zero(gpu, out_dtype, split):
+    # every expert empty (no tokens routed here): dW is zeros, whatever the
+    # layout of the empty operands (an empty [N, 0] tensor has row stride 1)
+    N, K, E = 160, 224, 3
+    go = torch.empty((N, 0), dtype=torch.uint8, device=gpu).view(torch.float8_e4m3fn)
+    ia = torch.empty((K, 0), dtype=torch.uint8, device=gpu).view(torch.float8_e4m3fn)
+    gs = torch.empty((N, 0), dtype=torch.uint8, device=gpu)
+    is_ = torch.empty((K, 0), dtype=torch.uint8, device=gpu)
+    ends = torch.zeros(E, dtype=torch.int32, device=gpu)
+    out = torch.full((E, N, K), float("nan"), dtype=out_dtype, device=gpu)
+    dw = ops.grouped_wgrad(go, ia, ends, gs, is_, out_dtype=out_dtype, out=out,
+                           split_tokens=split)
+    assert torch.all(dw == 0)
+
+
 def test_wgrad_split_k_chosen_for_few_tiles(gpu):
     # 2 experts x 2 x 2 output tiles: far fewer than compute units, so the
     # call splits the 16384 tokens of each expert on its own
