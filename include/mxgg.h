@@ -19,6 +19,8 @@
  * group 0 starts at 0) — the convention of torch._grouped_mm and of the
  * reference's callers (e2e_bench.py:42, wgrad_fused.py:64).  Empty groups are
  * allowed.  `group_ends` lives in device memory and is read only on the GPU.
+ * Ends that decrease or leave [0, rows] are read as their running maximum
+ * clamped to [0, rows] (see mxgg_offs_to_group_ends), so groups never overlap.
  */
 #ifndef MXGG_H
 #define MXGG_H
@@ -30,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 9
+#define MXGG_ABI_VERSION 10
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -65,6 +67,21 @@ typedef enum mxgg_scale_layout {
   MXGG_SCALES_ROW_MAJOR = 0,
   MXGG_SCALES_BLOCK_MAJOR = 1
 } mxgg_scale_layout;
+
+/*
+ * How a caller's `offs` vector describes the expert groups (mxgg_offs_to_group_ends).
+ *   ENDS  : cumulative token ends (torch._grouped_mm convention; the reference's
+ *           layer step, e2e_bench.py:42,117)
+ *   SIZES : tokens per group (the reference's wgrad_fused documentation,
+ *           wgrad_fused.py:37, and its wgrad benchmark, bench_wgrad_dsv3.py:52)
+ *   AUTO  : SIZES when the entries add up to exactly `tokens` and the last entry
+ *           is below `tokens`, ENDS otherwise
+ */
+typedef enum mxgg_offs_kind {
+  MXGG_OFFS_ENDS = 0,
+  MXGG_OFFS_SIZES = 1,
+  MXGG_OFFS_AUTO = 2
+} mxgg_offs_kind;
 
 /* ABI version of the loaded library (MXGG_ABI_VERSION at build time). */
 int mxgg_abi_version(void);
@@ -192,6 +209,37 @@ int mxgg_scales_to_block_major(const void* src, int64_t batch, int64_t rows, int
                                int64_t dst_bstride, int64_t ldd, void* stream);
 
 /*
+ * Group ends from a caller's `offs` (int32 [num_groups], device) read as
+ * `offs_kind`: group_ends = offs (ENDS) or its inclusive prefix sum (SIZES,
+ * saturated to int32), chosen on the device for AUTO with `tokens` the token
+ * count of the operands.  One workgroup, no host sync; group_ends may not
+ * alias offs.  1 <= num_groups <= 1024.
+ * Replaces nothing in the reference, whose wgrad entry points read only
+ * offs.shape[0] and split M // E tokens per expert (wgrad_fused.py:45-47); it
+ * lets the same call sites (wgrad_fused.py:37 sizes, e2e_bench.py:117 ends)
+ * honour unequal groups.
+ *
+ * Every kernel of this library reads group ends by one rule: m[g] = the
+ * running maximum of group_ends[0..g] clamped to [0, rows]; group g covers
+ * [m[g-1], m[g]) (m[-1] = 0).  Non-decreasing ends are used as given; a
+ * decreasing entry makes its group empty, so no row belongs to two groups.
+ */
+int mxgg_offs_to_group_ends(const int32_t* offs, int64_t num_groups, int64_t tokens,
+                            int offs_kind, int32_t* group_ends, void* stream);
+
+/*
+ * Zero the rows of a row-major matrix that lie past the last group end
+ * (rows r >= m[num_groups-1] under the rule above), which no grouped GEMM
+ * writes: out holds `rows` rows of `row_bytes` bytes with stride `ld_bytes`;
+ * out, row_bytes and ld_bytes are multiples of 16.  The end is read on the
+ * device.  For callers that hand the whole matrix on, e.g. as an input
+ * gradient to autograd (the reference has no counterpart: its groups always
+ * cover every row, fused_fwd.py:47-48).
+ */
+int mxgg_zero_rows_past_groups(void* out, int64_t rows, int64_t row_bytes, int64_t ld_bytes,
+                               const int32_t* group_ends, int64_t num_groups, void* stream);
+
+/*
  * Forward grouped GEMM  out[rows of g] = A[rows of g] . W[g]^T  (fp32 accumulate).
  *   a        : e4m3 [M, K], row stride lda
  *   a_scales : E8M0 BLOCK_MAJOR [K/32][ldas], ldas >= M       (or NULL)
@@ -253,10 +301,13 @@ int mxgg_grouped_fwd_split(const void* a, int64_t lda, const void* a_scales, int
  *   ia_scales_t : E8M0 BLOCK_MAJOR [M/32][ldias], ldias >= K   (or NULL)
  *                 (strides and bases multiples of 4; readable extent as for
  *                 mxgg_grouped_fwd)
- *   group_ends  : int32 [num_groups] token ends (device); every end must be a
- *                 multiple of 32 when scales are given (the padded layout that
- *                 mxgg_quant_dim1 produces), so a scale block never straddles
- *                 two groups
+ *   group_ends  : int32 [num_groups] token ends (device).  With scales every
+ *                 group bound must be a multiple of 32 (the padded layout that
+ *                 mxgg_quant_dim1 produces): a scale block may not span two
+ *                 groups, and an expert whose bounds are not multiples of 32 is
+ *                 written as NaN.  Without scales the bounds may be any token
+ *                 index (ranges off the 16-token load grid are masked token by
+ *                 token, at some speed cost for those experts only).
  *   dw          : [num_groups, N, K] bf16 or f32, contiguous; empty groups are
  *                 written with zeros
  * go_t and ia_t are 16-byte aligned, ldgo and ldia multiples of 16 and at most

@@ -398,6 +398,46 @@ int mxgg_scales_to_block_major(const void* src, int64_t batch, int64_t rows, int
       "scales_to_block_major");
 }
 
+int mxgg_offs_to_group_ends(const int32_t* offs, int64_t num_groups, int64_t tokens,
+                            int offs_kind, int32_t* group_ends, void* stream) {
+  if (offs_kind != MXGG_OFFS_ENDS && offs_kind != MXGG_OFFS_SIZES && offs_kind != MXGG_OFFS_AUTO)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "offs_to_group_ends: unknown offs_kind %d",
+                     offs_kind);
+  if (num_groups < 1 || num_groups > kMaxGroupsAbi)
+    return set_error(MXGG_ERR_UNSUPPORTED, "offs_to_group_ends: num_groups=%lld outside [1, %lld]",
+                     (long long)num_groups, (long long)kMaxGroupsAbi);
+  if (tokens < 0) return set_error(MXGG_ERR_SHAPE, "offs_to_group_ends: negative tokens");
+  if (!offs || !group_ends)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "offs_to_group_ends: null pointer");
+  if (offs == group_ends)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "offs_to_group_ends: group_ends aliases offs");
+  return check_launch(launch_offs_to_ends(offs, num_groups, tokens, offs_kind, group_ends,
+                                          static_cast<hipStream_t>(stream)),
+                      "offs_to_group_ends");
+}
+
+int mxgg_zero_rows_past_groups(void* out, int64_t rows, int64_t row_bytes, int64_t ld_bytes,
+                               const int32_t* group_ends, int64_t num_groups, void* stream) {
+  if (rows < 0 || row_bytes < 0 || ld_bytes < row_bytes)
+    return set_error(MXGG_ERR_SHAPE, "zero_rows_past_groups: rows=%lld row_bytes=%lld ld=%lld",
+                     (long long)rows, (long long)row_bytes, (long long)ld_bytes);
+  if (num_groups < 1 || num_groups > kMaxGroupsAbi)
+    return set_error(MXGG_ERR_UNSUPPORTED,
+                     "zero_rows_past_groups: num_groups=%lld outside [1, %lld]",
+                     (long long)num_groups, (long long)kMaxGroupsAbi);
+  if (rows == 0 || row_bytes == 0) return MXGG_OK;
+  if (!out || !group_ends)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "zero_rows_past_groups: null pointer");
+  if (!aligned16(out) || row_bytes % 16 != 0 || ld_bytes % 16 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT,
+                     "zero_rows_past_groups: out, row_bytes and ld_bytes must be multiples of 16");
+  if (rows > INT32_MAX)
+    return set_error(MXGG_ERR_UNSUPPORTED, "zero_rows_past_groups: rows above 2^31");
+  return check_launch(launch_zero_tail(static_cast<uint8_t*>(out), rows, row_bytes, ld_bytes,
+                                       group_ends, num_groups, static_cast<hipStream_t>(stream)),
+                      "zero_rows_past_groups");
+}
+
 static int grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
                        const void* w, int64_t w_group_stride, int64_t ldw, const void* w_scales,
                        int64_t ws_group_stride, int64_t ldws, const int32_t* group_ends,

@@ -64,6 +64,7 @@ struct __align__(16) Smem {
   int32_t scan_tmp[kThreads];
   int32_t chunks[kMaxGroups];      // wgrad: split-K chunks of the expert of each rank
   int32_t items[kMaxGroups + 1];   // wgrad: prefix of work items over ranks
+  int32_t gend[kMaxGroups];        // monotone clamped group ends (monotone_ends_to_lds)
 };
 
 // Raw 128-bit buffer descriptor (gfx9 layout: base, stride 0, num_records,
@@ -172,7 +173,7 @@ __device__ __forceinline__ void dma_x1(const desc_t& d, uint32_t lds_addr, uint3
 //  Scales: wave w copies block k0/32 + w of both operands: 256 rows = 64 lanes
 //  x 4 bytes in row order.  A block outside [klo, kend) lands as zeros (scale
 //  2^-127 on zero payload).
-template <bool SCALED>
+template <bool SCALED, bool MASK = false>
 struct Stream {
   uint32_t vp, vq;   // lane offset of load 0 without k0
   uint32_t kcol;     // lane's chunk column within a stage (bytes)
@@ -197,9 +198,11 @@ struct Stream {
 
   // Lane offsets of stage k0 (an out-of-range base when the chunk is outside
   // [klo, kend); adding a step to it stays out of range).
+  // MASK: a chunk that overlaps [klo, kend) at all is loaded (the bytes outside
+  // are zeroed in registers after the fragment reads, mask_frags()).
   __device__ __forceinline__ void stage_base(uint32_t k0, uint32_t& bp, uint32_t& bq) const {
     const uint32_t k = k0 + kcol;
-    const bool ok = k >= klo && k < kend;
+    const bool ok = (MASK ? k + 16u > klo : k >= klo) && k < kend;
     bp = ok ? vp + k0 : kOobOffset;
     bq = ok ? vq + k0 : kOobOffset;
   }
@@ -335,6 +338,38 @@ __device__ __forceinline__ void mfma_row(const Frags& f, v16f (&acc)[4][4]) {
   mfma1<I, 3>(f, acc);
 }
 
+// Bytes of the 4-byte word at contraction position c that lie in [klo, kend),
+// as a byte mask (0xFF per byte inside).
+__device__ __forceinline__ uint32_t bytes_below(int n) {
+  return n <= 0 ? 0u : (n >= 4 ? 0xFFFFFFFFu : (1u << (8 * n)) - 1u);
+}
+__device__ __forceinline__ uint32_t word_window(uint32_t c, uint32_t klo, uint32_t kend) {
+  return bytes_below((int)kend - (int)c) & ~bytes_below((int)klo - (int)c);
+}
+
+// Zero every fragment byte of k-step T of the stage starting at k0 whose
+// contraction index lies outside [klo, kend), in both operands (a zero on one
+// side alone would still turn a NaN code on the other into NaN).  Lane half h
+// holds chunk 4T+h in dwords 0..3 and chunk 4T+2+h in dwords 4..7 (FragAddr).
+template <int T>
+__device__ __forceinline__ void mask_frags(Frags& f, uint32_t k0, uint32_t klo, uint32_t kend) {
+  const uint32_t h = (threadIdx.x & 63u) >> 5;
+  const uint32_t clo = k0 + 16u * (4u * T + h), chi = clo + 32u;
+  uint32_t m[8];
+#pragma unroll
+  for (uint32_t d = 0; d < 4; ++d) {
+    m[d] = word_window(clo + 4u * d, klo, kend);
+    m[4 + d] = word_window(chi + 4u * d, klo, kend);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      f.a[i][d] &= (int)m[d];
+      f.b[i][d] &= (int)m[d];
+    }
+}
+
 #define MXGG_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 // Workgroup barrier after this wave's LDS reads have returned (no wait on
@@ -363,9 +398,14 @@ __device__ __forceinline__ void release_barrier() {
 // do not depend on whether scales are loaded: the scale loads of a stage come
 // after its data loads, and the publish wait keeps exactly the 16 newest
 // (data) loads in flight.
-template <bool SCALED>
+// MASK (unscaled only): [klo, kend) may have any bounds; chunks that straddle
+// them are loaded whole and the bytes outside are zeroed in registers before
+// they reach an MFMA.  Only experts whose token range is not a multiple of 16
+// take this path.
+template <bool SCALED, bool MASK = false>
 __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Operand& Q,
                                          uint32_t klo, uint32_t kend, v16f (&acc)[4][4]) {
+  static_assert(!(SCALED && MASK), "a scale block cannot be split by a token mask");
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -375,7 +415,7 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
   if (kend <= klo) return;
   const uint32_t kbeg = klo & ~(uint32_t)(kStageK - 1);
   const uint32_t nst = (kend - kbeg + kStageK - 1) / kStageK;
-  Stream<SCALED> st;
+  Stream<SCALED, MASK> st;
   st.init(P, Q, klo, kend);
   FragAddr fa;
   fa.init();
@@ -400,6 +440,10 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
     uint8_t* nxt = sm.ring[(s & 1u) ^ 1u];
     uint32_t bp, bq;
     st.stage_base(kbeg + (s + 2) * kStageK, bp, bq);
+    if constexpr (MASK) {
+      mask_frags<0>(f0, kbeg + s * kStageK, klo, kend);
+      MXGG_FENCE();
+    }
     // MFMA 0-7: rows 0-1 of f0 while k-step 1 of stage s is read into f1
     mfma1<0, 0>(f0, acc); read_q<1>(cur, fa, f1, 0); MXGG_FENCE();
     mfma1<0, 1>(f0, acc); read_q<1>(cur, fa, f1, 1); MXGG_FENCE();
@@ -411,6 +455,10 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
     mfma1<1, 3>(f0, acc); read_p<1>(cur, fa, f1, 3); read_scales<SCALED, 1>(cur, fa, f1); MXGG_FENCE();
     release_barrier();
     MXGG_FENCE();
+    if constexpr (MASK) {
+      mask_frags<1>(f1, kbeg + s * kStageK, klo, kend);
+      MXGG_FENCE();
+    }
     // MFMA 8-31: the 18 loads of stage s+2, three on every four MFMAs
     mfma1<2, 0>(f0, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
     mfma1<2, 1>(f0, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
@@ -621,14 +669,11 @@ __device__ void scan_counts(Smem& sm, const int32_t* tiles_of, int32_t* out, int
   __syncthreads();
 }
 
-__device__ __forceinline__ void group_range(const int32_t* ends, int g, int32_t limit,
-                                            int32_t& beg, int32_t& end) {
-  int32_t e = ends[g];
-  int32_t b = g > 0 ? ends[g - 1] : 0;
-  e = e < 0 ? 0 : (e > limit ? limit : e);
-  b = b < 0 ? 0 : (b > limit ? limit : b);
-  beg = b;
-  end = e > b ? e : b;
+// Rows [beg, end) of group g from the monotone group ends staged in LDS.
+__device__ __forceinline__ void group_range(const int32_t* gend, int g, int32_t& beg,
+                                            int32_t& end) {
+  beg = g > 0 ? gend[g - 1] : 0;
+  end = gend[g];
 }
 
 // ---------------------------------------------------------------------------
@@ -642,9 +687,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
   __shared__ Smem sm;
   const int E = args.group_ends ? args.E : 1;
   const int32_t M = args.M;
+  if (args.group_ends)
+    monotone_ends_to_lds(args.group_ends, E, M, sm.gend);
+  else if (threadIdx.x == 0)
+    sm.gend[0] = M;
+  __syncthreads();
   for (int g = threadIdx.x; g < E; g += kThreads) {
-    int32_t b = 0, e = M;
-    if (args.group_ends) group_range(args.group_ends, g, M, b, e);
+    int32_t b, e;
+    group_range(sm.gend, g, b, e);
     sm.order[g] = e > b ? (e - (b & ~3) + kTileQ - 1) / kTileQ : 0;
   }
   __syncthreads();
@@ -691,8 +741,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
       if ((uint32_t)sm.sched[mid] <= mt) lo = mid; else hi = mid - 1;
     }
     const int g = lo;
-    int32_t gb = 0, ge = M;
-    if (args.group_ends) group_range(args.group_ends, g, M, gb, ge);
+    int32_t gb, ge;
+    group_range(sm.gend, g, gb, ge);
     const uint32_t q0 = (uint32_t)(gb & ~3) + (mt - (uint32_t)sm.sched[g]) * kTileQ;
     const uint32_t p0 = nt * kTileP;
 
@@ -816,9 +866,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
   const int32_t M = args.M;
   const int32_t split = args.split;
   // sizes into sched[0..E-1], then rank experts by descending size (ties by index)
+  monotone_ends_to_lds(args.group_ends, E, M, sm.gend);
   for (int g = threadIdx.x; g < E; g += kThreads) {
     int32_t b, e;
-    group_range(args.group_ends, g, M, b, e);
+    group_range(sm.gend, g, b, e);
     sm.sched[g] = e - b;
   }
   __syncthreads();
@@ -876,7 +927,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
     uint32_t nt, kt;
     band_decode(local - chunk * per_expert, n_tiles, k_tiles, gm, nt, kt);
     int32_t tb, te;
-    group_range(args.group_ends, g, M, tb, te);
+    group_range(sm.gend, g, tb, te);
     int32_t cb = tb, ce = te;
     if (split > 0) {
       cb = tb + (int32_t)chunk * split;
@@ -899,7 +950,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
       Q.lds = (uint32_t)args.ldgos;
     }
     v16f acc[4][4];
-    if (((tb | te) & 31) != 0) {
+    if (SCALED && ((tb | te) & 31) != 0) {
       // A group boundary inside a 32-token block breaks the block/scale
       // pairing: the whole expert is written as NaN rather than a wrong value.
 #pragma unroll
@@ -908,6 +959,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_nanf("");
+    } else if (!SCALED && ((cb | ce) & 15) != 0) {
+      // unscaled, token range off the 16-byte load grid: masked to the token
+      mainloop<false, true>(sm, P, Q, (uint32_t)cb, (uint32_t)ce, acc);
     } else {
       mainloop<SCALED>(sm, P, Q, (uint32_t)cb, (uint32_t)ce, acc);
     }

@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mxgg_internal.h"
+
 namespace mxgg {
 
 enum { kModeRceil = 0, kModeFloor = 1 };
@@ -196,11 +198,8 @@ __device__ __forceinline__ void stage_group_tables(const int32_t* __restrict__ e
                                                    const int32_t* __restrict__ ends_pad, int E,
                                                    int64_t rows, int32_t* ends_s,
                                                    int32_t* pend_s) {
-  for (int g = threadIdx.x; g < E; g += blockDim.x) {
-    const int32_t e = ends[g];
-    ends_s[g] = e < 0 ? 0 : (e > rows ? (int32_t)rows : e);
-    pend_s[g] = ends_pad[g];
-  }
+  for (int g = threadIdx.x; g < E; g += blockDim.x) pend_s[g] = ends_pad[g];
+  monotone_ends_to_lds(ends, E, rows, ends_s);
 }
 
 // bf16(float(v_i) * sc) for the eight bf16 values of a 16-byte chunk (RNE).

@@ -19,6 +19,30 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // GPU tests can check the hardware convert against an independent encoder.
 constexpr int kCvtSoftwareFlag = 0x100;
 
+// Group ends as every kernel of the library reads them: m[g] = the running
+// maximum of ends[0..g], clamped to [0, rows]; group g covers rows
+// [m[g-1], m[g]) (m[-1] = 0).  Monotone input is used as given; a decreasing
+// entry makes its group empty instead of letting it overlap an earlier one, so
+// no row belongs to two groups and the group sizes sum to at most `rows`.
+// Called by every thread of the block; ends in the device array `ends`, the
+// result in LDS `m[E]`; ends with a barrier.
+__device__ __forceinline__ void monotone_ends_to_lds(const int32_t* __restrict__ ends, int E,
+                                                     int64_t rows, int32_t* m) {
+  for (int g = threadIdx.x; g < E; g += blockDim.x) {
+    const int32_t e = ends[g];
+    m[g] = e < 0 ? 0 : (e > rows ? (int32_t)rows : e);
+  }
+  __syncthreads();
+  int bad = 0;
+  for (int g = threadIdx.x + 1; g < E; g += blockDim.x) bad |= m[g] < m[g - 1];
+  // Well-formed ends (the usual case) cost one vote; others a serial pass.
+  if (__syncthreads_or(bad)) {
+    if (threadIdx.x == 0)
+      for (int g = 1; g < E; ++g) m[g] = m[g] > m[g - 1] ? m[g] : m[g - 1];
+    __syncthreads();
+  }
+}
+
 // Error reporting (capi.hip).
 int set_error(int status, const char* fmt, ...);
 
@@ -80,6 +104,12 @@ hipError_t launch_combine_score_grad(const uint16_t* dout, int64_t ldd, const ui
                                      int64_t ldy, int64_t yrows, const int32_t* perm,
                                      int64_t tokens, int topk, int64_t cols, float* dscore,
                                      hipStream_t stream);
+
+// Group-offset utilities (groups.hip).
+hipError_t launch_offs_to_ends(const int32_t* offs, int64_t E, int64_t tokens, int kind,
+                               int32_t* ends, hipStream_t stream);
+hipError_t launch_zero_tail(uint8_t* out, int64_t rows, int64_t row_bytes, int64_t ld_bytes,
+                            const int32_t* ends, int64_t E, hipStream_t stream);
 
 // Padded cumulative group ends of the token-axis casts (one workgroup).
 hipError_t launch_pad_ends(const int32_t* group_ends, int64_t num_groups, int64_t rows,

@@ -101,12 +101,13 @@ __global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__
 
 // ---------------------------------------------------------------------------
 // Block-wide prefix over group sizes, kept in LDS.
-//   ends_s[g]  : clamped end of group g (unpadded)
+//   ends_s[g]  : end of group g (unpadded; running maximum of the clamped ends)
 //   pend_s[g]  : padded cumulative end (each group rounded up to 32 tokens)
 // ---------------------------------------------------------------------------
 __device__ void groups_to_lds(const int32_t* __restrict__ ends, int E, int64_t rows,
                               int32_t* ends_s, int32_t* pend_s, int32_t* tmp /*256*/) {
   const int t = threadIdx.x;
+  monotone_ends_to_lds(ends, E, rows, ends_s);
   // Each thread owns up to 4 consecutive groups.
   int32_t local_pad[4];
   int32_t sum = 0;
@@ -116,13 +117,8 @@ __device__ void groups_to_lds(const int32_t* __restrict__ ends, int E, int64_t r
     const int g = g0 + u;
     int32_t pad = 0;
     if (g < E) {
-      int64_t e = ends[g];
-      int64_t st = g > 0 ? (int64_t)ends[g - 1] : 0;
-      e = e < 0 ? 0 : (e > rows ? rows : e);
-      st = st < 0 ? 0 : (st > rows ? rows : st);
-      const int64_t sz = e > st ? e - st : 0;
-      ends_s[g] = (int32_t)e;
-      pad = (int32_t)((sz + 31) & ~(int64_t)31);
+      const int32_t sz = ends_s[g] - (g > 0 ? ends_s[g - 1] : 0);
+      pad = (sz + 31) & ~31;
     }
     local_pad[u] = pad;
     sum += pad;
@@ -147,7 +143,7 @@ __device__ void groups_to_lds(const int32_t* __restrict__ ends, int E, int64_t r
 
 // ---------------------------------------------------------------------------
 // Padded group ends for dim1 (one workgroup): ends_pad[g] = sum over groups
-// <= g of round_up(size, 32), sizes taken from the clamped ends.
+// <= g of round_up(size, 32), sizes taken from the monotone clamped ends.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_pad_ends(const int32_t* __restrict__ ends, int E,
                                                   int64_t rows, int32_t* __restrict__ ends_pad) {

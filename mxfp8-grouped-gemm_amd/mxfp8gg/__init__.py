@@ -15,6 +15,7 @@ from .ops import (
     grouped_dgrad,
     grouped_mm,
     grouped_wgrad,
+    offs_to_group_ends,
     padded_token_capacity,
     quant_weight_dual,
     quant_weight_for_dgrad,
@@ -26,6 +27,7 @@ from .ops import (
     wgrad_fused,
     wgrad_kernel,
     wgrad_prepare,
+    zero_rows_past_groups,
 )
 from .weight_cache import WeightCastCache
 from .autograd import (
@@ -61,6 +63,7 @@ __all__ = [
     "grouped_mm", "grouped_wgrad", "grouped_dgrad", "quant_weight_for_dgrad",
     "quant_weight_dual", "swiglu_quant", "swiglu_backward_quant",
     "fused_grouped_fwd", "fwd_ge", "wgrad_fused", "wgrad_prepare", "wgrad_kernel",
+    "offs_to_group_ends", "zero_rows_past_groups",
     "triton_to_mxfp8_dim0", "triton_to_mxfp8_dim1",
     "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",
     "WeightCastCache",

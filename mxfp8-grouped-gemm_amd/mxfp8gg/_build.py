@@ -17,7 +17,7 @@ INCLUDE_DIR = PKG_DIR.parent.parent / "include"
 BUILD_DIR = PKG_DIR.parent / "_build"
 LIB_PATH = PKG_DIR / "libmxgg.so"
 
-SOURCES = ["capi.hip", "quant.hip", "swiglu.hip", "route.hip", "gemm.hip"]
+SOURCES = ["capi.hip", "quant.hip", "swiglu.hip", "route.hip", "groups.hip", "gemm.hip"]
 HEADERS = ["mxgg_internal.h", "mx_device.h"]
 
 ARCH = os.environ.get("MXGG_OFFLOAD_ARCH", "gfx950")

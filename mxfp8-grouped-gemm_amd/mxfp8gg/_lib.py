@@ -31,7 +31,11 @@ OUT_F32 = 1
 SCALES_ROW_MAJOR = 0
 SCALES_BLOCK_MAJOR = 1
 
-ABI_VERSION = 9
+OFFS_ENDS = 0
+OFFS_SIZES = 1
+OFFS_AUTO = 2
+
+ABI_VERSION = 10
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -63,6 +67,8 @@ SIGNATURES = {
     "mxgg_scales_to_block_major": (
         _I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P],
     ),
+    "mxgg_offs_to_group_ends": (_I, [_P, _I64, _I64, _I, _P, _P]),
+    "mxgg_zero_rows_past_groups": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P]),
     "mxgg_grouped_fwd": (
         _I,
         [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,

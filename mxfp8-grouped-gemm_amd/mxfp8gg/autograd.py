@@ -51,7 +51,8 @@ class MXFP8GroupedMM(torch.autograd.Function):
             saved += [wt, wts]
         else:
             wq, ws = ops.to_mxfp8_dim0(w, scaling_mode)
-        y = ops.grouped_mm(xq, wq, offs, xs, ws, out_dtype=torch.bfloat16)
+        y = ops.zero_rows_past_groups(ops.grouped_mm(xq, wq, offs, xs, ws, out_dtype=torch.bfloat16),
+                                      offs)
         ctx.save_for_backward(*saved)
         ctx.scaling_mode = scaling_mode
         ctx.w_dtype = w.dtype
@@ -79,7 +80,8 @@ class MXFP8GroupedMM(torch.autograd.Function):
         elif need_dw:
             dyqt, dyst, _ = ops.to_mxfp8_dim1(dy, offs, mode)
         if need_dx:
-            dx = ops.grouped_mm(dyq, wt, offs, dys, wts, out_dtype=torch.bfloat16)
+            dx = ops.zero_rows_past_groups(
+                ops.grouped_mm(dyq, wt, offs, dys, wts, out_dtype=torch.bfloat16), offs)
         if need_dw:
             dw = ops.grouped_wgrad(dyqt, xqt, pad, dyst, xst, out_dtype=ctx.w_dtype)
         return dx, dw, None, None, None
@@ -89,9 +91,9 @@ def mxfp8_grouped_mm(x: torch.Tensor, w: torch.Tensor, offs: torch.Tensor,
                      scaling_mode: str = "rceil", weight_cache=None) -> torch.Tensor:
     """Differentiable MXFP8 grouped GEMM: x bf16 [M, K], w bf16 [E, N, K],
     offs int32 group ends [E] (or [E+1] with a leading 0) -> bf16 [M, N].
-    Rows after the last group end are left unwritten, as in the forward op.
-    weight_cache: an optional WeightCastCache reusing w's casts while w is
-    unchanged."""
+    Rows after the last group end get zeros, in the output and in x's
+    gradient (the raw op grouped_mm leaves them untouched).  weight_cache: an
+    optional WeightCastCache reusing w's casts while w is unchanged."""
     return MXFP8GroupedMM.apply(x, w, offs, scaling_mode, weight_cache)
 
 
@@ -118,7 +120,8 @@ class MXFP8ExpertFFN(torch.autograd.Function):
         h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
         aq, as_ = ops.swiglu_quant(h, scaling_mode)
         (dq, ds), (wdt, wdts) = wcast(w_down, scaling_mode)
-        y = ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16)
+        y = ops.zero_rows_past_groups(ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16),
+                                      ends)
         ctx.save_for_backward(ends, h, xqt, xst, wgt, wgts, wdt, wdts)
         ctx.scaling_mode = scaling_mode
         ctx.dtypes = (w_gate_up.dtype, w_down.dtype)
@@ -139,7 +142,9 @@ class MXFP8ExpertFFN(torch.autograd.Function):
         if ctx.needs_input_grad[2]:
             dwd = ops.grouped_wgrad(dyqt, act["a_qt"], pad, dyst, act["a_st"], out_dtype=ctx.dtypes[1])
         if ctx.needs_input_grad[0]:
-            dx = ops.grouped_mm(act["dh_q"], wgt, ends, act["dh_s"], wgts, out_dtype=torch.bfloat16)
+            dx = ops.zero_rows_past_groups(
+                ops.grouped_mm(act["dh_q"], wgt, ends, act["dh_s"], wgts, out_dtype=torch.bfloat16),
+                ends)
         if ctx.needs_input_grad[1]:
             dwgu = ops.grouped_wgrad(act["dh_qt"], xqt, pad, act["dh_st"], xst,
                                      out_dtype=ctx.dtypes[0])
@@ -169,7 +174,8 @@ def _ffn_forward_only(x, w_gate_up, w_down, offs, scaling_mode, weight_cache=Non
     h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
     aq, as_ = ops.swiglu_quant(h, scaling_mode)
     dq, ds = _weight_dim0(w_down, scaling_mode, weight_cache)
-    return ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16)
+    y = ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16)
+    return ops.zero_rows_past_groups(y, ends) if ends is not None else y
 
 
 def moe_ffn(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,
@@ -178,8 +184,8 @@ def moe_ffn(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor,
     the reference's e2e_bench.py:56-134): gate+up projection with the fused
     weight w_gate_up [E, 2F, H] (gate rows first), SiLU(gate) * up, down
     projection w_down [E, H, F].  x: bf16 [M, H], tokens grouped by expert with
-    cumulative ends `offs`.  Rows after the last group end get no output and no
-    input gradient.  weight_cache: an optional WeightCastCache reusing the
+    cumulative ends `offs`.  Rows after the last group end get zero output and
+    zero input gradient.  weight_cache: an optional WeightCastCache reusing the
     weights' casts while they are unchanged (micro-batches between optimizer
     steps, evaluation)."""
     if not torch.is_grad_enabled() or not any(

@@ -89,6 +89,56 @@ def _group_ends(offs: torch.Tensor, num_groups: int, device) -> torch.Tensor:
     return offs.contiguous()
 
 
+def _mark_ends(t):
+    """Tag a tensor this library wrote as cumulative group ends (the padded
+    ends of the token-axis casts, routing plans), so the reference-named wgrad
+    entry points never read it as group sizes."""
+    if t is not None:
+        t._mxgg_group_ends = True
+    return t
+
+
+_OFFS_KINDS = {"ends": _lib.OFFS_ENDS, "sizes": _lib.OFFS_SIZES, "auto": _lib.OFFS_AUTO}
+
+
+def offs_to_group_ends(offs: torch.Tensor, tokens: int, offs_kind: str = "auto") -> torch.Tensor:
+    """Cumulative group ends (int32 [E], on the device) from an `offs` vector
+    given as cumulative ends ("ends"), per-group sizes ("sizes"), or either
+    ("auto": sizes when they add up to exactly `tokens` and the last entry is
+    below `tokens`, ends otherwise), decided on the device by one small kernel
+    (mxgg_offs_to_group_ends), with no host sync.  Tensors this library
+    returned as group ends (the padded ends of its token-axis casts, routing
+    plans) are always read as ends."""
+    if offs_kind not in _OFFS_KINDS:
+        raise ValueError(f"offs_kind must be one of {sorted(_OFFS_KINDS)}, got {offs_kind!r}")
+    if getattr(offs, "_mxgg_group_ends", False):
+        offs_kind = "ends"
+    if not isinstance(offs, torch.Tensor) or offs.dim() != 1:
+        raise ValueError("offs must be a 1-D tensor")
+    _need_gpu(offs, "offs")
+    src = offs.to(torch.int32).contiguous()
+    out = torch.empty_like(src)
+    _lib.check(_lib.load().mxgg_offs_to_group_ends(src.data_ptr(), src.numel(), int(tokens),
+                                                   _OFFS_KINDS[offs_kind], out.data_ptr(),
+                                                   _stream_ptr(src)), "offs_to_group_ends")
+    return _mark_ends(out)
+
+
+def zero_rows_past_groups(out: torch.Tensor, offs: torch.Tensor) -> torch.Tensor:
+    """Set the rows of a row-major 2-D `out` past the last group end to zero
+    (the rows no grouped GEMM writes), reading the ends on the device."""
+    _need_gpu(out, "out")
+    if out.dim() != 2 or out.stride(-1) != 1:
+        raise ValueError("out must be a row-major 2-D tensor")
+    E = offs.numel()
+    ends = _group_ends(offs, E, out.device)
+    esz = out.element_size()
+    _lib.check(_lib.load().mxgg_zero_rows_past_groups(
+        out.data_ptr(), out.shape[0], out.shape[1] * esz, out.stride(0) * esz, ends.data_ptr(),
+        E, _stream_ptr(out)), "zero_rows_past_groups")
+    return out
+
+
 def _ld16(n: int) -> int:
     return max(16, (n + 15) // 16 * 16)
 
@@ -245,7 +295,7 @@ def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mod
         "quant_dim1",
     )
     st = buf[:, :C].t()  # logical [C, cap/32], block-major storage
-    return qt, st, ends_pad
+    return qt, st, _mark_ends(ends_pad)
 
 
 def to_mxfp8_dual(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mode="rceil"):
@@ -283,7 +333,7 @@ def to_mxfp8_dual(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mod
             _mode(scaling_mode), _stream_ptr(x)),
         "quant_dual",
     )
-    return q, sbuf[:, :M].t(), qt, stbuf[:, :C].t(), ends_pad
+    return q, sbuf[:, :M].t(), qt, stbuf[:, :C].t(), _mark_ends(ends_pad)
 
 
 def _expert_ends(E: int, N: int, device) -> torch.Tensor:
@@ -404,7 +454,7 @@ def swiglu_backward_quant(h: torch.Tensor, grad_a: torch.Tensor, offs: torch.Ten
         "dh_q": dh_q, "dh_s": dh_sb[:, :M].t(),
         "dh_qt": dh_qt, "dh_st": dh_stb[:, :2 * f].t(),
         "a_qt": a_qt, "a_st": a_stb[:, :f].t(),
-        "offs_pad": ends_pad,
+        "offs_pad": _mark_ends(ends_pad),
     }
     if return_bf16:
         out["dh"] = dh
@@ -602,7 +652,9 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
     go: e4m3 [N, M] (dY transposed, token-contiguous); ia: e4m3 [K, M]
     (X transposed); offs: int32 [E] cumulative token ends; scales: E8M0
     [N, M/32] / [K, M/32] along tokens, both or neither.  With scales every
-    group end must be a multiple of 32 (the layout to_mxfp8_dim1 produces).
+    group end must be a multiple of 32 (the layout to_mxfp8_dim1 produces): an
+    expert whose bounds are not is written as NaN, since a scale block would
+    span two experts.  Without scales the ends may be any token index.
     Empty groups yield zeros.
     split_tokens: split-K chunk in tokens (multiple of 128), 0 for none, None
     to choose from the shapes (wgrad_split_tokens).  A split call writes the
@@ -675,34 +727,60 @@ def _split_kw(kwargs):
     return out_dtype
 
 
-def wgrad_fused(go, ia, offs, go_scales=None, ia_scales=None, **kwargs):
+def _wgrad_offs(offs, tokens: int, offs_kind: str, device):
+    if not isinstance(offs, torch.Tensor):
+        offs = torch.as_tensor(offs, dtype=torch.int32)
+    if offs.dim() != 1 or offs.numel() < 1:
+        raise ValueError(f"offs must be a non-empty 1-D tensor, got shape {tuple(offs.shape)}")
+    if offs.device != device:
+        marked = getattr(offs, "_mxgg_group_ends", False)
+        offs = offs.to(device, non_blocking=True)
+        if marked:
+            _mark_ends(offs)
+    return offs_to_group_ends(offs, tokens, offs_kind)
+
+
+def wgrad_fused(go, ia, offs, go_scales=None, ia_scales=None, *, offs_kind="auto", **kwargs):
     """Drop-in for wgrad_fused.wgrad_fused (wgrad_fused.py:34-71).
 
-    go (N, M) e4m3, ia (K, M) e4m3, offs (E,) int32 cumulative token ends,
-    optional E8M0 scales (N, M/32) and (K, M/32).  No restacking: the kernel
-    contracts each group's token range in place.  Returns (E, N, K), bf16 by
-    default like the reference; pass out_dtype=torch.float32 for fp32 grads.
-    Scales are used only when both are given, as in the reference.
+    go (N, M) e4m3, ia (K, M) e4m3, offs (E,) int32, optional E8M0 scales
+    (N, M/32) and (K, M/32).  The reference documents offs as group sizes
+    (wgrad_fused.py:37; bench_wgrad_dsv3.py:52 passes [M/E] * E) while its
+    layer step passes cumulative ends (e2e_bench.py:42,117); it reads neither
+    and splits M // E tokens per expert.  Here the groups are honoured: with
+    offs_kind="auto" (default) offs is read as sizes when its entries add up
+    to exactly M and its last entry is below M, as cumulative ends otherwise;
+    "sizes" / "ends" force one reading (offs_to_group_ends).  Group ends from
+    this library's token-axis casts are always read as ends.  No restacking:
+    the kernel contracts each group's token range in place.  Returns
+    (E, N, K), bf16 by default like the reference; pass
+    out_dtype=torch.float32 for fp32 grads.  Scales are used only when both
+    are given, as in the reference.
     """
     out_dtype = _split_kw(dict(kwargs))
+    _need_gpu(go, "go")
     use_scales = go_scales is not None and ia_scales is not None
-    return grouped_wgrad(go, ia, offs, go_scales if use_scales else None,
+    ends = _wgrad_offs(offs, go.shape[1], offs_kind, go.device)
+    return grouped_wgrad(go, ia, ends, go_scales if use_scales else None,
                          ia_scales if use_scales else None, out_dtype=out_dtype)
 
 
-def wgrad_prepare(go, ia, offs, go_scales=None, ia_scales=None):
+def wgrad_prepare(go, ia, offs, go_scales=None, ia_scales=None, *, offs_kind="auto"):
     """Drop-in for wgrad_fused.wgrad_prepare (wgrad_fused.py:74-103).
 
     The reference restacks per group here; this kernel needs no restacking,
     so the dict references the caller's tensors (same keys as the reference).
+    "offs" holds the cumulative group ends read from `offs` as wgrad_fused
+    reads it (sizes or ends, see there).
     """
+    _need_gpu(go, "go")
     N, M = go.shape
     K = ia.shape[0]
     E = offs.shape[0]
     use_scales = go_scales is not None and ia_scales is not None
     return {
         "A": go, "B": ia,
-        "offs": _group_ends(offs, E, go.device),
+        "offs": _wgrad_offs(offs, M, offs_kind, go.device),
         "As": go_scales if use_scales else None, "Bs": ia_scales if use_scales else None,
         "E": E, "N": N, "K": K, "M": M,
         "flops": 2 * M * N * K,

@@ -24,7 +24,7 @@ from typing import NamedTuple
 
 import torch
 
-from . import _lib
+from . import _lib, ops
 from .ops import (_FP8, _block_major_buffer, _mode, _need_gpu, _stream_ptr,
                   padded_token_capacity)
 
@@ -81,7 +81,7 @@ def route_plan(expert_idx: torch.Tensor, num_experts: int, pad_multiple: int = 3
                             _stream_ptr(idx)),
         "route_plan",
     )
-    return RoutePlan(perm, src, offs, counts, T, K, num_experts, pad_multiple)
+    return RoutePlan(perm, src, ops._mark_ends(offs), counts, T, K, num_experts, pad_multiple)
 
 
 def _rows_ok(t: torch.Tensor) -> torch.Tensor:

@@ -172,14 +172,15 @@ void mxo_quant_dim1(const uint16_t* x, int64_t rows, int64_t cols, const int32_t
   uint8_t out[32];
   const int64_t groups = ends ? E : 1;
   int64_t pcol = 0;
+  int64_t m_prev = 0; /* running maximum of the clamped ends */
   memset(qt, 0, (size_t)(cols * cap));
   for (int64_t g = 0; g < groups; ++g) {
-    /* group g = [clamp(ends[g-1]), clamp(ends[g])), clamped to [0, rows] */
-    int64_t beg = (ends && g > 0) ? ends[g - 1] : 0;
+    /* group g = [m[g-1], m[g]), m[g] = max(m[g-1], clamp(ends[g], 0, rows)) */
+    const int64_t beg = m_prev;
     int64_t end = ends ? ends[g] : rows;
-    beg = beg < 0 ? 0 : (beg > rows ? rows : beg);
     end = end < 0 ? 0 : (end > rows ? rows : end);
     if (end < beg) end = beg;
+    m_prev = end;
     const int64_t size = end - beg;
     const int64_t nblk = (size + 31) / 32;
     for (int64_t c = 0; c < cols; ++c)

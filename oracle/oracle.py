@@ -150,14 +150,16 @@ def dequant(q: np.ndarray, s: np.ndarray | None) -> np.ndarray:
 
 
 def group_bounds(ends, rows: int):
-    """[(beg, end)] per group, clamped like the kernels: beg = ends[g-1]."""
+    """[(beg, end)] per group under the library's documented rule for group
+    ends: m[g] = the running maximum of ends[0..g] clamped to [0, rows], group
+    g = [m[g-1], m[g]) with m[-1] = 0 (well-formed non-decreasing ends are used
+    as given; a decreasing entry gives an empty group)."""
     out = []
-    prev = 0
+    m_prev = 0
     for e in np.asarray(ends).tolist():
-        b = min(max(prev, 0), rows)
-        en = min(max(e, 0), rows)
-        out.append((b, max(en, b)))
-        prev = e
+        m = min(max(m_prev, e, 0), rows)
+        out.append((m_prev, m))
+        m_prev = m
     return out
 
 

@@ -176,3 +176,13 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_offs_helpers_reject_cpu_tensors():
+    t = torch.tensor([4, 4], dtype=torch.int32)
+    with pytest.raises(ValueError, match="ROCm GPU only"):
+        mxfp8gg.offs_to_group_ends(t, 8)
+    with pytest.raises(ValueError, match="offs_kind"):
+        mxfp8gg.offs_to_group_ends(t, 8, "cumulative")
+    with pytest.raises(ValueError, match="ROCm GPU only"):
+        mxfp8gg.zero_rows_past_groups(torch.zeros(4, 8), t)

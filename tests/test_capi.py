@@ -494,3 +494,42 @@ def test_combine_score_grad_rejects(lib, kw, status):
     a.update(kw)
     assert lib.mxgg_combine_score_grad(a["d"], a["ldd"], a["y"], a["rows"], a["cols"], a["ldy"],
                                        a["perm"], a["T"], a["K"], a["grad"], None) == status
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(kind=3), _lib.ERR_INVALID_ARGUMENT),
+    (dict(kind=-1), _lib.ERR_INVALID_ARGUMENT),
+    (dict(E=0), _lib.ERR_UNSUPPORTED),
+    (dict(E=1025), _lib.ERR_UNSUPPORTED),
+    (dict(tokens=-1), _lib.ERR_SHAPE),
+    (dict(offs=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ends=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ends=FAKE), _lib.ERR_INVALID_ARGUMENT),      # aliases offs
+])
+def test_offs_to_group_ends_rejects(lib, kw, status):
+    a = dict(offs=FAKE, E=4, tokens=256, kind=_lib.OFFS_AUTO, ends=FAKE + 64)
+    a.update(kw)
+    assert lib.mxgg_offs_to_group_ends(a["offs"], a["E"], a["tokens"], a["kind"], a["ends"],
+                                       None) == status
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(rows=-1), _lib.ERR_SHAPE),
+    (dict(ld=16), _lib.ERR_SHAPE),                     # stride below the row
+    (dict(E=0), _lib.ERR_UNSUPPORTED),
+    (dict(out=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ends=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(out=FAKE + 8), _lib.ERR_ALIGNMENT),
+    (dict(row_bytes=40, ld=48), _lib.ERR_ALIGNMENT),
+    (dict(rows=1 << 31), _lib.ERR_UNSUPPORTED),
+])
+def test_zero_rows_past_groups_rejects(lib, kw, status):
+    a = dict(out=FAKE, rows=64, row_bytes=64, ld=64, ends=FAKE, E=2)
+    a.update(kw)
+    assert lib.mxgg_zero_rows_past_groups(a["out"], a["rows"], a["row_bytes"], a["ld"],
+                                          a["ends"], a["E"], None) == status
+
+
+def test_zero_rows_past_groups_empty_is_noop(lib):
+    assert lib.mxgg_zero_rows_past_groups(None, 0, 64, 64, None, 1, None) == _lib.OK
+    assert lib.mxgg_zero_rows_past_groups(None, 8, 0, 0, None, 1, None) == _lib.OK

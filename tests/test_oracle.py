@@ -196,6 +196,44 @@ def test_dim1_equals_transposed_dim0_per_group(mode):
 
 
 # ---------------------------------------------------------------------------
+# group ends: the running-maximum rule for malformed (decreasing / out of
+# range) ends, stated independently with numpy
+# ---------------------------------------------------------------------------
+def _bounds_numpy(ends, rows):
+    m = np.clip(np.maximum.accumulate(np.asarray(ends, dtype=np.int64)), 0, rows)
+    return list(zip(np.r_[0, m[:-1]].tolist(), m.tolist()))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_group_bounds_running_max_rule(seed):
+    rng = np.random.default_rng(seed)
+    rows = int(rng.integers(1, 500))
+    ends = rng.integers(-50, rows + 80, int(rng.integers(1, 12)))
+    b = O.group_bounds(ends, rows)
+    assert b == _bounds_numpy(ends, rows)
+    # disjoint, contiguous from row 0, sizes sum to at most rows
+    assert b[0][0] == 0 and all(b[i][1] == b[i + 1][0] for i in range(len(b) - 1))
+    assert all(t >= s for s, t in b) and sum(t - s for s, t in b) <= rows
+    # well-formed cumulative ends are used as given
+    ok = np.sort(rng.integers(0, rows + 1, 5))
+    assert O.group_bounds(ok, rows) == list(zip(np.r_[0, ok[:-1]].tolist(), ok.tolist()))
+
+
+@pytest.mark.parametrize("ends", [[30, 10, 50], [80, 0, 80, 0], [-3, 20, 5, 200]])
+def test_dim1_decreasing_ends_equal_their_running_max(ends):
+    g = torch.Generator().manual_seed(7)
+    M = 80
+    x = _bf16_bits(torch.randn(M, 8, generator=g).to(torch.bfloat16))
+    e = np.array(ends, dtype=np.int32)
+    mono = np.clip(np.maximum.accumulate(e), 0, M).astype(np.int32)
+    cap = (M + 31 * len(ends) + 31) // 32 * 32
+    a = O.quant_dim1(x, e, cap)
+    b = O.quant_dim1(x, mono, cap)
+    for u, v in zip(a, b):
+        assert np.array_equal(u, v)
+
+
+# ---------------------------------------------------------------------------
 # GEMM references
 # ---------------------------------------------------------------------------
 def _kat(name):
