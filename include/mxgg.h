@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 10
+#define MXGG_ABI_VERSION 11
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -290,6 +290,29 @@ int mxgg_grouped_fwd_split(const void* a, int64_t lda, const void* a_scales, int
                            int64_t M, int64_t N, int64_t K,
                            void* out, int64_t ldo, int out_dtype,
                            void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * mxgg_grouped_fwd_split without a workspace argument and without any
+ * allocation: the split partials go to scratch memory the library holds per
+ * device (a static device array of 16 KB + 256 x 256 KB = 64 MiB + 16 KiB,
+ * reserved on every device the library runs on until the process ends).
+ * Same arguments, results and rules as mxgg_grouped_fwd_split; calls no
+ * hipMalloc / hipFree.  Returns MXGG_ERR_UNSUPPORTED on a device whose
+ * persistent grid needs more than 256 partials (more than 256 compute units).
+ * Every call on one device shares that scratch, which keeps the last call's
+ * contents: calls that overlap in time on one device (different streams, or
+ * graph replays running concurrently) race; calls ordered on one stream are
+ * safe.  Nothing in it needs to start at zero (each call writes its own header).
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).
+ */
+int mxgg_grouped_fwd_split_noalloc(const void* a, int64_t lda, const void* a_scales,
+                                   int64_t ldas, const void* w, int64_t w_group_stride,
+                                   int64_t ldw, const void* w_scales, int64_t ws_group_stride,
+                                   int64_t ldws, const int32_t* group_ends, int64_t num_groups,
+                                   int64_t M, int64_t N, int64_t K, void* out, int64_t ldo,
+                                   int out_dtype, void* stream);
 
 /*
  * Weight-gradient grouped GEMM, contracting over the ragged token dimension:

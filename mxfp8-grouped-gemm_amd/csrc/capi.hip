@@ -544,6 +544,26 @@ int mxgg_grouped_fwd_split(const void* a, int64_t lda, const void* a_scales, int
                      stream);
 }
 
+int mxgg_grouped_fwd_split_noalloc(const void* a, int64_t lda, const void* a_scales,
+                                   int64_t ldas, const void* w, int64_t w_group_stride,
+                                   int64_t ldw, const void* w_scales, int64_t ws_group_stride,
+                                   int64_t ldws, const int32_t* group_ends, int64_t num_groups,
+                                   int64_t M, int64_t N, int64_t K, void* out, int64_t ldo,
+                                   int out_dtype, void* stream) {
+  const int64_t need = fwd_split_workspace_bytes();
+  if (need > noalloc_scratch_bytes())
+    return set_error(MXGG_ERR_UNSUPPORTED,
+                     "grouped_fwd_split_noalloc: this device needs %lld bytes of split scratch, "
+                     "the library holds %lld (at most 256 compute units)",
+                     (long long)need, (long long)noalloc_scratch_bytes());
+  void* ws = noalloc_scratch();
+  if (ws == nullptr)
+    return set_error(MXGG_ERR_DEVICE,
+                     "grouped_fwd_split_noalloc: no device address for the library scratch");
+  return grouped_fwd(a, lda, a_scales, ldas, w, w_group_stride, ldw, w_scales, ws_group_stride,
+                     ldws, group_ends, num_groups, M, N, K, out, ldo, out_dtype, ws, stream);
+}
+
 static int grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, int64_t ldgos,
                          const void* ia_t, int64_t ldia, const void* ia_scales_t, int64_t ldias,
                          const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t N,

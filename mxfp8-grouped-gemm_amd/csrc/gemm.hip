@@ -31,6 +31,8 @@
 // Persistent grid (one workgroup per CU), tiles dealt round-robin with each XCD
 // taking a contiguous slice of every round.
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "mxgg_internal.h"
 
@@ -1066,6 +1068,32 @@ int64_t wgrad_split_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t E, 
 
 int64_t fwd_split_workspace_bytes() {
   return kSplitHdrBytes + (int64_t)persistent_grid() * kPartialBytes;
+}
+
+// Scratch of the allocation-free forward split (mxgg_grouped_fwd_split_noalloc):
+// the split header and one fp32 256x256 partial per workgroup of a persistent
+// grid of up to kNoallocUnits workgroups.  Every device holds its own copy
+// until the process ends.  In host code `scratch` only names the symbol: the
+// device address comes from hipGetSymbolAddress, once per device.
+constexpr int64_t kNoallocUnits = 256;
+constexpr int64_t kNoallocScratchBytes = kSplitHdrBytes + kNoallocUnits * kPartialBytes;
+static __device__ __align__(256) uint8_t scratch[kNoallocScratchBytes];
+
+int64_t noalloc_scratch_bytes() { return kNoallocScratchBytes; }
+
+void* noalloc_scratch() {
+  static std::mutex mu;
+  static std::vector<void*> ptrs;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((int)ptrs.size() <= dev) ptrs.resize(dev + 1, nullptr);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
 }
 
 hipError_t launch_grouped_fwd(const FwdArgs& a, hipStream_t stream) {

@@ -161,6 +161,10 @@ struct FwdArgs {
 };
 hipError_t launch_grouped_fwd(const FwdArgs& args, hipStream_t stream);
 int64_t fwd_split_workspace_bytes();
+// The library's own per-device scratch for the forward split (device address
+// of the current device's copy, nullptr if the symbol lookup fails) and its size.
+void* noalloc_scratch();
+int64_t noalloc_scratch_bytes();
 
 struct WgradArgs {
   const uint8_t* go;   // [N, M] token-contiguous

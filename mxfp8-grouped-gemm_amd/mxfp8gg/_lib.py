@@ -35,7 +35,7 @@ OFFS_ENDS = 0
 OFFS_SIZES = 1
 OFFS_AUTO = 2
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -79,6 +79,11 @@ SIGNATURES = {
         _I,
         [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
          _P, _I64, _I, _P, _I64, _P],
+    ),
+    "mxgg_grouped_fwd_split_noalloc": (
+        _I,
+        [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
+         _P, _I64, _I, _P],
     ),
     "mxgg_grouped_wgrad": (
         _I,
