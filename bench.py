@@ -14,7 +14,7 @@ reference's CPU path (dequantise + per-group fp32 matmul with torch on the
 host cores) on a bounded sample of C2.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                      [--only fwd|wgrad|copy|ref8|c5|routing]
+                      [--only fwd|wgrad|copy|ref8|refwgrad|c5|routing|dense|small|traffic]
 """
 import argparse
 import json
@@ -85,6 +85,66 @@ def ref_equal_shapes(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
             "reference_geomean_unscaled": REF_GEOMEAN_UNSCALED,
             "vs_reference_scaled": round(gs / REF_GEOMEAN_SCALED, 3),
             "vs_reference_unscaled": round(gu / REF_GEOMEAN_UNSCALED, 3)}
+
+
+# The reference's wgrad is published as a geometric mean over the 8 DSv3 shapes
+# of bench_wgrad_dsv3.py:10-19 (equal groups, no scales, bf16 dW): 1913 TFLOPS
+# (wgrad_fused.py:2) and 1839 TFLOPS (memory/2026-06-10.md:100).
+REF_WGRAD_SHAPES = [  # (name, E, N, K, M) as in bench_wgrad_dsv3.py:10-19
+    ("gate_up", 4, 2048, 7168, 32768), ("down", 4, 7168, 2048, 32768),
+    ("gate_up", 4, 2048, 7168, 128000), ("down", 4, 7168, 2048, 128000),
+    ("gate_up", 8, 2048, 7168, 32768), ("down", 8, 7168, 2048, 32768),
+    ("gate_up", 8, 2048, 7168, 128000), ("down", 8, 7168, 2048, 128000),
+]
+REF_WGRAD_GEOMEANS = (1913.0, 1839.0)
+
+
+def ref_wgrad_shapes(torch, mxfp8gg, dev, steps=10, warmup=3):
+    """Weight gradient on the reference's own 8 wgrad shapes: operands cast as
+    bench_wgrad_dsv3.py:41-52 does (go = dY^T [N, M], ia = X^T [K, M], randn,
+    offs = [M/E] * E group sizes) and called through the reference-named
+    wgrad_prepare / wgrad_kernel; unscaled (the published configuration) and
+    with E8M0 scales (token-axis casts), bf16 dW (what wgrad_kernel returns)
+    and fp32 dW."""
+    import math
+    from mxfp8gg import ops
+    rows = []
+    gen = torch.Generator(device=dev).manual_seed(3)
+    for name, E, N, K, M in REF_WGRAD_SHAPES:
+        mg = M // E
+        dy = torch.randn((M, N), generator=gen, device=dev).to(torch.bfloat16)
+        x = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+        go8 = dy.t().contiguous().to(torch.float8_e4m3fn)
+        ia8 = x.t().contiguous().to(torch.float8_e4m3fn)
+        sizes = torch.full((E,), mg, dtype=torch.int32, device=dev)
+        data = mxfp8gg.wgrad_prepare(go8, ia8, sizes)
+        ends = torch.arange(1, E + 1, dtype=torch.int32, device=dev) * mg
+        go, gos, pad = mxfp8gg.to_mxfp8_dim1(dy, ends)
+        ia, ias, _ = mxfp8gg.to_mxfp8_dim1(x, ends)
+        del dy, x
+        fl = 2 * M * N * K
+        row = {"shape": name, "E": E, "N": N, "K": K, "M": M}
+        for dt, tag in ((torch.bfloat16, "bf16"), (torch.float32, "f32")):
+            out = torch.empty((E, N, K), dtype=dt, device=dev)
+            ms_u = time_launches(
+                lambda: ops.grouped_wgrad(data["A"], data["B"], data["offs"], out_dtype=dt,
+                                          out=out), steps, warmup, torch)
+            ms_s = time_launches(
+                lambda: ops.grouped_wgrad(go, ia, pad, gos, ias, out_dtype=dt, out=out),
+                steps, warmup, torch)
+            row[f"unscaled_{tag}_tflops"] = round(fl / ms_u / 1e9, 1)
+            row[f"scaled_{tag}_tflops"] = round(fl / ms_s / 1e9, 1)
+            del out
+        rows.append(row)
+        del go8, ia8, go, gos, ia, ias, data
+    res = {"shapes": rows}
+    for key in ("unscaled_bf16", "scaled_bf16", "unscaled_f32", "scaled_f32"):
+        res[f"geomean_{key}_tflops"] = round(
+            math.exp(sum(math.log(r[f"{key}_tflops"]) for r in rows) / len(rows)), 1)
+    res["reference_geomeans"] = list(REF_WGRAD_GEOMEANS)
+    res["vs_reference_unscaled_bf16"] = [round(res["geomean_unscaled_bf16_tflops"] / r, 3)
+                                         for r in REF_WGRAD_GEOMEANS]
+    return res
 
 
 def dense_c2_shape(torch, mxfp8gg, dev, steps=10, warmup=3):
@@ -301,6 +361,87 @@ def routing_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     return out
 
 
+GEMM_SOURCE = ROOT / "mxfp8-grouped-gemm_amd" / "csrc" / "gemm.hip"
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_grouped_fwd_c2.json"
+
+
+def _source_hash():
+    import hashlib
+    return hashlib.sha256(GEMM_SOURCE.read_bytes()).hexdigest()
+
+
+def _pmc_pass(only, counter, out_dir):
+    """One rocprofv3 counter pass over `bench.py --only <only>` in a child
+    process; returns {kernel name: (mean counter value per dispatch, dispatches)}."""
+    import csv
+    import shutil
+    import subprocess
+    shutil.rmtree(out_dir, ignore_errors=True)
+    cmd = ["timeout", "-s", "KILL", "90", "rocprofv3", "--pmc", counter, "--output-format", "csv",
+           "-d", str(out_dir), "-o", "p", "--", sys.executable, str(ROOT / "bench.py"),
+           "--only", only, "--steps", "3", "--warmup", "1", "--no-cpu"]
+    log("traffic pass: " + " ".join(cmd))
+    subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), check=False,
+                   stdout=subprocess.DEVNULL)
+    files = sorted(Path(out_dir).rglob("*counter_collection.csv"))
+    if not files:
+        raise RuntimeError(f"rocprofv3 wrote no counter file under {out_dir}")
+    tot, ids = {}, {}
+    for r in csv.DictReader(open(files[0])):
+        k = r["Kernel_Name"]
+        tot[k] = tot.get(k, 0.0) + float(r["Counter_Value"])
+        ids.setdefault(k, set()).add(r["Dispatch_Id"])
+    return {k: (tot[k] / len(ids[k]), len(ids[k])) for k in tot}
+
+
+def measure_traffic():
+    """HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes (KiB per dispatch), each scaled by what the same counter
+    reads for a 1 GiB device copy, written to profiles/ with the hash of the
+    kernel source it was measured on."""
+    base = ROOT / "gpurun_out" / "traffic"
+    res = {}
+    for only in ("fwd", "copy"):
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            res[(only, counter)] = _pmc_pass(only, counter, base / f"{only}_{counter}")
+    fwd = {c: next(v for k, v in res[("fwd", c)].items() if "k_grouped_fwd" in k)
+           for c in ("FETCH_SIZE", "WRITE_SIZE")}
+    cp = {c: max(res[("copy", c)].values()) for c in ("FETCH_SIZE", "WRITE_SIZE")}
+    nbytes = 1 << 30
+    ff = nbytes / (cp["FETCH_SIZE"][0] * 1024)
+    wf = nbytes / (cp["WRITE_SIZE"][0] * 1024)
+    rd = fwd["FETCH_SIZE"][0] * 1024 * ff
+    wr = fwd["WRITE_SIZE"][0] * 1024 * wf
+    out = {
+        "kernel": "k_grouped_fwd<true,false> on C2 (65536 tokens, 32 experts, K=7168, N=4096)",
+        "kernel_source": str(GEMM_SOURCE.relative_to(ROOT)),
+        "kernel_source_sha256": _source_hash(),
+        "hbm_bytes_per_launch": int(rd + wr),
+        "hbm_read_bytes": int(rd), "hbm_write_bytes": int(wr),
+        "fetch_size_kib_per_dispatch": fwd["FETCH_SIZE"][0],
+        "write_size_kib_per_dispatch": fwd["WRITE_SIZE"][0],
+        "calibration": {"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
+                        "copy_fetch_size_kib": cp["FETCH_SIZE"][0],
+                        "copy_write_size_kib": cp["WRITE_SIZE"][0],
+                        "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
+        "algorithmic_bytes_per_launch": 1990197248,
+        "command": "python3 bench.py --only traffic",
+    }
+    TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    return out
+
+
+def stored_traffic():
+    """The traffic figure of profiles/ when it was measured on the current
+    kernel source, else None (a changed kernel needs `bench.py --only traffic`)."""
+    if not TRAFFIC_FILE.exists():
+        return None, "no traffic measurement under profiles/"
+    t = json.loads(TRAFFIC_FILE.read_text())
+    if t.get("kernel_source_sha256") != _source_hash():
+        return None, "stale: kernel source changed since the measurement (bench.py --only traffic)"
+    return t.get("hbm_bytes_per_launch"), "rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated"
+
+
 def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, budget_s=12.0):
     """The reference's CPU path on a bounded sample of the workload: whole
     experts of C2, in order, until `budget_s` of CPU work has run."""
@@ -342,16 +483,22 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "c5", "routing",
-                                       "dense", "small"],
+    ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "refwgrad", "c5",
+                                       "routing", "dense", "small", "traffic"],
                     default="all",
                     help="fwd / wgrad: time only that GEMM (for profiler runs); copy: a plain "
                          "1 GiB device-to-device copy, the reference for HBM byte counters; "
-                         "ref8: the reference's 8 equal-group shapes only; c5: the full "
+                         "ref8: the reference's 8 equal-group shapes only; refwgrad: its 8 "
+                         "wgrad shapes only; c5: the full "
                          "expert-FFN layer step only; routing: C5 as a routed top-8 layer; "
                          "dense: C2's shape as one dense GEMM, with hipBLASLt beside it; "
-                         "small: launches with fewer tiles than compute units, split or not")
+                         "small: launches with fewer tiles than compute units, split or not; "
+                         "traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes of fwd and copy "
+                         "(child processes) -> profiles/traffic_grouped_fwd_c2.json")
     args = ap.parse_args()
+    if args.only == "traffic":   # no GPU use in this process: rocprofv3 runs children
+        print(json.dumps(measure_traffic()), flush=True)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the MXFP8 grouped GEMM shards by expert and "
               "this build runs a single GPU's expert share; --gpus must be 1", file=sys.stderr)
@@ -380,6 +527,9 @@ def main():
         return
     if args.only == "ref8":
         print(json.dumps(ref_equal_shapes(torch, mxfp8gg, workloads, dev)), flush=True)
+        return
+    if args.only == "refwgrad":
+        print(json.dumps(ref_wgrad_shapes(torch, mxfp8gg, dev)), flush=True)
         return
     if args.only == "copy":
         nbytes = 1 << 30
@@ -475,6 +625,8 @@ def main():
         del go, gos, ia, ias, dw
         log("reference's 8 equal-group shapes")
         components["ref_equal_shapes"] = ref_equal_shapes(torch, mxfp8gg, workloads, dev)
+        log("reference's 8 wgrad shapes")
+        components["ref_wgrad_shapes"] = ref_wgrad_shapes(torch, mxfp8gg, dev)
         log("C2's shape as one dense GEMM (kernel ceiling, vendor library beside it)")
         components["dense_c2_shape"] = dense_c2_shape(torch, mxfp8gg, dev)
         log("small launches split along K")
@@ -484,10 +636,7 @@ def main():
         log("C5 as a routed top-8 layer (dispatch, combine)")
         components["routing_c5"] = routing_c5(torch, mxfp8gg, workloads, dev)
 
-    traffic = None
-    tfile = ROOT / "profiles" / "traffic_grouped_fwd_c2.json"
-    if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    traffic, traffic_note = stored_traffic()
 
     cpu = None
     if not args.no_cpu and args.only == "all":
@@ -520,6 +669,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(tflops / PEAK_MXFP8_TFLOPS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_note,
             "kernel": "k_grouped_fwd<true,false> (one launch per step)",
         },
         "cpu_baseline": cpu,
