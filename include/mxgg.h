@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 11
+#define MXGG_ABI_VERSION 12
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -267,6 +267,29 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
                      const int32_t* group_ends, int64_t num_groups,
                      int64_t M, int64_t N, int64_t K,
                      void* out, int64_t ldo, int out_dtype, void* stream);
+
+/*
+ * Forward grouped GEMM of the gate+up projection fused with SwiGLU and the
+ * row-wise MXFP8 cast of its result, for the forward-only (inference) pass:
+ *   h[rows of g] = A[rows of g] . W[g]^T      (fp32 accumulate, rounded to bf16)
+ *   a = bf16(bf16(silu(h[:, :F])) * h[:, F:])  (as mxgg_swiglu_quant_dim0)
+ * and writes only the cast of a: payload q [M, F] e4m3 (row stride ldq) and
+ * E8M0 scales, logically [M, F/32], in `scale_layout` with stride lds.
+ *   w : [E, 2F, K] e4m3, gate rows 0..F-1 then up rows F..2F-1 of each expert
+ *       (the fused gate+up weight), with w_scales as for mxgg_grouped_fwd
+ * Every other argument as mxgg_grouped_fwd (N = 2F).  F % 128 == 0.  The
+ * result equals mxgg_grouped_fwd (bf16 out) followed by
+ * mxgg_swiglu_quant_dim0 on the rows inside the groups; rows past the last
+ * group end are not written.  bf16 h is never written to memory.
+ * Replaces the reference's forward layer step gate/up GEMMs, eager
+ * `silu(hg) * hu` and `.to(float8)` (e2e_bench.py:56-61).
+ */
+int mxgg_grouped_fwd_swiglu_quant(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                                  const void* w, int64_t w_group_stride, int64_t ldw,
+                                  const void* w_scales, int64_t ws_group_stride, int64_t ldws,
+                                  const int32_t* group_ends, int64_t num_groups, int64_t M,
+                                  int64_t F, int64_t K, void* q, int64_t ldq, void* scales,
+                                  int64_t lds, int scale_layout, int scale_mode, void* stream);
 
 /*
  * mxgg_grouped_fwd with a caller-owned workspace of at least

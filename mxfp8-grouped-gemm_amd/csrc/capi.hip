@@ -438,12 +438,22 @@ int mxgg_zero_rows_past_groups(void* out, int64_t rows, int64_t row_bytes, int64
                       "zero_rows_past_groups");
 }
 
+// Outputs of the fused SwiGLU forward (mxgg_grouped_fwd_swiglu_quant).
+struct SwigluOut {
+  void* q;
+  int64_t ldq;
+  void* scales;
+  int64_t lds;
+  int layout, mode;
+};
+
 static int grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
                        const void* w, int64_t w_group_stride, int64_t ldw, const void* w_scales,
                        int64_t ws_group_stride, int64_t ldws, const int32_t* group_ends,
                        int64_t num_groups, int64_t M, int64_t N, int64_t K, void* out,
-                       int64_t ldo, int out_dtype, void* workspace, void* stream) {
-  if (out_dtype != MXGG_OUT_BF16 && out_dtype != MXGG_OUT_F32)
+                       int64_t ldo, int out_dtype, void* workspace, void* stream,
+                       const SwigluOut* sw = nullptr) {
+  if (!sw && out_dtype != MXGG_OUT_BF16 && out_dtype != MXGG_OUT_F32)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd: unknown out_dtype %d", out_dtype);
   if (M < 0 || N < 0 || K < 0)
     return set_error(MXGG_ERR_SHAPE, "grouped_fwd: negative size");
@@ -459,8 +469,9 @@ static int grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t
     return set_error(MXGG_ERR_UNSUPPORTED, "grouped_fwd: num_groups=%lld outside [1, %lld]",
                      (long long)num_groups, (long long)kMaxGroupsAbi);
   if (M == 0 || N == 0) return MXGG_OK;
-  if (!a || !w || !out) return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd: null pointer");
-  if (lda < K || ldw < K || ldo < N || (scaled && (ldas < M || ldws < N)))
+  if (!a || !w || (!sw && !out))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd: null pointer");
+  if (lda < K || ldw < K || (!sw && ldo < N) || (scaled && (ldas < M || ldws < N)))
     return set_error(MXGG_ERR_SHAPE,
                      "grouped_fwd: leading dimension smaller than the row (block-major scales: "
                      "ldas >= M, ldws >= N)");
@@ -482,7 +493,7 @@ static int grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t
                      "grouped_fwd: a and w must be 16-byte aligned with lda, ldw and the expert "
                      "stride multiples of 16");
   const int esz = out_dtype == MXGG_OUT_F32 ? 4 : 2;
-  if ((reinterpret_cast<uintptr_t>(out) % (4 * esz)) != 0 || ldo % 4 != 0)
+  if (!sw && ((reinterpret_cast<uintptr_t>(out) % (4 * esz)) != 0 || ldo % 4 != 0))
     return set_error(MXGG_ERR_ALIGNMENT,
                      "grouped_fwd: out must be aligned to 4 elements with ldo % 4 == 0");
   if ((M - 1) * lda + K > kMaxBufferBytes || (N - 1) * ldw + K > kMaxBufferBytes)
@@ -512,6 +523,19 @@ static int grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t
   args.out_f32 = out_dtype == MXGG_OUT_F32;
   args.scaled = scaled;
   args.split_ws = static_cast<float*>(workspace);
+  args.swiglu_mode = -1;
+  args.aq = nullptr;
+  args.as_out = nullptr;
+  args.ldaq = args.as_row = args.as_blk = 0;
+  if (sw) {
+    const bool bm = sw->layout == MXGG_SCALES_BLOCK_MAJOR;
+    args.swiglu_mode = sw->mode;
+    args.aq = static_cast<uint8_t*>(sw->q);
+    args.as_out = static_cast<uint8_t*>(sw->scales);
+    args.ldaq = sw->ldq;
+    args.as_row = bm ? 1 : sw->lds;
+    args.as_blk = bm ? sw->lds : 1;
+  }
   return check_launch(launch_grouped_fwd(args, static_cast<hipStream_t>(stream)), "grouped_fwd");
 }
 
@@ -525,6 +549,41 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
 }
 
 int64_t mxgg_grouped_fwd_workspace_bytes(void) { return fwd_split_workspace_bytes(); }
+
+int mxgg_grouped_fwd_swiglu_quant(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                                  const void* w, int64_t w_group_stride, int64_t ldw,
+                                  const void* w_scales, int64_t ws_group_stride, int64_t ldws,
+                                  const int32_t* group_ends, int64_t num_groups, int64_t M,
+                                  int64_t F, int64_t K, void* q, int64_t ldq, void* scales,
+                                  int64_t lds, int scale_layout, int scale_mode, void* stream) {
+  if (scale_mode != MXGG_SCALE_RCEIL && scale_mode != MXGG_SCALE_FLOOR)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd_swiglu_quant: unknown scale_mode %d",
+                     scale_mode);
+  if (!valid_layout(scale_layout))
+    return set_error(MXGG_ERR_INVALID_ARGUMENT,
+                     "grouped_fwd_swiglu_quant: unknown scale_layout %d", scale_layout);
+  if (F < 0 || F % 128 != 0)
+    return set_error(MXGG_ERR_SHAPE,
+                     "grouped_fwd_swiglu_quant: F=%lld must be a non-negative multiple of 128",
+                     (long long)F);
+  if (F > (INT64_C(1) << 29))
+    return set_error(MXGG_ERR_UNSUPPORTED, "grouped_fwd_swiglu_quant: F above 2^29");
+  if (M > 0 && F > 0) {
+    if (!q || !scales)
+      return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd_swiglu_quant: null output");
+    const bool bm = scale_layout == MXGG_SCALES_BLOCK_MAJOR;
+    if (ldq < F || lds < (bm ? M : F / 32))
+      return set_error(MXGG_ERR_SHAPE,
+                       "grouped_fwd_swiglu_quant: leading dimension smaller than the row");
+    if ((reinterpret_cast<uintptr_t>(q) & 7u) != 0 || ldq % 8 != 0)
+      return set_error(MXGG_ERR_ALIGNMENT,
+                       "grouped_fwd_swiglu_quant: q must be 8-byte aligned with ldq %% 8 == 0");
+  }
+  const SwigluOut sw{q, ldq, scales, lds, scale_layout, scale_mode};
+  return grouped_fwd(a, lda, a_scales, ldas, w, w_group_stride, ldw, w_scales, ws_group_stride,
+                     ldws, group_ends, num_groups, M, 2 * F, K, nullptr, 0, MXGG_OUT_BF16, nullptr,
+                     stream, &sw);
+}
 
 int mxgg_grouped_fwd_split(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
                            const void* w, int64_t w_group_stride, int64_t ldw,

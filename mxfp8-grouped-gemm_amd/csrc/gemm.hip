@@ -34,6 +34,7 @@
 #include <mutex>
 #include <vector>
 
+#include "mx_device.h"
 #include "mxgg_internal.h"
 
 namespace mxgg {
@@ -43,7 +44,6 @@ constexpr int kTileP = 256;
 constexpr int kTileQ = 256;
 constexpr int kStageK = 128;    // contraction elements (bytes) per stage
 constexpr int kThreads = 256;
-constexpr int kMaxGroups = 1024;
 constexpr uint32_t kOpBytes = 256u * kStageK;          // one operand of one stage: 32 KB
 constexpr uint32_t kScaleOff = 2u * kOpBytes;          // scale rows after P and Q data
 constexpr uint32_t kStageBytes = kScaleOff + 4u * 512u;  // + [4 blocks][P, Q][256]
@@ -99,6 +99,10 @@ struct Operand {
   uint32_t ld;    // bytes per data row
   uint32_t lds;   // bytes per scale block-row (multiple of 4)
   uint32_t row0;  // first operand row of this tile (multiple of 4)
+  // Operand row of tile row 128, minus row0: 128 for a plain tile of 256
+  // consecutive rows; F for the gate+up tile of the fused SwiGLU forward
+  // (tile rows 0..127 = gate rows, 128..255 = the matching up rows F later).
+  uint32_t hi;
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -193,8 +197,8 @@ struct Stream {
     vp = (P.row0 + r) * P.ld + kcol;
     vq = (Q.row0 + r) * Q.ld + kcol;
     if (SCALED) {
-      sp = P.row0 + 4u * lane;
-      sq = Q.row0 + 4u * lane;
+      sp = P.row0 + 4u * lane + (lane >= 32u ? P.hi - 128u : 0u);
+      sq = Q.row0 + 4u * lane + (lane >= 32u ? Q.hi - 128u : 0u);
     }
   }
 
@@ -209,18 +213,18 @@ struct Stream {
     bq = ok ? vq + k0 : kOobOffset;
   }
 
-  __device__ __forceinline__ static uint32_t step(uint32_t i, uint32_t ld) {
-    return (128u * (i >> 2) + (i & 3u)) * ld;
+  __device__ __forceinline__ static uint32_t step(uint32_t i, const Operand& X) {
+    return ((i >> 2) * X.hi + (i & 3u)) * X.ld;
   }
 
   __device__ __forceinline__ void load_p(uint8_t* stage, const Operand& P, uint32_t bp,
                                          uint32_t i) const {
-    dma_x4(P.data, lds_offset(stage) + 4096u * i + 1024u * wave_id(), bp + step(i, P.ld));
+    dma_x4(P.data, lds_offset(stage) + 4096u * i + 1024u * wave_id(), bp + step(i, P));
   }
   __device__ __forceinline__ void load_q(uint8_t* stage, const Operand& Q, uint32_t bq,
                                          uint32_t i) const {
     dma_x4(Q.data, lds_offset(stage) + kOpBytes + 4096u * i + 1024u * wave_id(),
-           bq + step(i, Q.ld));
+           bq + step(i, Q));
   }
   // Scale rows of k-block k0/32 + wave; operand X = P (OP 0) or Q (OP 1).
   template <int OP>
@@ -505,13 +509,6 @@ __device__ __forceinline__ uint32_t swap_lane_pair(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  const __bf16 ha = (__bf16)a, hb = (__bf16)b;
-  const uint16_t ua = *reinterpret_cast<const uint16_t*>(&ha);
-  const uint16_t ub = *reinterpret_cast<const uint16_t*>(&hb);
-  return (uint32_t)ua | ((uint32_t)ub << 16);
-}
-
 // Write the tile: output row = Q index in [qbeg, qend), column = P index < pend.
 // Accumulator register r of block (i, j) in lane (l32, h) is D[8(r/4) + 4h +
 // r%4][l32] of the 32x32 MFMA, i.e. P index 128wp + 4c + i with
@@ -618,6 +615,79 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
   __syncthreads();
 }
 
+// Epilogue of the fused gate+up forward: the tile's P rows are 128 gate rows
+// (waves wp = 0) and the 128 matching up rows (wp = 1), so a = SiLU(gate) * up
+// of 128 consecutive features of 256 tokens is formed here and written as its
+// row-wise MXFP8 cast: e4m3 payload aq[token][pg + f] and one E8M0 byte per
+// 32 features at s[token * s_row + block * s_blk].  The bf16 gate+up output h
+// of the unfused path never reaches HBM (33 KB written per tile instead of
+// 128 KB).  The arithmetic is the unfused path's: h rounded to bf16, then
+// swiglu_a_chunk and the dim0 cast rule of the standalone kernels.
+//   1. every wave stages its 128 x 128 sub-tile as bf16 in the idle LDS ring:
+//      row q (token) x 512 B, gate columns in 16-byte chunks 0..15, up in
+//      16..31, chunk index XOR-swizzled by (q / 4) mod 16 (each half-wave then
+//      touches every bank at most twice, writing and reading);
+//   2. lane (qq, k) of wave w takes token 64w + 4i + qq and features
+//      8k .. 8k+7 on trip i: one 16-byte read of gate and of up, SwiGLU,
+//      block amax over the quad k = 4b .. 4b+3, 8 payload bytes (16 lanes
+//      write one 128-byte row piece), the quad's first lane the scale byte.
+template <int MODE>
+__device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4], uint8_t* aq,
+                                                int64_t ldq, uint8_t* sc, int64_t s_row,
+                                                int64_t s_blk, uint32_t q0, uint32_t qbeg,
+                                                uint32_t qend, uint32_t pg) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t wp = wave & 1u, wq = wave >> 1;
+  const uint32_t l32 = lane & 31u, h = lane >> 5;
+  uint8_t* st = &sm.ring[0][0];
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t q = 128u * wq + 4u * l32 + j;
+    const uint32_t sw = (q >> 2) & 15u;
+    uint8_t* row = st + q * 512u;
+#pragma unroll
+    for (uint32_t a = 0; a < 4; ++a)
+#pragma unroll
+      for (uint32_t b = 0; b < 2; ++b) {
+        // registers r and r + 1 hold P columns 4c .. 4c+7 of the wave's half,
+        // c = 8a + 4h + 2b
+        const int r = (int)(4u * a + 2u * b);
+        const uint32_t chunk = 16u * wp + 4u * a + 2u * h + b;
+        *reinterpret_cast<uint4*>(row + ((chunk ^ sw) << 4)) =
+            make_uint4(pack_bf16x2(acc[0][j][r], acc[1][j][r]),
+                       pack_bf16x2(acc[2][j][r], acc[3][j][r]),
+                       pack_bf16x2(acc[0][j][r + 1], acc[1][j][r + 1]),
+                       pack_bf16x2(acc[2][j][r + 1], acc[3][j][r + 1]));
+      }
+  }
+  __syncthreads();
+  const uint32_t k = lane & 15u, qq = lane >> 4;
+#pragma unroll 2
+  for (uint32_t i = 0; i < 16u; ++i) {
+    const uint32_t q = 64u * wave + 4u * i + qq;
+    const uint32_t sw = (q >> 2) & 15u;
+    const uint8_t* row = st + q * 512u;
+    const uint4 g = *reinterpret_cast<const uint4*>(row + ((k ^ sw) << 4));
+    const uint4 u = *reinterpret_cast<const uint4*>(row + ((16u + (k ^ sw)) << 4));
+    const uint4 a = swiglu_a_chunk(g, u);
+    uint32_t am = amax16_of_chunk(a);
+    am = max(am, (uint32_t)__shfl_xor((int)am, 1));
+    am = max(am, (uint32_t)__shfl_xor((int)am, 2));
+    const uint32_t b = e8m0_from_amax16<MODE>(am);
+    const uint2 o = __any(b == 255u) ? encode_chunk8<MODE, false, true>(a, b)
+                                     : encode_chunk8<MODE, false, false>(a, b);
+    const uint32_t tok = q0 + q;
+    if (tok >= qbeg && tok < qend) {
+      *reinterpret_cast<uint2*>(aq + (int64_t)tok * ldq + pg + 8u * k) = o;
+      if ((k & 3u) == 0)
+        sc[(int64_t)tok * s_row + (int64_t)((pg >> 5) + (k >> 2)) * s_blk] = (uint8_t)b;
+    }
+  }
+  // every wave has read the staging area before the next tile's loads land
+  __syncthreads();
+}
+
 // Decode a position in the tile order into (mt, nt): bands of `gm`
 // consecutive m-tiles are walked column by column so that neighbouring tiles
 // share either their Q rows or their P rows.
@@ -684,8 +754,14 @@ __device__ __forceinline__ void group_range(const int32_t* gend, int g, int32_t&
 // (the scale DMA copies 4 rows per lane); rows outside the group are computed
 // but not stored.
 // ---------------------------------------------------------------------------
-template <bool SCALED, bool F32>
+// Output of the forward: bf16 or fp32 out[m][n], or (SWIGLU_*) the MXFP8
+// cast of SiLU(gate) * up for a weight holding [gate; up] rows.
+enum { kOutBf16 = 0, kOutF32 = 1, kOutSwigluRceil = 2, kOutSwigluFloor = 3 };
+
+template <bool SCALED, int OUT>
 __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint32_t gm) {
+  constexpr bool F32 = OUT == kOutF32;
+  constexpr bool SWIGLU = OUT >= kOutSwigluRceil;
   __shared__ Smem sm;
   const int E = args.group_ends ? args.E : 1;
   const int32_t M = args.M;
@@ -702,7 +778,9 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
   __syncthreads();
   scan_counts(sm, sm.order, sm.sched, E);
   const uint32_t m_tiles = (uint32_t)sm.sched[E];
-  const uint32_t n_tiles = ((uint32_t)args.N + kTileP - 1) / kTileP;
+  // SWIGLU: N = 2F weight rows; a tile covers 128 features of a (F % 128 == 0)
+  const uint32_t n_tiles = SWIGLU ? (uint32_t)args.N / 256u
+                                  : ((uint32_t)args.N + kTileP - 1) / kTileP;
   const uint32_t total = m_tiles * n_tiles;
   const uint32_t K = (uint32_t)args.K;
   // With a workspace, a last round of tiles that would leave at least half of
@@ -746,16 +824,18 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
     int32_t gb, ge;
     group_range(sm.gend, g, gb, ge);
     const uint32_t q0 = (uint32_t)(gb & ~3) + (mt - (uint32_t)sm.sched[g]) * kTileQ;
-    const uint32_t p0 = nt * kTileP;
+    const uint32_t p0 = nt * (SWIGLU ? 128u : kTileP);
 
     Operand P, Q;
     const uint8_t* wg = args.w + (int64_t)g * args.w_gstride;
     P.data = make_desc(wg, (uint32_t)((int64_t)(args.N - 1) * args.ldw + K));
     P.ld = (uint32_t)args.ldw;
     P.row0 = p0;
+    P.hi = SWIGLU ? (uint32_t)args.N / 2u : 128u;
     Q.data = make_desc(args.a, (uint32_t)((int64_t)(M - 1) * args.lda + K));
     Q.ld = (uint32_t)args.lda;
     Q.row0 = q0;
+    Q.hi = 128u;
     if (SCALED) {
       const uint8_t* wsg = args.ws + (int64_t)g * args.ws_gstride;
       P.scale = make_desc(wsg, scale_extent(K / 32, args.ldws, args.N));
@@ -778,6 +858,11 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
       char* slot = reinterpret_cast<char*>(args.split_ws) + kSplitHdrBytes +
                    (int64_t)(t * S + split) * kPartialBytes;
       epilogue<true>(sm, acc, slot, 1024, 0u, 0u, 256u, 0u, 256u);
+    } else if constexpr (SWIGLU) {
+      mainloop<SCALED>(sm, P, Q, 0u, K, acc);
+      epilogue_swiglu<OUT == kOutSwigluRceil ? kModeRceil : kModeFloor>(
+          sm, acc, args.aq, args.ldaq, args.as_out, args.as_row, args.as_blk, q0, (uint32_t)gb,
+          (uint32_t)ge, p0);
     } else {
       mainloop<SCALED>(sm, P, Q, 0u, K, acc);
       const int64_t ldo_bytes = args.ldo * (F32 ? 4 : 2);
@@ -942,9 +1027,11 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
     P.data = make_desc(args.ia, (uint32_t)((int64_t)(args.K - 1) * args.ldia + M));
     P.ld = (uint32_t)args.ldia;
     P.row0 = p0;
+    P.hi = 128u;
     Q.data = make_desc(args.go, (uint32_t)((int64_t)(args.N - 1) * args.ldgo + M));
     Q.ld = (uint32_t)args.ldgo;
     Q.row0 = q0;
+    Q.hi = 128u;
     if (SCALED) {
       P.scale = make_desc(args.ias, scale_extent(M / 32, args.ldias, args.K));
       P.lds = (uint32_t)args.ldias;
@@ -1100,12 +1187,24 @@ hipError_t launch_grouped_fwd(const FwdArgs& a, hipStream_t stream) {
   if (a.M == 0 || a.N == 0) return hipSuccess;
   const dim3 grid(persistent_grid()), block(kThreads);
   const uint32_t gm = 8;
-#define MXGG_FWD(S, F) hipLaunchKernelGGL((k_grouped_fwd<S, F>), grid, block, 0, stream, a, gm)
-  if (a.scaled) {
-    if (a.out_f32) MXGG_FWD(true, true); else MXGG_FWD(true, false);
-  } else {
-    if (a.out_f32) MXGG_FWD(false, true); else MXGG_FWD(false, false);
+  const int out = a.swiglu_mode == MXGG_SCALE_RCEIL   ? kOutSwigluRceil
+                  : a.swiglu_mode == MXGG_SCALE_FLOOR ? kOutSwigluFloor
+                  : a.out_f32                         ? kOutF32
+                                                      : kOutBf16;
+#define MXGG_FWD(S, O) hipLaunchKernelGGL((k_grouped_fwd<S, O>), grid, block, 0, stream, a, gm)
+#define MXGG_FWD_OUT(S)                                           \
+  switch (out) {                                                  \
+    case kOutF32: MXGG_FWD(S, kOutF32); break;                    \
+    case kOutSwigluRceil: MXGG_FWD(S, kOutSwigluRceil); break;    \
+    case kOutSwigluFloor: MXGG_FWD(S, kOutSwigluFloor); break;    \
+    default: MXGG_FWD(S, kOutBf16); break;                        \
   }
+  if (a.scaled) {
+    MXGG_FWD_OUT(true)
+  } else {
+    MXGG_FWD_OUT(false)
+  }
+#undef MXGG_FWD_OUT
 #undef MXGG_FWD
   if (a.split_ws == nullptr) return hipGetLastError();
   const hipError_t err = hipGetLastError();

@@ -189,6 +189,31 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
+// a / b from the hardware reciprocal and one Newton step on the residual
+// (fma), the classic correction that returns the correctly rounded quotient
+// except in rare near-tie cases; infinities and NaN fall back to a * rcp(b).
+__device__ __forceinline__ float div_nr(float a, float b) {
+  const float r = __builtin_amdgcn_rcpf(b);
+  const float q = a * r;
+  const float q1 = __builtin_fmaf(__builtin_fmaf(-q, b, a), r, q);
+  return q1 == q1 ? q1 : q;
+}
+
+// SwiGLU of the two bf16 values of a word of gate and of up:
+// a = bf16(bf16(g / (1 + exp(-g))) * u), packed (torch's eager bf16
+// F.silu(gate) * up).  Shared by the standalone SwiGLU kernels and the
+// gate+up GEMM epilogue, so both give the same bits.
+__device__ __forceinline__ uint32_t swiglu_a_word(uint32_t gw, uint32_t uw) {
+  const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
+  const uint32_t sw = pack_bf16x2(div_nr(g0, 1.0f + expf(-g0)), div_nr(g1, 1.0f + expf(-g1)));
+  return pack_bf16x2(bf16_lo(sw) * bf16_lo(uw), bf16_hi(sw) * bf16_hi(uw));
+}
+
+__device__ __forceinline__ uint4 swiglu_a_chunk(const uint4& g, const uint4& u) {
+  return make_uint4(swiglu_a_word(g.x, u.x), swiglu_a_word(g.y, u.y), swiglu_a_word(g.z, u.z),
+                    swiglu_a_word(g.w, u.w));
+}
+
 // Group tables of the token-axis casts, staged in LDS by every workgroup:
 //   ends_s[g] : end of group g clamped to [0, rows]
 //   pend_s[g] : padded cumulative end (every group rounded up to 32 tokens),

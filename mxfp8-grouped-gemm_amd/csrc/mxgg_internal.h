@@ -158,6 +158,14 @@ struct FwdArgs {
   // Optional workspace of fwd_split_workspace_bytes(): the tiles of a last,
   // sparse round of tiles are then split along K over the idle CUs.
   float* split_ws;
+  // Fused SwiGLU output (swiglu_mode = MXGG_SCALE_RCEIL / _FLOOR, -1 = off):
+  // w holds [gate; up] (N = 2F rows), and instead of `out` the kernel writes
+  // the row-wise MXFP8 cast of a = SiLU(gate) * up: payload aq [M, F] (row
+  // stride ldaq bytes), scale byte (m, b) at as_out[m * as_row + b * as_blk].
+  int32_t swiglu_mode;
+  uint8_t* aq;
+  uint8_t* as_out;
+  int64_t ldaq, as_row, as_blk;
 };
 hipError_t launch_grouped_fwd(const FwdArgs& args, hipStream_t stream);
 int64_t fwd_split_workspace_bytes();

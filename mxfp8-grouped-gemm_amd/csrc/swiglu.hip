@@ -28,28 +28,6 @@
 namespace mxgg {
 namespace {
 
-// a / b from the hardware reciprocal and one Newton step on the residual
-// (fma), the classic correction that returns the correctly rounded quotient
-// except in rare near-tie cases; infinities and NaN fall back to a * rcp(b).
-__device__ __forceinline__ float div_nr(float a, float b) {
-  const float r = __builtin_amdgcn_rcpf(b);
-  const float q = a * r;
-  const float q1 = __builtin_fmaf(__builtin_fmaf(-q, b, a), r, q);
-  return q1 == q1 ? q1 : q;
-}
-
-// a for the two values of a word of gate and up (packed bf16 result).
-__device__ __forceinline__ uint32_t swiglu_a_word(uint32_t gw, uint32_t uw) {
-  const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
-  const uint32_t sw = pack_bf16x2(div_nr(g0, 1.0f + expf(-g0)), div_nr(g1, 1.0f + expf(-g1)));
-  return pack_bf16x2(bf16_lo(sw) * bf16_lo(uw), bf16_hi(sw) * bf16_hi(uw));
-}
-
-__device__ __forceinline__ uint4 swiglu_a_chunk(const uint4& g, const uint4& u) {
-  return make_uint4(swiglu_a_word(g.x, u.x), swiglu_a_word(g.y, u.y), swiglu_a_word(g.z, u.z),
-                    swiglu_a_word(g.w, u.w));
-}
-
 struct ActWord {
   uint32_t a, dg, du;  // two packed bf16 results each
 };

@@ -14,6 +14,7 @@ from .ops import (
     fwd_ge,
     grouped_dgrad,
     grouped_mm,
+    grouped_mm_swiglu_quant,
     grouped_wgrad,
     offs_to_group_ends,
     padded_token_capacity,
@@ -60,7 +61,7 @@ from .torchao_compat import (
 __all__ = [
     "MxggError", "load_library",
     "to_mxfp8_dim0", "to_mxfp8_dim1", "to_mxfp8_dual", "padded_token_capacity",
-    "grouped_mm", "grouped_wgrad", "grouped_dgrad", "quant_weight_for_dgrad",
+    "grouped_mm", "grouped_mm_swiglu_quant", "grouped_wgrad", "grouped_dgrad", "quant_weight_for_dgrad",
     "quant_weight_dual", "swiglu_quant", "swiglu_backward_quant",
     "fused_grouped_fwd", "fwd_ge", "wgrad_fused", "wgrad_prepare", "wgrad_kernel",
     "offs_to_group_ends", "zero_rows_past_groups",

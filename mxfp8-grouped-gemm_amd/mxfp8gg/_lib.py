@@ -35,7 +35,7 @@ OFFS_ENDS = 0
 OFFS_SIZES = 1
 OFFS_AUTO = 2
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -75,6 +75,11 @@ SIGNATURES = {
          _P, _I64, _I, _P],
     ),
     "mxgg_grouped_fwd_workspace_bytes": (_I64, []),
+    "mxgg_grouped_fwd_swiglu_quant": (
+        _I,
+        [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
+         _P, _I64, _P, _I64, _I, _I, _P],
+    ),
     "mxgg_grouped_fwd_split": (
         _I,
         [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,

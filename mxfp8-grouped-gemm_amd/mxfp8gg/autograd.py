@@ -167,12 +167,24 @@ def _weight_dim0(w, scaling_mode, weight_cache):
     return ops.to_mxfp8_dim0(w, scaling_mode)
 
 
+def _gate_up_act(xq, xs, wq, ws, ends, scaling_mode):
+    """MXFP8 cast of SiLU(gate) * up of the gate+up projection: one fused
+    kernel when the intermediate size allows (F % 128 == 0, activations under
+    2 GiB), else the GEMM's bf16 output through the standalone SwiGLU cast
+    (the same bits either way)."""
+    F2 = wq.shape[1]
+    if F2 % 256 == 0 and (xq.shape[0] == 0 or
+                          (xq.shape[0] - 1) * xq.stride(0) + xq.shape[1] <= ops._MAX_OPERAND_BYTES):
+        return ops.grouped_mm_swiglu_quant(xq, wq, ends, xs, ws, scaling_mode)
+    h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
+    return ops.swiglu_quant(h, scaling_mode)
+
+
 def _ffn_forward_only(x, w_gate_up, w_down, offs, scaling_mode, weight_cache=None):
     _, ends = _check_ffn(x, w_gate_up, w_down, offs)
     xq, xs = ops.to_mxfp8_dim0(x, scaling_mode)
     wq, ws = _weight_dim0(w_gate_up, scaling_mode, weight_cache)
-    h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
-    aq, as_ = ops.swiglu_quant(h, scaling_mode)
+    aq, as_ = _gate_up_act(xq, xs, wq, ws, ends, scaling_mode)
     dq, ds = _weight_dim0(w_down, scaling_mode, weight_cache)
     y = ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16)
     return ops.zero_rows_past_groups(y, ends) if ends is not None else y
@@ -275,8 +287,7 @@ def _routed_forward_only(x, expert_idx, scores, w_gate_up, w_down, pad_multiple,
     plan = routing.route_plan(expert_idx, E, pad_multiple)
     xq, xs = routing.gather_to_mxfp8_dim0(x, plan, scaling_mode)
     wq, ws = _weight_dim0(w_gate_up, scaling_mode, weight_cache)
-    h = ops.grouped_mm(xq, wq, plan.offs, xs, ws, out_dtype=torch.bfloat16)
-    aq, as_ = ops.swiglu_quant(h, scaling_mode)
+    aq, as_ = _gate_up_act(xq, xs, wq, ws, plan.offs, scaling_mode)
     dq, ds = _weight_dim0(w_down, scaling_mode, weight_cache)
     y = ops.grouped_mm(aq, dq, plan.offs, as_, ds, out_dtype=torch.bfloat16)
     return routing.combine(y, plan, scores)

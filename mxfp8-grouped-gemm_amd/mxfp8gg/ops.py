@@ -577,6 +577,59 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
     return out
 
 
+def grouped_mm_swiglu_quant(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
+                            a_scales: torch.Tensor | None = None,
+                            w_scales: torch.Tensor | None = None, scaling_mode="rceil"):
+    """The gate+up projection, SiLU(gate) * up and its row-wise MXFP8 cast in
+    one kernel (mxgg_grouped_fwd_swiglu_quant), for forward-only passes.
+
+    a: e4m3 [M, K]; w: e4m3 [E, 2F, K] with gate rows first (the fused gate+up
+    weight); scales and offs as for grouped_mm.  F % 128 == 0.  Returns
+    (q float8_e4m3fn [M, F], scales uint8 [M, F/32] view of block-major
+    storage), equal to swiglu_quant(grouped_mm(a, w, ...)) on the rows inside
+    the groups (rows past the last group end are not written); the bf16
+    [M, 2F] projection output is never materialised.  The reference runs the
+    gate and up GEMMs, eager SiLU * up and the fp8 cast separately
+    (e2e_bench.py:56-61)."""
+    _need_gpu(a, "a")
+    _need_gpu(w, "w")
+    if a.dim() != 2 or w.dim() != 3:
+        raise ValueError(f"expected a [M, K] and w [E, 2F, K], got {tuple(a.shape)} and {tuple(w.shape)}")
+    M, K = a.shape
+    E, N2, K2 = w.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: {K} vs {K2}")
+    if N2 % 256 != 0:
+        raise ValueError(f"w has {N2} rows; the fused path needs 2F with F % 128 == 0")
+    F = N2 // 2
+    a8 = _as_u8(_rowmajor(a), "a")
+    w8 = _as_u8(_rowmajor(w), "w")
+    if (a_scales is None) != (w_scales is None):
+        raise ValueError("a_scales and w_scales must both be given or both be None")
+    sa = sw = None
+    ldas = ldws = wsg = 0
+    if a_scales is not None:
+        sa, ldas = _scales_2d(a_scales, M, K // 32, "a_scales")
+        sw, wsg, ldws = _scales_3d(w_scales, E, N2, K // 32, "w_scales")
+    ends = None
+    if offs is not None:
+        ends = _group_ends(offs, E, a.device)
+    elif E != 1:
+        raise ValueError("offs is required when w holds more than one expert")
+    if M > 0 and (M - 1) * a8.stride(0) + K > _MAX_OPERAND_BYTES:
+        raise ValueError("the fused SwiGLU forward takes activations below 2 GiB per call")
+    q = torch.empty((M, F), dtype=_FP8, device=a.device)
+    buf = _block_major_buffer(M, F // 32, a.device)
+    lib = _lib.load()
+    _lib.check(lib.mxgg_grouped_fwd_swiglu_quant(
+        a8.data_ptr(), a8.stride(0), sa.data_ptr() if sa is not None else None, ldas,
+        w8.data_ptr(), w8.stride(0), w8.stride(1), sw.data_ptr() if sw is not None else None,
+        wsg, ldws, ends.data_ptr() if ends is not None else None, E, M, F, K,
+        q.data_ptr(), F, buf.data_ptr(), buf.stride(0), _lib.SCALES_BLOCK_MAJOR,
+        _mode(scaling_mode), _stream_ptr(a)), "grouped_fwd_swiglu_quant")
+    return q, buf[:, :M].t()
+
+
 def fused_grouped_fwd(a_fp8, w_fp8, offs, a_scales=None, w_scales=None,
                       BLOCK_M=128, BLOCK_N=128, BLOCK_K=128,
                       GROUP_SIZE_M=8, num_stages=None, num_warps=None, *,
