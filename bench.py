@@ -290,6 +290,33 @@ def layer_step_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     return out
 
 
+def gate_up_swiglu_c5(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
+    """C5's gate+up projection (131072 tokens, Zipf(1.0) over 32 experts,
+    hidden 7168, intermediate 2048) three ways: the grouped GEMM alone (bf16
+    h [M, 4096]), GEMM + the standalone SwiGLU cast (the training forward),
+    and the fused kernel that writes only the MXFP8 cast of SiLU(gate) * up
+    (the forward-only pass)."""
+    from mxfp8gg import ops
+    sizes = workloads.c5_sizes()
+    M, H, F, E = int(sizes.sum()), 7168, 2048, 32
+    gen = torch.Generator(device=dev).manual_seed(0)
+    xq, xs = mxfp8gg.to_mxfp8_dim0(torch.randn((M, H), generator=gen, device=dev).to(torch.bfloat16))
+    wq, ws = mxfp8gg.to_mxfp8_dim0(
+        (torch.randn((E, 2 * F, H), generator=gen, device=dev) * 0.006).to(torch.bfloat16))
+    offs = torch.from_numpy(workloads.ends_of(sizes)).to(dev)
+    h = torch.empty((M, 2 * F), dtype=torch.bfloat16, device=dev)
+    fl = 2 * M * 2 * F * H
+    ms_g = time_launches(lambda: ops.grouped_mm(xq, wq, offs, xs, ws, out=h), steps, warmup, torch)
+    ms_u = time_launches(lambda: ops.swiglu_quant(ops.grouped_mm(xq, wq, offs, xs, ws, out=h)),
+                         steps, warmup, torch)
+    ms_f = time_launches(lambda: ops.grouped_mm_swiglu_quant(xq, wq, offs, xs, ws), steps, warmup,
+                         torch)
+    return {"tokens": M, "gemm_bf16_h_ms": round(ms_g, 4),
+            "gemm_bf16_h_tflops": round(fl / ms_g / 1e9, 1),
+            "gemm_then_swiglu_cast_ms": round(ms_u, 4),
+            "fused_ms": round(ms_f, 4), "fused_tflops": round(fl / ms_f / 1e9, 1)}
+
+
 def routing_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     """C5 as a routed MoE layer: 16384 tokens x top-8 over 32 experts (Zipf(1.0)
     preference), hidden 7168, intermediate 2048.  Times the device dispatch
@@ -515,6 +542,7 @@ def main():
 
     if args.only == "c5":
         print(json.dumps(layer_step_c5(torch, mxfp8gg, workloads, dev)), flush=True)
+        print(json.dumps(gate_up_swiglu_c5(torch, mxfp8gg, workloads, dev)), flush=True)
         return
     if args.only == "routing":
         print(json.dumps(routing_c5(torch, mxfp8gg, workloads, dev)), flush=True)
@@ -633,6 +661,8 @@ def main():
         components["small_launches"] = small_launches(torch, mxfp8gg, dev)
         log("C5: expert-FFN layer step (forward + backward)")
         components["layer_step_c5"] = layer_step_c5(torch, mxfp8gg, workloads, dev)
+        log("C5 gate+up with SwiGLU: unfused vs fused")
+        components["gate_up_swiglu_c5"] = gate_up_swiglu_c5(torch, mxfp8gg, workloads, dev)
         log("C5 as a routed top-8 layer (dispatch, combine)")
         components["routing_c5"] = routing_c5(torch, mxfp8gg, workloads, dev)
 

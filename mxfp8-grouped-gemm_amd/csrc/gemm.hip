@@ -631,11 +631,11 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
 //      8k .. 8k+7 on trip i: one 16-byte read of gate and of up, SwiGLU,
 //      block amax over the quad k = 4b .. 4b+3, 8 payload bytes (16 lanes
 //      write one 128-byte row piece), the quad's first lane the scale byte.
-template <int MODE>
-__device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4], uint8_t* aq,
-                                                int64_t ldq, uint8_t* sc, int64_t s_row,
-                                                int64_t s_blk, uint32_t q0, uint32_t qbeg,
-                                                uint32_t qend, uint32_t pg) {
+// The tile rounded to bf16 and staged in the idle LDS ring as 256 rows (Q
+// index) x 512 B (P index 0..255), 16-byte chunk k of row q at chunk
+// k ^ ((q / 4) mod 16): a half-wave writing one chunk column of 32 rows, or
+// reading one whole row, touches every bank at most twice.
+__device__ __forceinline__ void stage_bf16_tile(Smem& sm, const v16f (&acc)[4][4]) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t wp = wave & 1u, wq = wave >> 1;
@@ -662,6 +662,57 @@ __device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4
       }
   }
   __syncthreads();
+}
+
+// bf16 output through the bf16 staging: wave w stores rows 64w .. 64w+63 of
+// the tile, two whole 512-byte rows per store instruction (lanes 0-31 one
+// row, 32-63 the next).
+__device__ __forceinline__ void epilogue_bf16(Smem& sm, const v16f (&acc)[4][4], char* out,
+                                              int64_t ldo_bytes, uint32_t q0, uint32_t qbeg,
+                                              uint32_t qend, uint32_t p0, uint32_t pend) {
+  stage_bf16_tile(sm, acc);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t c = lane & 31u;
+  const uint32_t p = p0 + 8u * c;
+  const uint8_t* st = &sm.ring[0][0];
+#pragma unroll
+  for (uint32_t i0 = 0; i0 < 32u; i0 += 8u) {
+    u32x4 v[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const uint32_t q = 64u * wave + 2u * (i0 + u) + (lane >> 5);
+      v[u] = *reinterpret_cast<const u32x4*>(st + q * 512u + ((c ^ ((q >> 2) & 15u)) << 4));
+    }
+    // keep the reads here instead of letting them sink into the guarded stores
+    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                 "+v"(v[6]), "+v"(v[7]));
+#pragma unroll
+    for (uint32_t u = 0; u < 8u; ++u) {
+      const uint32_t q = q0 + 64u * wave + 2u * (i0 + u) + (lane >> 5);
+      if (q < qbeg || q >= qend || p >= pend) continue;
+      uint16_t* dst = reinterpret_cast<uint16_t*>(out + (int64_t)q * ldo_bytes) + p;
+      if (p + 8u <= pend && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+        __builtin_nontemporal_store(v[u], reinterpret_cast<u32x4*>(dst));
+      } else {
+        for (uint32_t k = 0; k < 8u && p + k < pend; ++k)
+          dst[k] = (uint16_t)(v[u][k >> 1] >> (16u * (k & 1u)));
+      }
+    }
+  }
+  // every wave has read the staging area before the next tile's loads land
+  __syncthreads();
+}
+
+template <int MODE>
+__device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4], uint8_t* aq,
+                                                int64_t ldq, uint8_t* sc, int64_t s_row,
+                                                int64_t s_blk, uint32_t q0, uint32_t qbeg,
+                                                uint32_t qend, uint32_t pg) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6;
+  uint8_t* st = &sm.ring[0][0];
+  stage_bf16_tile(sm, acc);
   const uint32_t k = lane & 15u, qq = lane >> 4;
 #pragma unroll 2
   for (uint32_t i = 0; i < 16u; ++i) {
@@ -866,8 +917,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
     } else {
       mainloop<SCALED>(sm, P, Q, 0u, K, acc);
       const int64_t ldo_bytes = args.ldo * (F32 ? 4 : 2);
-      epilogue<F32>(sm, acc, reinterpret_cast<char*>(args.out), ldo_bytes, q0, (uint32_t)gb,
-                    (uint32_t)ge, p0, (uint32_t)args.N);
+      if constexpr (F32)
+        epilogue<true>(sm, acc, reinterpret_cast<char*>(args.out), ldo_bytes, q0, (uint32_t)gb,
+                       (uint32_t)ge, p0, (uint32_t)args.N);
+      else
+        epilogue_bf16(sm, acc, reinterpret_cast<char*>(args.out), ldo_bytes, q0, (uint32_t)gb,
+                      (uint32_t)ge, p0, (uint32_t)args.N);
     }
   }
 }
@@ -1063,8 +1118,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
     }
     char* out = reinterpret_cast<char*>(args.dw) +
                 (int64_t)g * args.N * args.K * (F32 ? 4 : 2);
-    epilogue<F32>(sm, acc, out, (int64_t)args.K * (F32 ? 4 : 2), q0, 0u, (uint32_t)args.N, p0,
-                  (uint32_t)args.K, F32 && split > 0 && !staged);
+    if constexpr (F32)
+      epilogue<true>(sm, acc, out, (int64_t)args.K * 4, q0, 0u, (uint32_t)args.N, p0,
+                     (uint32_t)args.K, split > 0 && !staged);
+    else
+      epilogue_bf16(sm, acc, out, (int64_t)args.K * 2, q0, 0u, (uint32_t)args.N, p0,
+                    (uint32_t)args.K);
   }
 }
 
