@@ -14,7 +14,7 @@ reference's CPU path (dequantise + per-group fp32 matmul with torch on the
 host cores) on a bounded sample of C2.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                      [--only fwd|wgrad|copy|ref8|refwgrad|c5|routing|dense|small|traffic]
+                      [--only fwd|wgrad|copy|ref8|refwgrad|c5|routing|dense|small|traffic|hbm]
 """
 import argparse
 import json
@@ -290,6 +290,42 @@ def layer_step_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     return out
 
 
+def hbm_ceiling(torch, mxfp8gg, dev, steps=10, warmup=3):
+    """What plain device kernels reach on this box's HBM, next to the casts on
+    the same data: torch's fill_ (write), sum (read), copy_ (read + write) of
+    2 GiB, and torch's own bf16 -> fp8 conversion (2 bytes read, 1 written per
+    element: the casts' traffic mix without the scales) of C2's X
+    (65536 x 7168), against this library's row-wise and dual casts of that X.
+    GB/s counts algorithmic bytes."""
+    nb = 2 << 30
+    a = torch.empty(nb, dtype=torch.uint8, device=dev)
+    b = torch.empty(nb, dtype=torch.uint8, device=dev)
+    a.fill_(1)
+    res = {}
+    ms = time_launches(lambda: b.fill_(3), steps, warmup, torch)
+    res["write_fill"] = {"GBps": round(nb / ms / 1e6, 1)}
+    ai = a.view(torch.int32)
+    ms = time_launches(lambda: ai.sum(), steps, warmup, torch)
+    res["read_sum"] = {"GBps": round(nb / ms / 1e6, 1)}
+    ms = time_launches(lambda: b.copy_(a), steps, warmup, torch)
+    res["copy"] = {"GBps": round(2 * nb / ms / 1e6, 1)}
+    del a, b, ai
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((65536, 7168), generator=gen, device=dev).to(torch.bfloat16)
+    n = x.numel()
+    ms = time_launches(lambda: x.to(torch.float8_e4m3fn), steps, warmup, torch)
+    res["torch_bf16_to_fp8"] = {"GBps": round(3 * n / ms / 1e6, 1), "bytes_per_elt": 3}
+    ms = time_launches(lambda: mxfp8gg.to_mxfp8_dim0(x), steps, warmup, torch)
+    res["mxgg_quant_dim0"] = {"GBps": round((3 + 1 / 32) * n / ms / 1e6, 1),
+                              "bytes_per_elt": 3.03125}
+    offs = torch.tensor([65536], dtype=torch.int32, device=dev)
+    ms = time_launches(lambda: mxfp8gg.to_mxfp8_dual(x, offs), steps, warmup, torch)
+    res["mxgg_quant_dual"] = {"GBps": round((2 + 2 * (1 + 1 / 32)) * n / ms / 1e6, 1),
+                              "bytes_per_elt": 4.0625}
+    del x
+    return res
+
+
 def gate_up_swiglu_c5(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
     """C5's gate+up projection (131072 tokens, Zipf(1.0) over 32 experts,
     hidden 7168, intermediate 2048) three ways: the grouped GEMM alone (bf16
@@ -511,7 +547,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "refwgrad", "c5",
-                                       "routing", "dense", "small", "traffic"],
+                                       "routing", "dense", "small", "traffic", "hbm"],
                     default="all",
                     help="fwd / wgrad: time only that GEMM (for profiler runs); copy: a plain "
                          "1 GiB device-to-device copy, the reference for HBM byte counters; "
@@ -520,6 +556,7 @@ def main():
                          "expert-FFN layer step only; routing: C5 as a routed top-8 layer; "
                          "dense: C2's shape as one dense GEMM, with hipBLASLt beside it; "
                          "small: launches with fewer tiles than compute units, split or not; "
+                         "hbm: plain-kernel HBM rates beside the casts; "
                          "traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes of fwd and copy "
                          "(child processes) -> profiles/traffic_grouped_fwd_c2.json")
     args = ap.parse_args()
@@ -555,6 +592,9 @@ def main():
         return
     if args.only == "ref8":
         print(json.dumps(ref_equal_shapes(torch, mxfp8gg, workloads, dev)), flush=True)
+        return
+    if args.only == "hbm":
+        print(json.dumps(hbm_ceiling(torch, mxfp8gg, dev)), flush=True)
         return
     if args.only == "refwgrad":
         print(json.dumps(ref_wgrad_shapes(torch, mxfp8gg, dev)), flush=True)
@@ -661,6 +701,8 @@ def main():
         components["small_launches"] = small_launches(torch, mxfp8gg, dev)
         log("C5: expert-FFN layer step (forward + backward)")
         components["layer_step_c5"] = layer_step_c5(torch, mxfp8gg, workloads, dev)
+        log("HBM ceiling of plain kernels beside the casts")
+        components["hbm_ceiling"] = hbm_ceiling(torch, mxfp8gg, dev)
         log("C5 gate+up with SwiGLU: unfused vs fused")
         components["gate_up_swiglu_c5"] = gate_up_swiglu_c5(torch, mxfp8gg, workloads, dev)
         log("C5 as a routed top-8 layer (dispatch, combine)")
