@@ -340,11 +340,11 @@ int mxgg_swiglu_bwd_quant(const void* gate, const void* up, int64_t ldh, const v
                      "swiglu_bwd_quant: dh_q 8-byte aligned with lddq %% 8 == 0; dh_qt and a_qt "
                      "16-byte aligned with strides multiples of 16");
   // one-dimensional grid of 256-thread workgroups: at most 2^24 - 1 of them
-  const int64_t wgs = ((rows_pad_cap + 127) / 128) * ((cols + 63) / 64);
+  const int64_t wgs = ((rows_pad_cap + 127) / 128) * ((cols + 127) / 128);
   if (rows > INT32_MAX || rows_pad_cap > INT32_MAX || cols > INT32_MAX || wgs >= (INT64_C(1) << 24))
     return set_error(MXGG_ERR_UNSUPPORTED,
                      "swiglu_bwd_quant: rows or rows_pad_cap above 2^31, or "
-                     "ceil(rows_pad_cap/128) * ceil(cols/64) = %lld workgroups (at most 2^24 - 1)",
+                     "ceil(rows_pad_cap/128) * ceil(cols/128) = %lld workgroups (at most 2^24 - 1)",
                      (long long)wgs);
   SwigluBwdLaunch l;
   l.gate = static_cast<const uint16_t*>(gate);

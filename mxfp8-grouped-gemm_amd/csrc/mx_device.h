@@ -107,6 +107,20 @@ __device__ __forceinline__ uint32_t amax16_of_word(uint32_t w) {
   return lo > hi ? lo : hi;
 }
 
+// Max over the four lanes of a quad, through DPP quad permutations [1,0,3,2]
+// and [2,3,0,1] (VALU only, no LDS round trip).  Every lane of the quad must
+// be active.
+__device__ __forceinline__ uint32_t quad_max(uint32_t x) {
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0xB1, 0xF, 0xF, false));
+  return max(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x4E, 0xF, 0xF, false));
+}
+
+// Streaming (nontemporal) 8-byte store of payload bytes that this kernel does
+// not read back.
+__device__ __forceinline__ void store_stream(uint8_t* p, uint2 v) {
+  __builtin_nontemporal_store(u32x2{v.x, v.y}, reinterpret_cast<u32x2*>(p));
+}
+
 // Lane-wise max of two pairs of 16-bit integers (v_pk_max_u16).
 __device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));

@@ -13,6 +13,7 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Flag OR-ed into scale_mode: use the bit-level software e4m3 encoder instead
 // of v_cvt_pk_fp8_f32.  Both must give identical bytes; the flag exists so the

@@ -121,18 +121,24 @@ __global__ __launch_bounds__(256) void k_swiglu_dim0(
 }
 
 // ---------------------------------------------------------------------------
-// Backward.  A workgroup covers 128 padded token positions x 64 features of
-// a (so 2 x 64 features of h and dh); wave w takes positions 32w .. 32w+31,
-// exactly one 32-token scale block.  Lane (tg = lane % 4, fg = lane / 4) owns
-// 8 positions (8 tg ..) and 4 features (4 fg ..): it loads 8 token rows of
-// gate, up and da as 8-byte vectors (sixteen lanes read 128 contiguous bytes
-// of a row), computes a, d_gate and d_up in registers, and emits
+// Backward.  A workgroup covers 128 padded token positions x 128 features of
+// a (so 2 x 128 features of h and dh); wave w takes positions 32w .. 32w+31,
+// exactly one 32-token scale block.  Lane (tg = lane % 2, fg = lane / 2) owns
+// 16 positions (16 tg ..) and 4 features (4 fg ..): it loads 16 token rows of
+// gate, up and da as 8-byte vectors (32 lanes read 256 contiguous bytes of a
+// row), computes a, d_gate and d_up in registers (in place of the inputs),
+// and emits
 //   row-wise casts of d_gate / d_up: a 32-feature block is the eight lanes
-//     fg = 8k .. 8k+7 (amax combined with xor-4 / xor-8 / xor-16 shuffles);
-//   token-axis casts of a, d_gate, d_up: a 32-token block is the four lanes
-//     tg = 0 .. 3 (xor-1 / xor-2 shuffles), 8 payload bytes per feature, so the
-//     four waves write 128 contiguous bytes of every output row.
-// Padded positions map to tokens as in the token-axis cast; a run of 8 never
+//     of one 16-lane row with the same tg (amax combined with DPP rotations
+//     by 2, 4 and 8 within the row); a wave's store covers whole 128-byte
+//     lines of two token rows;
+//   token-axis casts of a, d_gate, d_up: a 32-token block is the two lanes
+//     tg = 0, 1 (one DPP swap), 16 payload bytes per feature, so the four
+//     waves write 128 contiguous bytes of every output row.
+// (Measured at C5's shape: 3.2 TB/s with 32 positions x 64 features per
+// workgroup, whose row-wise lines were split between two workgroups, 3.8 TB/s
+// so.  Streaming stores pay off for the whole-line row-wise stores only.)
+// Padded positions map to tokens as in the token-axis cast; a run of 16 never
 // straddles a group because groups start on multiples of 32.
 // ---------------------------------------------------------------------------
 struct SwigluBwdArgs {
@@ -161,55 +167,44 @@ __device__ __forceinline__ float half_f(const uint2& v, int j) {
   return (j & 1) ? bf16_hi(w) : bf16_lo(w);
 }
 
-// Writes n <= 8 scale bytes b[j] at p[j * stride], as one 8-byte store when
-// all eight are contiguous and aligned.
-__device__ __forceinline__ void store_scale8(uint8_t* p, int64_t stride, const uint32_t (&b)[8],
-                                             int n) {
-  if (stride == 1 && n == 8 && (reinterpret_cast<uintptr_t>(p) & 7u) == 0) {
-    *reinterpret_cast<uint2*>(p) = make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
-                                              b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (j < n) p[(int64_t)j * stride] = (uint8_t)b[j];
-  }
-}
-
-// Token-axis cast of the lane's 4 features x 8 positions held in v[0..7]:
-// feature j goes to row j of `qrow` (8 payload bytes; qrow already points at
-// column P of the lane's first feature row) and its scale byte to srow[j *
-// st_row]; the lane with tg == 0 writes the 4 scale bytes.  ANY: some block
-// of the wave holds a NaN (decided once per wave, so the common case runs the
-// short encoder without per-lane branches).
+// Token-axis cast of the lane's 4 features x 16 positions held in v[0..15]:
+// feature j goes to row j of `qrow` (16 payload bytes; qrow already points at
+// column P of the lane's first feature row).  ANY: some block of the wave
+// holds a NaN (decided once per wave, so the common case runs the short
+// encoder without per-lane branches).
 template <int MODE, bool SW, bool ANY>
-__device__ __forceinline__ void token_axis_payload(const uint2 (&v)[8], const uint32_t (&bytes)[4],
+__device__ __forceinline__ void token_axis_payload(const uint2 (&v)[16], const uint32_t (&bytes)[4],
                                                    uint8_t* qrow, int64_t ldqt, bool out_ok) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t lo = encode4_sel<MODE, SW, ANY>(half_f(v[0], j), half_f(v[1], j),
-                                                   half_f(v[2], j), half_f(v[3], j), bytes[j]);
-    const uint32_t hi = encode4_sel<MODE, SW, ANY>(half_f(v[4], j), half_f(v[5], j),
-                                                   half_f(v[6], j), half_f(v[7], j), bytes[j]);
-    if (out_ok) *reinterpret_cast<uint2*>(qrow + j * ldqt) = make_uint2(lo, hi);
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = encode4_sel<MODE, SW, ANY>(half_f(v[4 * k], j), half_f(v[4 * k + 1], j),
+                                        half_f(v[4 * k + 2], j), half_f(v[4 * k + 3], j), bytes[j]);
+    if (out_ok) *reinterpret_cast<uint4*>(qrow + j * ldqt) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
 
+// Max of the two lanes of a pair (DPP quad permutation [1,0,3,2]).
+__device__ __forceinline__ uint32_t pair_max_u16x2(uint32_t x) {
+  return pk_max_u16(x, (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0xB1, 0xF, 0xF, false));
+}
+
 template <int MODE, bool SW>
-__device__ __forceinline__ void emit_token_axis(const uint2 (&v)[8], uint8_t* qrow, int64_t ldqt,
+__device__ __forceinline__ void emit_token_axis(const uint2 (&v)[16], uint8_t* qrow, int64_t ldqt,
                                                 uint8_t* srow, int64_t st_row, bool out_ok,
                                                 bool scale_lane) {
   // amax of both features of a word at once (packed 16-bit max), combined
-  // over the four lanes of the 32-token block.
+  // over the two lanes of the 32-token block.
   uint32_t mx = 0, my = 0;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 16; ++i) {
     mx = pk_max_u16(mx, abs_bf16x2(v[i].x));
     my = pk_max_u16(my, abs_bf16x2(v[i].y));
   }
-  mx = pk_max_u16(mx, (uint32_t)__shfl_xor((int)mx, 1));
-  my = pk_max_u16(my, (uint32_t)__shfl_xor((int)my, 1));
-  mx = pk_max_u16(mx, (uint32_t)__shfl_xor((int)mx, 2));
-  my = pk_max_u16(my, (uint32_t)__shfl_xor((int)my, 2));
+  mx = pair_max_u16x2(mx);
+  my = pair_max_u16x2(my);
   uint32_t bytes[4];
   bytes[0] = e8m0_from_amax16<MODE>(mx & 0xFFFFu);
   bytes[1] = e8m0_from_amax16<MODE>(mx >> 16);
@@ -232,43 +227,55 @@ __device__ __forceinline__ void emit_token_axis(const uint2 (&v)[8], uint8_t* qr
   }
 }
 
-// Row-wise cast of 4 features x 8 tokens (chunk v[i] of token i) into qrow
-// (row of the first token, already offset to the lane's column), scale bytes
-// into srow[i * s_row]; the eight lanes of a 32-feature block share amax.
+// Row-wise cast of 4 features x 16 tokens (chunk v[i] of token i) into qrow
+// (row of the first token, already offset to the lane's column); the eight
+// lanes of a 32-feature block share amax.
 template <int MODE, bool SW, bool ANY>
-__device__ __forceinline__ void row_wise_payload(const uint2 (&v)[8], const uint32_t (&bytes)[8],
+__device__ __forceinline__ void row_wise_payload(const uint2 (&v)[16], const uint32_t (&bytes)[16],
                                                  uint8_t* qrow, int64_t ldq, int ntok) {
-  uint32_t o[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    o[i] = encode4_sel<MODE, SW, ANY>(bf16_lo(v[i].x), bf16_hi(v[i].x), bf16_lo(v[i].y),
-                                      bf16_hi(v[i].y), bytes[i]);
-  if (ntok == 8) {  // every run but the last one of a group
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t o = encode4_sel<MODE, SW, ANY>(bf16_lo(v[i].x), bf16_hi(v[i].x),
+                                                  bf16_lo(v[i].y), bf16_hi(v[i].y), bytes[i]);
+    if (i < ntok) __builtin_nontemporal_store(o, reinterpret_cast<uint32_t*>(qrow + i * ldq));
+  }
+}
+
+// Writes n <= 16 scale bytes b[j] at p[j * stride], as one 16-byte store when
+// all sixteen are contiguous and aligned.
+__device__ __forceinline__ void store_scale16(uint8_t* p, int64_t stride, const uint32_t (&b)[16],
+                                              int n) {
+  if (stride == 1 && n == 16 && (reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+    uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint32_t*>(qrow + i * ldq) = o[i];
+    for (int k = 0; k < 4; ++k)
+      w[k] = b[4 * k] | (b[4 * k + 1] << 8) | (b[4 * k + 2] << 16) | (b[4 * k + 3] << 24);
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
   } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (i < ntok) *reinterpret_cast<uint32_t*>(qrow + i * ldq) = o[i];
+    for (int j = 0; j < 16; ++j)
+      if (j < n) p[(int64_t)j * stride] = (uint8_t)b[j];
   }
 }
 
 template <int MODE, bool SW>
-__device__ __forceinline__ void emit_row_wise(const uint2 (&v)[8], uint8_t* qrow, int64_t ldq,
+__device__ __forceinline__ void emit_row_wise(const uint2 (&v)[16], uint8_t* qrow, int64_t ldq,
                                               uint8_t* srow, int64_t s_row, int ntok,
                                               bool scale_lane) {
   // amax of each token's 4 features, two tokens packed per shuffle, combined
   // over the eight lanes of the 32-feature block.
-  uint32_t bytes[8];
+  uint32_t bytes[16];
   bool nan = false;
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < 8; ++t) {
     const uint32_t m0 = pk_max_u16(abs_bf16x2(v[2 * t].x), abs_bf16x2(v[2 * t].y));
     const uint32_t m1 = pk_max_u16(abs_bf16x2(v[2 * t + 1].x), abs_bf16x2(v[2 * t + 1].y));
     uint32_t m = max(m0 & 0xFFFFu, m0 >> 16) | (max(m1 & 0xFFFFu, m1 >> 16) << 16);
-    m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 4));
-    m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 8));
-    m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 16));
+    // the block's eight lanes are those of one 16-lane row with the same
+    // parity: rotations by 2, 4 and 8 within the row reach all of them
+    m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x122, 0xF, 0xF, false));
+    m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x124, 0xF, 0xF, false));
+    m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x128, 0xF, 0xF, false));
     bytes[2 * t] = e8m0_from_amax16<MODE>(m & 0xFFFFu);
     bytes[2 * t + 1] = e8m0_from_amax16<MODE>(m >> 16);
     nan |= (bytes[2 * t] == 255u) | (bytes[2 * t + 1] == 255u);
@@ -277,76 +284,67 @@ __device__ __forceinline__ void emit_row_wise(const uint2 (&v)[8], uint8_t* qrow
     row_wise_payload<MODE, SW, true>(v, bytes, qrow, ldq, ntok);
   else
     row_wise_payload<MODE, SW, false>(v, bytes, qrow, ldq, ntok);
-  if (scale_lane && ntok > 0) store_scale8(srow, s_row, bytes, ntok);
+  if (scale_lane && ntok > 0) store_scale16(srow, s_row, bytes, ntok);
 }
 
-// Optional bf16 copy of 8 token rows x 4 features (dh may be null).
-__device__ __forceinline__ void store_bf16_rows(const uint2 (&v)[8], uint16_t* dh, int64_t off,
+// Optional bf16 copy of 16 token rows x 4 features (dh may be null).
+__device__ __forceinline__ void store_bf16_rows(const uint2 (&v)[16], uint16_t* dh, int64_t off,
                                                 int64_t ld, int ntok) {
   if (dh == nullptr) return;
-  if (ntok == 8) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<uint2*>(dh + off + i * ld) = v[i];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (i < ntok) *reinterpret_cast<uint2*>(dh + off + i * ld) = v[i];
-  }
+  for (int i = 0; i < 16; ++i)
+    if (i < ntok) *reinterpret_cast<uint2*>(dh + off + i * ld) = v[i];
 }
 
-// At most 168 VGPRs (three waves per SIMD): the kernel streams and needs the
-// extra waves to keep loads in flight; the compiler fits it without spills.
+// 16 token rows of three inputs stay in registers: two waves per SIMD.
 template <int MODE, bool SW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_swiglu_bwd(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_swiglu_bwd(
     const SwigluBwdArgs p) {
   __shared__ int32_t ends_s[kMaxGroups];
   __shared__ int32_t pend_s[kMaxGroups];
   const int lane = threadIdx.x & 63;
-  const int tg = lane & 3, fg = lane >> 2;
-  // Feature blocks vary fastest over the (one-dimensional) grid, so the
-  // workgroups that write the two 64-byte halves of a row-wise output line run
-  // at the same time.
-  const uint32_t nfb = ((uint32_t)p.cols + 63u) / 64u;
+  const int tg = lane & 1, fg = lane >> 1;
+  const uint32_t nfb = ((uint32_t)p.cols + 127u) / 128u;
   const uint32_t fb = blockIdx.x % nfb, pb = blockIdx.x / nfb;
-  const int64_t P = (int64_t)pb * 128 + (threadIdx.x >> 6) * 32 + 8 * tg;
-  const int f = (int)fb * 64 + 4 * fg;
+  const int64_t P = (int64_t)pb * 128 + (threadIdx.x >> 6) * 32 + 16 * tg;
+  const int f = (int)fb * 128 + 4 * fg;
 
   int64_t tok0 = 0;
   int ntok = 0;
   if (p.ends != nullptr) {
     stage_group_tables(p.ends, p.ends_pad, p.E, p.rows, ends_s, pend_s);
     __syncthreads();
-    padded_run_tokens(P, 8, ends_s, pend_s, p.E, tok0, ntok);
+    padded_run_tokens(P, 16, ends_s, pend_s, p.E, tok0, ntok);
   } else {
     tok0 = P;
     const int64_t n = p.rows - P;
-    ntok = n <= 0 ? 0 : (n >= 8 ? 8 : (int)n);
+    ntok = n <= 0 ? 0 : (n >= 16 ? 16 : (int)n);
   }
   if (f >= p.cols) ntok = 0;
 
   const uint16_t* gp = p.gate + tok0 * p.ldh + f;
   const uint16_t* upp = p.up + tok0 * p.ldh + f;
   const uint16_t* dp = p.da + tok0 * p.ldda + f;
-  uint2 g[8], u[8], d[8];
+  // gate, up and da are loaded into A, DG, DU and replaced there by a,
+  // d_gate and d_up, one token at a time (interleaving all 32 exp/div chains
+  // would need far more registers than this streaming kernel can hold)
+  uint2 A[16], DG[16], DU[16];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    g[i] = u[i] = d[i] = make_uint2(0, 0);
+  for (int i = 0; i < 16; ++i) {
+    A[i] = DG[i] = DU[i] = make_uint2(0, 0);
     if (i < ntok) {
-      g[i] = *reinterpret_cast<const uint2*>(gp + i * p.ldh);
-      u[i] = *reinterpret_cast<const uint2*>(upp + i * p.ldh);
-      d[i] = *reinterpret_cast<const uint2*>(dp + i * p.ldda);
+      A[i] = *reinterpret_cast<const uint2*>(gp + i * p.ldh);
+      DG[i] = *reinterpret_cast<const uint2*>(upp + i * p.ldh);
+      DU[i] = *reinterpret_cast<const uint2*>(dp + i * p.ldda);
     }
   }
-  uint2 A[8], DG[8], DU[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const ActWord r0 = swiglu_bwd_word(g[i].x, u[i].x, d[i].x);
-    const ActWord r1 = swiglu_bwd_word(g[i].y, u[i].y, d[i].y);
+  for (int i = 0; i < 16; ++i) {
+    const ActWord r0 = swiglu_bwd_word(A[i].x, DG[i].x, DU[i].x);
+    const ActWord r1 = swiglu_bwd_word(A[i].y, DG[i].y, DU[i].y);
     A[i] = make_uint2(r0.a, r1.a);
     DG[i] = make_uint2(r0.dg, r1.dg);
     DU[i] = make_uint2(r0.du, r1.du);
-    // One token at a time: interleaving all 32 exp/div chains would need far
-    // more registers than the occupancy of this streaming kernel allows.
     __builtin_amdgcn_sched_barrier(0);
   }
 
@@ -354,7 +352,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   store_bf16_rows(DG, p.dh, tok0 * p.lddh + f, p.lddh, ntok);
   store_bf16_rows(DU, p.dh, tok0 * p.lddh + cols + f, p.lddh, ntok);
 
-  // Row-wise casts: d_gate into columns f.., d_up into columns cols + f.. of dq.
   const bool row_scale_lane = (fg & 7) == 0;
   uint8_t* qrow = p.dq + tok0 * p.lddq + f;
   uint8_t* srow = p.ds + tok0 * p.ds_row;
@@ -363,8 +360,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
   emit_row_wise<MODE, SW>(DU, qrow + cols, p.lddq, srow + ((cols + f) >> 5) * p.ds_blk, p.ds_row,
                           ntok, row_scale_lane);
 
-  // Token-axis casts: a -> rows f.. of aqt; d_gate -> rows f.., d_up -> rows
-  // cols + f.. of dqt.  Padded positions carry zeros (zero payload, byte 0).
   const bool out_ok = f < p.cols && P < p.cap;
   const bool tok_scale_lane = tg == 0;
   const int64_t sblk = P >> 5;
@@ -392,7 +387,7 @@ hipError_t swiglu_dim0_impl(const uint16_t* gate, const uint16_t* up, int64_t ld
 
 template <int MODE, bool SW>
 hipError_t swiglu_bwd_impl(const SwigluBwdArgs& p, hipStream_t stream) {
-  dim3 grid((unsigned)(((p.cap + 127) / 128) * ((p.cols + 63) / 64)));
+  dim3 grid((unsigned)(((p.cap + 127) / 128) * ((p.cols + 127) / 128)));
   hipLaunchKernelGGL((k_swiglu_bwd<MODE, SW>), grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }

@@ -327,9 +327,9 @@ def _swiglu_bwd(lib, **kw):
     (dict(lddqt=136), _lib.ERR_ALIGNMENT),
     (dict(dq=FAKE + 4), _lib.ERR_ALIGNMENT),
     (dict(dh=FAKE + 8), _lib.ERR_ALIGNMENT),
-    # 1024 position blocks x 16384 feature blocks: 2^24 workgroups, over the grid limit
-    (dict(cols=1 << 20, ldh=2 << 20, ldga=1 << 20, lddq=2 << 20, cap=131072, lddqt=131072,
-          ldaqt=131072, lddst=2 << 20, ldast=1 << 20), _lib.ERR_UNSUPPORTED),
+    # 1024 position blocks x 16384 feature blocks of 128: 2^24 workgroups, over the grid limit
+    (dict(cols=1 << 21, ldh=2 << 21, ldga=1 << 21, lddq=2 << 21, cap=131072, lddqt=131072,
+          ldaqt=131072, lddst=2 << 21, ldast=1 << 21), _lib.ERR_UNSUPPORTED),
 ])
 def test_swiglu_bwd_quant_rejects(lib, kw, status):
     assert _swiglu_bwd(lib, **kw) == status
