@@ -290,13 +290,14 @@ def layer_step_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
     return out
 
 
-def hbm_ceiling(torch, mxfp8gg, dev, steps=10, warmup=3):
+def hbm_ceiling(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
     """What plain device kernels reach on this box's HBM, next to the casts on
-    the same data: torch's fill_ (write), sum (read), copy_ (read + write) of
-    2 GiB, and torch's own bf16 -> fp8 conversion (2 bytes read, 1 written per
-    element: the casts' traffic mix without the scales) of C2's X
-    (65536 x 7168), against this library's row-wise and dual casts of that X.
-    GB/s counts algorithmic bytes."""
+    the same data: torch's fill_ (write), sum and amax (read), copy_ (read +
+    write) of 2 GiB, and torch's own bf16 -> fp8 conversion (2 bytes read, 1
+    written per element: the casts' traffic mix without the scales) of C2's X
+    (65536 x 7168), against this library's row-wise, token-axis and dual casts
+    of that X, and its two SwiGLU kernels at C5's shape.  GB/s counts
+    algorithmic bytes."""
     nb = 2 << 30
     a = torch.empty(nb, dtype=torch.uint8, device=dev)
     b = torch.empty(nb, dtype=torch.uint8, device=dev)
@@ -304,12 +305,14 @@ def hbm_ceiling(torch, mxfp8gg, dev, steps=10, warmup=3):
     res = {}
     ms = time_launches(lambda: b.fill_(3), steps, warmup, torch)
     res["write_fill"] = {"GBps": round(nb / ms / 1e6, 1)}
-    ai = a.view(torch.int32)
-    ms = time_launches(lambda: ai.sum(), steps, warmup, torch)
+    af = a.view(torch.float32)
+    ms = time_launches(lambda: af.sum(), steps, warmup, torch)
     res["read_sum"] = {"GBps": round(nb / ms / 1e6, 1)}
+    ms = time_launches(lambda: af.amax(), steps, warmup, torch)
+    res["read_amax"] = {"GBps": round(nb / ms / 1e6, 1)}
     ms = time_launches(lambda: b.copy_(a), steps, warmup, torch)
     res["copy"] = {"GBps": round(2 * nb / ms / 1e6, 1)}
-    del a, b, ai
+    del a, b, af
     gen = torch.Generator(device=dev).manual_seed(0)
     x = torch.randn((65536, 7168), generator=gen, device=dev).to(torch.bfloat16)
     n = x.numel()
@@ -322,7 +325,27 @@ def hbm_ceiling(torch, mxfp8gg, dev, steps=10, warmup=3):
     ms = time_launches(lambda: mxfp8gg.to_mxfp8_dual(x, offs), steps, warmup, torch)
     res["mxgg_quant_dual"] = {"GBps": round((2 + 2 * (1 + 1 / 32)) * n / ms / 1e6, 1),
                               "bytes_per_elt": 4.0625}
+    ms = time_launches(lambda: mxfp8gg.to_mxfp8_dim1(x, offs), steps, warmup, torch)
+    res["mxgg_quant_dim1"] = {"GBps": round((3 + 1 / 32) * n / ms / 1e6, 1),
+                              "bytes_per_elt": 3.03125}
     del x
+    # the SwiGLU kernels at C5's shape (131072 tokens, intermediate 2048,
+    # Zipf(1.0) groups): forward reads h [M, 2F] and writes a's cast; backward
+    # reads h and dA and writes the row-wise cast of dh and the token-axis
+    # casts of dh and a
+    sizes = workloads.c5_sizes()
+    M, F = int(sizes.sum()), 2048
+    e5 = torch.from_numpy(workloads.ends_of(sizes)).to(dev)
+    cap = mxfp8gg.padded_token_capacity(M, len(sizes))
+    h = torch.randn((M, 2 * F), generator=gen, device=dev).to(torch.bfloat16)
+    da = (torch.randn((M, F), generator=gen, device=dev) * 0.05).to(torch.bfloat16)
+    cast = 1 + 1 / 32
+    ms = time_launches(lambda: mxfp8gg.swiglu_quant(h), steps, warmup, torch)
+    res["mxgg_swiglu_fwd_c5"] = {"GBps": round((M * 2 * F * 2 + M * F * cast) / ms / 1e6, 1)}
+    ms = time_launches(lambda: mxfp8gg.swiglu_backward_quant(h, da, e5), steps, warmup, torch)
+    b_bwd = M * 2 * F * 2 + M * F * 2 + M * 2 * F * cast + 3 * F * cap * cast
+    res["mxgg_swiglu_bwd_c5"] = {"GBps": round(b_bwd / ms / 1e6, 1)}
+    del h, da
     return res
 
 
@@ -594,7 +617,7 @@ def main():
         print(json.dumps(ref_equal_shapes(torch, mxfp8gg, workloads, dev)), flush=True)
         return
     if args.only == "hbm":
-        print(json.dumps(hbm_ceiling(torch, mxfp8gg, dev)), flush=True)
+        print(json.dumps(hbm_ceiling(torch, mxfp8gg, workloads, dev)), flush=True)
         return
     if args.only == "refwgrad":
         print(json.dumps(ref_wgrad_shapes(torch, mxfp8gg, dev)), flush=True)
@@ -702,7 +725,7 @@ def main():
         log("C5: expert-FFN layer step (forward + backward)")
         components["layer_step_c5"] = layer_step_c5(torch, mxfp8gg, workloads, dev)
         log("HBM ceiling of plain kernels beside the casts")
-        components["hbm_ceiling"] = hbm_ceiling(torch, mxfp8gg, dev)
+        components["hbm_ceiling"] = hbm_ceiling(torch, mxfp8gg, workloads, dev)
         log("C5 gate+up with SwiGLU: unfused vs fused")
         components["gate_up_swiglu_c5"] = gate_up_swiglu_c5(torch, mxfp8gg, workloads, dev)
         log("C5 as a routed top-8 layer (dispatch, combine)")
