@@ -27,9 +27,8 @@
  * keeps the closed forms above): the byte of an infinite amax (RCEIL 254,
  * FLOOR 247), of an all-zero block (0), and the RCEIL payload multiplier 1
  * for scale byte 0 (blocks with amax < 448 * 2^-127).  Every other rule is
- * checked against torch's
- * e4m3 cast, brute force and the reference's known-answer vectors
- * (tests/test_oracle.py).
+ * checked against torch's e4m3 cast, brute force and the reference's
+ * known-answer vectors (tests/test_oracle.py).
  *
  * The implementation deliberately differs from the GPU kernels: e4m3 rounding
  * is a nearest-value search over the decoded code table, and the scale
