@@ -208,13 +208,23 @@ def _out_code(dtype: torch.dtype) -> int:
 # ---------------------------------------------------------------------------
 # bf16 -> MXFP8 casts
 # ---------------------------------------------------------------------------
-def to_mxfp8_dim0(x: torch.Tensor, scaling_mode="rceil"):
+def _layout_code(scale_layout: str) -> int:
+    if scale_layout == "block":
+        return _lib.SCALES_BLOCK_MAJOR
+    if scale_layout == "row":
+        return _lib.SCALES_ROW_MAJOR
+    raise ValueError(f"scale_layout must be 'block' or 'row', got {scale_layout!r}")
+
+
+def to_mxfp8_dim0(x: torch.Tensor, scaling_mode="rceil", scale_layout: str = "block"):
     """Row-wise MXFP8: 1x32 blocks along the last dimension.
 
     x: bf16 [..., K] (K % 32 == 0).  Returns (q float8_e4m3fn [..., K],
-    scales uint8 [..., K/32]) with E8M0 bytes (2^(b-127)).  The scales are a
-    view of block-major storage ([K/32][rows], what the GEMM kernels read);
-    .contiguous() gives the row-major copy.
+    scales uint8 [..., K/32]) with E8M0 bytes (2^(b-127)).  scale_layout
+    "block" (default): the scales are a view of block-major storage
+    ([K/32][rows], what the GEMM kernels read, so they take it without a
+    conversion); "row": contiguous row-major scales, written so by the cast
+    itself (what torchao's casts return; a GEMM call converts them).
     """
     _need_gpu(x, "x")
     if x.dtype != torch.bfloat16:
@@ -226,15 +236,21 @@ def to_mxfp8_dim0(x: torch.Tensor, scaling_mode="rceil"):
         x2 = x2.contiguous()
     rows = x2.shape[0]
     nblk = K // 32
+    layout = _layout_code(scale_layout)
     q = torch.empty((rows, K), dtype=_FP8, device=x.device)
-    buf = _block_major_buffer(rows, nblk, x.device)
+    if layout == _lib.SCALES_ROW_MAJOR:
+        buf = torch.empty((rows, nblk), dtype=torch.uint8, device=x.device)
+    else:
+        buf = _block_major_buffer(rows, nblk, x.device)
     lib = _lib.load()
     _lib.check(
         lib.mxgg_quant_dim0(x2.data_ptr(), rows, K, x2.stride(0), q.data_ptr(), q.stride(0),
-                            buf.data_ptr(), buf.stride(0), _lib.SCALES_BLOCK_MAJOR,
+                            buf.data_ptr(), max(buf.stride(0), 1), layout,
                             _mode(scaling_mode), _stream_ptr(x)),
         "quant_dim0",
     )
+    if layout == _lib.SCALES_ROW_MAJOR:
+        return q.reshape(shape), buf.reshape(tuple(shape[:-1]) + (nblk,))
     lead = tuple(shape[:-1])
     lead_strides = []
     acc = 1
@@ -256,7 +272,8 @@ def padded_token_capacity(num_tokens: int, num_groups: int | None) -> int:
     return (num_tokens + 31 * num_groups + 127) // 128 * 128
 
 
-def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mode="rceil"):
+def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mode="rceil",
+                  scale_layout: str = "block"):
     """Token-axis MXFP8 for the wgrad operands, written transposed.
 
     x: bf16 [M, C] (tokens x features).  Blocks of 32 run along M and restart
@@ -265,7 +282,8 @@ def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mod
     Returns (qt float8_e4m3fn [C, M_pad], st uint8 [C, M_pad/32], offs_pad)
     where offs_pad are the padded cumulative ends (int32 [E], None without
     offs) and M_pad = padded_token_capacity(M, E) >= offs_pad[-1].  st is a
-    view of block-major storage ([M_pad/32][C]).
+    view of block-major storage ([M_pad/32][C]) with scale_layout "block"
+    (default), contiguous row-major with "row".
     """
     _need_gpu(x, "x")
     if x.dtype != torch.bfloat16 or x.dim() != 2:
@@ -280,21 +298,25 @@ def to_mxfp8_dim1(x: torch.Tensor, offs: torch.Tensor | None = None, scaling_mod
         ends = _group_ends(offs, E, x.device)
         ends_pad = torch.empty(E, dtype=torch.int32, device=x.device)
     cap = padded_token_capacity(M, E)
+    layout = _layout_code(scale_layout)
     qt = torch.empty((C, cap), dtype=_FP8, device=x.device)
-    buf = _block_major_buffer(C, cap // 32, x.device)
+    if layout == _lib.SCALES_ROW_MAJOR:
+        buf = torch.empty((C, cap // 32), dtype=torch.uint8, device=x.device)
+    else:
+        buf = _block_major_buffer(C, cap // 32, x.device)
     lib = _lib.load()
     _lib.check(
         lib.mxgg_quant_dim1(
             x2.data_ptr(), M, C, x2.stride(0),
             ends.data_ptr() if ends is not None else None, E or 0, cap,
-            qt.data_ptr(), qt.stride(0), buf.data_ptr(), buf.stride(0),
-            _lib.SCALES_BLOCK_MAJOR,
+            qt.data_ptr(), qt.stride(0), buf.data_ptr(), max(buf.stride(0), 1), layout,
             ends_pad.data_ptr() if ends_pad is not None else None,
             _mode(scaling_mode), _stream_ptr(x),
         ),
         "quant_dim1",
     )
-    st = buf[:, :C].t()  # logical [C, cap/32], block-major storage
+    # logical [C, cap/32]: the buffer itself (row-major) or a view of it
+    st = buf if layout == _lib.SCALES_ROW_MAJOR else buf[:, :C].t()
     return qt, st, _mark_ends(ends_pad)
 
 

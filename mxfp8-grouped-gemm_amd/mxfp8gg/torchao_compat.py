@@ -22,19 +22,27 @@ def _e8m0_view(s: torch.Tensor) -> torch.Tensor:
     return s.view(_E8M0) if _E8M0 is not None else s
 
 
-def triton_to_mxfp8_dim0(x: torch.Tensor, inner_block_size: int = 32, scaling_mode="floor"):
-    """torchao-named row-wise cast: returns (data e4m3 like x, scales e8m0 [..., K/32])."""
+def triton_to_mxfp8_dim0(x: torch.Tensor, inner_block_size: int = 32, scaling_mode="floor",
+                         scale_layout: str = "row"):
+    """torchao-named row-wise cast: returns (data e4m3 like x, scales e8m0 [..., K/32]).
+
+    The scales are contiguous (scale_layout "row", as torchao returns them:
+    .view() and reshape work); a grouped GEMM call then re-lays them
+    block-major on the device (1/32 of the payload's bytes).  "block" returns
+    the block-major view the GEMM reads in place."""
     if inner_block_size != 32:
         raise ValueError("only 32-element blocks are supported (MX block size)")
-    q, s = ops.to_mxfp8_dim0(x, scaling_mode)
+    q, s = ops.to_mxfp8_dim0(x, scaling_mode, scale_layout)
     return q, _e8m0_view(s)
 
 
-def triton_to_mxfp8_dim1(x: torch.Tensor, inner_block_size: int = 32, scaling_mode="floor"):
+def triton_to_mxfp8_dim1(x: torch.Tensor, inner_block_size: int = 32, scaling_mode="floor",
+                         scale_layout: str = "row"):
     """torchao-named column-wise cast of a row-major [M, K] tensor.
 
     Returns (data, scales): data is the [M, K] logical view of column-major
-    storage (a [K, M] row-major buffer transposed), scales e8m0 [K, M/32].
+    storage (a [K, M] row-major buffer transposed), scales e8m0 [K, M/32],
+    contiguous (scale_layout "row"; "block" as in triton_to_mxfp8_dim0).
     M must be a multiple of 32 (no grouping: one block sequence per column).
     """
     if inner_block_size != 32:
@@ -43,7 +51,7 @@ def triton_to_mxfp8_dim1(x: torch.Tensor, inner_block_size: int = 32, scaling_mo
     M = x2.shape[0]
     if M % 32 != 0:
         raise ValueError(f"dim1 cast needs rows % 32 == 0, got {M}")
-    qt, st, _ = ops.to_mxfp8_dim1(x2, None, scaling_mode)
+    qt, st, _ = ops.to_mxfp8_dim1(x2, None, scaling_mode, scale_layout)
     return qt.t(), _e8m0_view(st)
 
 

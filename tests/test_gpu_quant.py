@@ -115,9 +115,33 @@ def test_dim1_ungrouped_and_torchao_layout(gpu):
     assert d.shape == (96, 64) and d.stride() == (1, 96)   # column-major [M, K]
     assert torch.equal(d.t().view(torch.uint8), qt.view(torch.uint8))
     assert torch.equal(sc.view(torch.uint8), st)
+    assert sc.is_contiguous() and sc.shape == (64, 3)     # torchao's contiguous scales
     d0, s0 = mxfp8gg.triton_to_mxfp8_dim0(x, scaling_mode="floor")
     rq0, rs0 = O.quant_dim0(bits(x), O.FLOOR)
     assert np.array_equal(u8(d0), rq0) and np.array_equal(u8(s0), rs0)
+    assert s0.is_contiguous() and s0.view(-1).numel() == 96 * 2
+    # the block-major view on request, same bytes
+    _, s0b = mxfp8gg.triton_to_mxfp8_dim0(x, scaling_mode="floor", scale_layout="block")
+    assert s0b.stride(0) == 1 and torch.equal(s0b.view(torch.uint8), s0.view(torch.uint8))
+
+
+@pytest.mark.parametrize("shape", [(3, 40, 128), (77, 64)])
+def test_row_major_scale_layout_option(gpu, shape):
+    g = torch.Generator(device=gpu).manual_seed(17)
+    x = torch.randn(*shape, generator=g, device=gpu).to(torch.bfloat16)
+    q, s = ops.to_mxfp8_dim0(x)
+    qr, sr = ops.to_mxfp8_dim0(x, scale_layout="row")
+    assert sr.is_contiguous() and sr.shape == s.shape
+    assert torch.equal(q.view(torch.uint8), qr.view(torch.uint8)) and torch.equal(s, sr)
+    x2 = x.reshape(-1, shape[-1])
+    ends = torch.tensor([x2.shape[0] // 3, x2.shape[0]], dtype=torch.int32, device=gpu)
+    qt, st, pad = ops.to_mxfp8_dim1(x2, ends)
+    qtr, str_, padr = ops.to_mxfp8_dim1(x2, ends, scale_layout="row")
+    assert str_.is_contiguous() and str_.shape == st.shape
+    assert torch.equal(qt.view(torch.uint8), qtr.view(torch.uint8)) and torch.equal(st, str_)
+    assert torch.equal(pad, padr)
+    with pytest.raises(ValueError, match="scale_layout"):
+        ops.to_mxfp8_dim0(x, scale_layout="col")
 
 
 def test_dim1_nan_inf_blocks(gpu):
