@@ -528,15 +528,19 @@ def stored_traffic():
     return t.get("hbm_bytes_per_launch"), "rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated"
 
 
-def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, budget_s=12.0):
+def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, gpu_out=None, budget_s=12.0):
     """The reference's CPU path on a bounded sample of the workload: whole
-    experts of C2, in order, until `budget_s` of CPU work has run."""
+    experts of C2, in order, until `budget_s` of CPU work has run.  With the
+    GPU's output of the same launch, also the largest error of its sampled
+    rows against that CPU result, max|gpu - cpu| / max|cpu| per expert (the
+    normwise measure of the parity tests, bound 1e-2)."""
     import torch
     from oracle import oracle as O
 
     done_tokens = 0
     t_total = 0.0
     experts = 0
+    worst = 0.0
     b = 0
     for g, e in enumerate(ends_np.tolist()):
         if e > b:
@@ -545,15 +549,18 @@ def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, budget_s=12.0):
             w_q = wq[g:g + 1].cpu().view(torch.uint8)
             w_s = ws[g:g + 1].cpu()
             t0 = time.perf_counter()
-            O.cpu_baseline_fwd(a_q, a_s, w_q, w_s, torch.tensor([e - b], dtype=torch.int32))
+            ref = O.cpu_baseline_fwd(a_q, a_s, w_q, w_s, torch.tensor([e - b], dtype=torch.int32))
             t_total += time.perf_counter() - t0
+            if gpu_out is not None:
+                got = gpu_out[b:e].float().cpu()
+                worst = max(worst, float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30)))
             done_tokens += e - b
             experts += 1
         b = e
         if t_total >= budget_s:
             break
     tflops = 2.0 * done_tokens * n * k / t_total / 1e12
-    return {
+    res = {
         "value": round(tflops, 4),
         "unit": "TFLOPS",
         "cores": torch.get_num_threads(),
@@ -561,6 +568,9 @@ def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, budget_s=12.0):
         "sample": f"C2 experts 0..{experts - 1} ({done_tokens} tokens x N={n} x K={k}): "
                   f"dequantise e4m3*2^(b-127) to fp32, per-group fp32 matmul, {t_total:.1f} s",
     }
+    if gpu_out is not None:
+        res["gpu_max_rel_err"] = float(f"{worst:.3e}")
+    return res
 
 
 def main():
@@ -736,7 +746,7 @@ def main():
     cpu = None
     if not args.no_cpu and args.only == "all":
         log("CPU baseline (reference CPU path on a bounded sample)")
-        cpu = cpu_baseline(xq, xs, wq, ws, ends_np, N, K)
+        cpu = cpu_baseline(xq, xs, wq, ws, ends_np, N, K, gpu_out=out)
 
     line = {
         "metric": "MXFP8 grouped-GEMM TFLOPS fwd & wgrad, DSv3 32-expert shape; % of MFMA peak",
