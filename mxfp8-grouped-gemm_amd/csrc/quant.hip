@@ -213,6 +213,12 @@ __device__ __forceinline__ void token_payload(const uint4 (&v)[16], const uint32
   }
 }
 
+// Grid order of the token-axis cast (see k_quant_dim1).
+template <int GATHER>
+__host__ __device__ __forceinline__ bool feature_fastest(int64_t cap) {
+  return GATHER == 0 && (cap + 127) / 128 <= 65535;
+}
+
 struct RowOut {
   uint8_t* q;     // [rows, cols] row-wise payload
   uint8_t* s;     // scale bytes, byte (r, b) at s[r * s_row + b * s_blk]
@@ -234,8 +240,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATHER ? 4 
   __shared__ int32_t pend_s[kMaxGroups];
   const int lane = threadIdx.x & 63;
   const int tg = lane & 7, fg = lane >> 3;
-  const int64_t P = (int64_t)blockIdx.x * 128 + 16 * tg;
-  const int f = blockIdx.y * 256 + (threadIdx.x >> 6) * 64 + 8 * fg;
+  // Feature blocks vary fastest over the grid for token-order rows (the
+  // workgroups reading the 256-feature pieces of the same 128 rows run
+  // together: +8% on C4's dY, +4% dual), positions fastest for gathered rows
+  // (measured 17% faster that way) and when the positions outgrow the grid's
+  // y range (dim1_grid makes the same choice).
+  const bool ffast = feature_fastest<GATHER>(rows_pad_cap);
+  const uint32_t pblk = ffast ? blockIdx.y : blockIdx.x;
+  const uint32_t fblk = ffast ? blockIdx.x : blockIdx.y;
+  const int64_t P = (int64_t)pblk * 128 + 16 * tg;
+  const int f = (int)fblk * 256 + (threadIdx.x >> 6) * 64 + 8 * fg;
 
   int64_t tok0 = 0;
   int ntok = 0;
@@ -384,7 +398,8 @@ hipError_t dim1_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
   }
-  dim3 grid((unsigned)((cap + 127) / 128), (unsigned)((cols + 255) / 256));
+  const unsigned pblocks = (unsigned)((cap + 127) / 128), fblocks = (unsigned)((cols + 255) / 256);
+  const dim3 grid = feature_fastest<GATHER>(cap) ? dim3(fblocks, pblocks) : dim3(pblocks, fblocks);
   hipLaunchKernelGGL((k_quant_dim1<MODE, SW, ROW, GATHER>), grid, dim3(256), 0, stream, x, rows,
                      (int)cols, ldx, ends, ends_pad, (int)E, cap, qt, ldqt, st, st_row, st_blk, ro,
                      ga);
