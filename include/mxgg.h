@@ -457,7 +457,8 @@ int mxgg_gather_quant_dual(const void* x, int64_t tokens, int64_t cols, int64_t 
  * without row_scale), read straight from token order: the MXFP8 expert input
  * of a forward-only pass, which needs no token-axis cast.  rows = rows of the
  * routed layout (every row is written; padding rows as zero blocks); every
- * other argument as mxgg_quant_dim0.
+ * other argument as mxgg_quant_dim0.  cols <= 65535 * 512 (else
+ * MXGG_ERR_UNSUPPORTED).
  */
 int mxgg_gather_quant_dim0(const void* x, int64_t tokens, int64_t cols, int64_t ldx,
                            const int32_t* src, int64_t topk, int64_t rows, void* q, int64_t ldq,

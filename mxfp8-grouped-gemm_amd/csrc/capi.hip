@@ -847,6 +847,10 @@ int mxgg_gather_quant_dim0(const void* x, int64_t tokens, int64_t cols, int64_t 
                             scale_layout, scale_mode);
   if (st != MXGG_OK || rows == 0 || cols == 0) return st;
   if (!src) return set_error(MXGG_ERR_INVALID_ARGUMENT, "gather_quant_dim0: null src");
+  // the column blocks of 512 form the grid's y dimension
+  if ((cols + 511) / 512 > 65535)
+    return set_error(MXGG_ERR_UNSUPPORTED, "gather_quant_dim0: cols=%lld above 65535 * 512",
+                     (long long)cols);
   return check_launch(
       launch_gather_quant_dim0(static_cast<const uint16_t*>(x), tokens, ldx, src, (int)topk, rows,
                                cols, static_cast<uint8_t*>(q), ldq, static_cast<uint8_t*>(scales),

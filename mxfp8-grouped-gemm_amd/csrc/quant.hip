@@ -44,11 +44,15 @@ __global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__
                                                     int64_t s_blk, Gather ga) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int cc = blockIdx.x * 64 + lane;  // chunk column
+  // column blocks vary fastest over the grid for token-order rows, row blocks
+  // for gathered rows (measured 7% faster at C5's routing)
+  const uint32_t cb = GATHER ? blockIdx.y : blockIdx.x, rb = GATHER ? blockIdx.x : blockIdx.y;
+  const uint32_t nrb = GATHER ? gridDim.x : gridDim.y;
+  const int cc = cb * 64 + lane;          // chunk column
   const bool col_ok = cc < cols8;         // whole quads share col_ok (cols8 % 4 == 0)
   // block-major scales with 8-byte aligned block columns: one store per quad
   const bool pack_s = s_row == 1 && ((s_blk | (int64_t)(uintptr_t)s) & 7) == 0;
-  for (int64_t r0 = (int64_t)blockIdx.y * 32 + wave * 8; r0 < rows; r0 += (int64_t)gridDim.y * 32) {
+  for (int64_t r0 = (int64_t)rb * 32 + wave * 8; r0 < rows; r0 += (int64_t)nrb * 32) {
     uint4 v[8];
     if (GATHER) {
       int32_t sl[8];
@@ -382,7 +386,9 @@ hipError_t dim0_impl(const uint16_t* x, int64_t rows, int64_t cols, int64_t ldx,
                      int64_t ldq, uint8_t* s, int64_t s_row, int64_t s_blk, const Gather& ga,
                      hipStream_t stream) {
   const int cols8 = (int)(cols / 8);
-  dim3 grid((cols8 + 63) / 64, (unsigned)std::min<int64_t>((rows + 31) / 32, 65535));
+  const unsigned cblocks = (unsigned)((cols8 + 63) / 64);
+  const dim3 grid = GATHER ? dim3((unsigned)std::min<int64_t>((rows + 31) / 32, 1 << 20), cblocks)
+                           : dim3(cblocks, (unsigned)std::min<int64_t>((rows + 31) / 32, 65535));
   hipLaunchKernelGGL((k_quant_dim0<MODE, SW, GATHER>), grid, dim3(256), 0, stream, x, rows, cols8,
                      ldx, q, ldq, s, s_row, s_blk, ga);
   return hipGetLastError();

@@ -441,6 +441,8 @@ def _gather_dim0(lib, **kw):
     (dict(layout=7), _lib.ERR_INVALID_ARGUMENT),
     (dict(x=FAKE + 4), _lib.ERR_ALIGNMENT),
     (dict(q=FAKE + 8), _lib.ERR_ALIGNMENT),
+    # 65536 column blocks of 512: past the grid's y range
+    (dict(cols=65536 * 512, ldx=65536 * 512, ldq=65536 * 512), _lib.ERR_UNSUPPORTED),
 ])
 def test_gather_quant_dim0_rejects(lib, kw, status):
     assert _gather_dim0(lib, **kw) == status
