@@ -168,6 +168,21 @@ def test_dim1_c4_sampled_features(gpu):
     assert np.array_equal(u8(qt[idx]), rq) and np.array_equal(u8(st[idx]), rs)
 
 
+def test_dim1_past_the_grid_y_range_equals_transposed_dim0(gpu):
+    # 2^23 tokens: 65536 blocks of 128 positions, one more than the grid's y
+    # range, so the cast takes its positions-fastest grid.  One group: the
+    # token-axis cast is then the row-wise cast of x transposed (independent
+    # kernel, itself pinned against the oracle above).
+    M, C = 1 << 23, 32
+    g = torch.Generator(device=gpu).manual_seed(18)
+    x = torch.randn(M, C, generator=g, device=gpu).to(torch.bfloat16)
+    qt, st, pad = ops.to_mxfp8_dim1(x)
+    assert pad is None and qt.shape == (C, M) and (M + 127) // 128 > 65535
+    q0, s0 = ops.to_mxfp8_dim0(x.t().contiguous())
+    assert torch.equal(qt.view(torch.uint8), q0.view(torch.uint8))
+    assert torch.equal(st, s0)
+
+
 # ---------------------------------------------------------------------------
 # dual cast: both casts of one tensor from a single read
 # ---------------------------------------------------------------------------

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import mxfp8gg
-from mxfp8gg import workloads
+from mxfp8gg import _lib, ops, workloads
 from oracle import oracle as O
 from tests._helpers import bits, from_bits, u8
 
@@ -126,6 +126,32 @@ def test_gather_to_mxfp8_dim0_matches_oracle(gpu, mode_name, mode, T, K, E, H, p
     q2, s2 = mxfp8gg.to_mxfp8_dim0(mxfp8gg.gather_rows(x, plan), mode_name)
     assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8))
     assert torch.equal(s.contiguous(), s2.contiguous())
+
+
+def test_gather_to_mxfp8_dim0_past_one_grid_pass(gpu):
+    # more routed rows than one pass of the gathered cast's grid (2^20 blocks
+    # of 32 rows): the rows past it come from the grid-stride loop.  Every
+    # routed row must be the cast of its token's row (zero for padding).
+    T, K, H = 1000, 4, 32
+    rows = (1 << 25) + 96
+    g = torch.Generator(device=gpu).manual_seed(19)
+    x = torch.randn(T, H, generator=g, device=gpu).to(torch.bfloat16)
+    src = torch.randint(-T * K // 8, T * K, (rows,), generator=g, device=gpu, dtype=torch.int32)
+    src[src < 0] = -1
+    q = torch.zeros((rows, H), dtype=torch.uint8, device=gpu)
+    sbuf = ops._block_major_buffer(rows, H // 32, gpu)
+    lib = _lib.load()
+    st = lib.mxgg_gather_quant_dim0(x.data_ptr(), T, H, H, src.data_ptr(), K, rows, q.data_ptr(), H,
+                                    sbuf.data_ptr(), sbuf.stride(0), _lib.SCALES_BLOCK_MAJOR,
+                                    _lib.SCALE_RCEIL, torch.cuda.current_stream(gpu).cuda_stream)
+    assert st == 0, lib.mxgg_last_error()
+    rq, rs = O.quant_dim0(bits(x), O.RCEIL)
+    # per token: payload row and scale byte, then gathered on the device
+    tq = torch.from_numpy(np.concatenate([rq, np.zeros((1, H), np.uint8)])).to(gpu)
+    ts = torch.from_numpy(np.concatenate([rs[:, 0], np.zeros(1, np.uint8)])).to(gpu)
+    tok = torch.where(src >= 0, src // K, torch.full_like(src, T)).long()
+    assert torch.equal(q, tq[tok])
+    assert torch.equal(sbuf[0, :rows], ts[tok])
 
 
 @pytest.mark.parametrize("scaled", [False, True])
