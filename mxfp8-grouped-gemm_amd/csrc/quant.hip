@@ -163,11 +163,12 @@ __global__ __launch_bounds__(256) void k_pad_ends(const int32_t* __restrict__ en
 
 // ---------------------------------------------------------------------------
 // dim1.  A wave covers 128 padded token positions x 64 features; lane
-// (tg = lane % 8, fg = lane / 8) owns positions 16*tg .. +15 of the tile and
+// (fg = lane % 8, tg = lane / 8) owns positions 16*tg .. +15 of the tile and
 // features 8*fg .. +7.  It loads its 16 token rows as 16-byte vectors (eight
-// lanes read one whole 128-byte line of a row), takes each feature's amax over
-// its 16 tokens (two features at once with packed 16-bit max), combines it
-// with lane tg^1 (the other half of the 32-token block), and writes 16 payload
+// consecutive lanes read one whole 128-byte line of a row), takes each
+// feature's amax over its 16 tokens (two features at once with packed 16-bit
+// max), combines it with lane tg^1 = lane^8 (the other half of the 32-token
+// block; a DPP rotation by 8 within the 16-lane row), and writes 16 payload
 // bytes per feature (eight lanes write one whole 128-byte line of an output
 // row).  No LDS transpose is needed.  Padded positions map to tokens through
 // the padded group ends; a run of 16 never straddles two groups because every
@@ -176,9 +177,11 @@ __global__ __launch_bounds__(256) void k_pad_ends(const int32_t* __restrict__ en
 //
 // ROW (the dual cast) also writes the row-wise cast of the same data from the
 // same registers: for each of its tokens a lane holds one 8-feature chunk, the
-// four lanes fg = 4k .. 4k+3 hold a 32-feature block (amax over xor-8 / xor-16
-// shuffles, two tokens per shuffle).  Every token inside a group is covered by
-// exactly one lane run, so each row-wise row is written once.
+// quad fg = 4k .. 4k+3 holds a 32-feature block (amax over two DPP quad
+// permutations, two tokens per step).  Every token inside a group is covered
+// by exactly one lane run, so each row-wise row is written once.  (With the
+// lanes the other way round, tg = lane % 8, the block took two LDS shuffles:
+// the dual cast ran 3% and its gathered forms 12% slower.)
 // ---------------------------------------------------------------------------
 // Row-wise payload of a lane's 16 token chunks (row i at qrow + i * ldq).
 template <int MODE, bool SW, bool ANY>
@@ -243,7 +246,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATHER ? 4 
   __shared__ int32_t ends_s[kMaxGroups];
   __shared__ int32_t pend_s[kMaxGroups];
   const int lane = threadIdx.x & 63;
-  const int tg = lane & 7, fg = lane >> 3;
+  const int fg = lane & 7, tg = lane >> 3;
   // Feature blocks vary fastest over the grid for token-order rows (the
   // workgroups reading the 256-feature pieces of the same 128 rows run
   // together: +8% on C4's dY, +4% dual), positions fastest for gathered rows
@@ -318,8 +321,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATHER ? 4 
       const uint32_t m0 = amax16_of_chunk(v[2 * t]);
       const uint32_t m1 = amax16_of_chunk(v[2 * t + 1]);
       uint32_t m = m0 | (m1 << 16);
-      m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 8));
-      m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 16));
+      m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0xB1, 0xF, 0xF, false));
+      m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x4E, 0xF, 0xF, false));
       rb[2 * t] = e8m0_from_amax16<MODE>(m & 0xFFFFu);
       rb[2 * t + 1] = e8m0_from_amax16<MODE>(m >> 16);
       nan |= (rb[2 * t] == 255u) | (rb[2 * t + 1] == 255u);
@@ -359,7 +362,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATHER ? 4 
       const uint32_t w = k == 0 ? v[i].x : k == 1 ? v[i].y : k == 2 ? v[i].z : v[i].w;
       m = pk_max_u16(m, abs_bf16x2(w));
     }
-    m = pk_max_u16(m, (uint32_t)__shfl_xor((int)m, 1));
+    m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x128, 0xF, 0xF, false));
     bytes[2 * k] = e8m0_from_amax16<MODE>(m & 0xFFFFu);
     bytes[2 * k + 1] = e8m0_from_amax16<MODE>(m >> 16);
     tnan |= (bytes[2 * k] == 255u) | (bytes[2 * k + 1] == 255u);
