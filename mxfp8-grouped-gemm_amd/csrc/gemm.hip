@@ -723,8 +723,7 @@ __device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4
     const uint4 u = *reinterpret_cast<const uint4*>(row + ((16u + (k ^ sw)) << 4));
     const uint4 a = swiglu_a_chunk(g, u);
     uint32_t am = amax16_of_chunk(a);
-    am = max(am, (uint32_t)__shfl_xor((int)am, 1));
-    am = max(am, (uint32_t)__shfl_xor((int)am, 2));
+    am = quad_max(am);
     const uint32_t b = e8m0_from_amax16<MODE>(am);
     const uint2 o = __any(b == 255u) ? encode_chunk8<MODE, false, true>(a, b)
                                      : encode_chunk8<MODE, false, false>(a, b);

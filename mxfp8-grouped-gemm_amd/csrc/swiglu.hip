@@ -106,8 +106,7 @@ __global__ __launch_bounds__(256) void k_swiglu_dim0(
     for (int k = 0; k < 4; ++k) {
       a[k] = swiglu_a_chunk(g[k], u[k]);
       uint32_t am = amax16_of_chunk(a[k]);
-      am = max(am, (uint32_t)__shfl_xor((int)am, 1));
-      am = max(am, (uint32_t)__shfl_xor((int)am, 2));
+      am = quad_max(am);
       b[k] = e8m0_from_amax16<MODE>(am);
       nan |= b[k] == 255u;
     }
