@@ -105,6 +105,9 @@ struct Operand {
   uint32_t hi;
 };
 
+// Cache-policy operand of the buffer store builtins: the nontemporal bit.
+constexpr int kCacheNT = 2;
+
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ uint32_t wave_id() {
@@ -530,11 +533,23 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
                                          uint32_t qend, uint32_t p0, uint32_t pend,
                                          bool accumulate = false) {
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t wave = wave_id();
   const uint32_t wp = wave & 1u, wq = wave >> 1;
   const uint32_t l32 = lane & 31u, h = lane >> 5;
   uint8_t* stage = &sm.ring[0][0] + wave * 32768u;
   const uint32_t p = p0 + wp * 128u + 4u * l32;  // this lane's 4 columns on the way out
+  // fp32 stores of a wave whose 128 rows and 128 columns all lie inside the
+  // output go through one buffer descriptor based at its first row and
+  // column: a per-lane offset fixed for the tile plus a scalar row offset per
+  // store, no guards.
+  const uint32_t qw = q0 + 128u * wq, pw = p0 + 128u * wp;
+  const bool interior = F32 && !accumulate && qw >= qbeg && qw + 128u <= qend &&
+                        pw + 128u <= pend &&
+                        ((reinterpret_cast<uintptr_t>(out) | (uintptr_t)ldo_bytes) & 15u) == 0 &&
+                        ldo_bytes < (int64_t)1 << 24;
+  const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
+      out + (int64_t)qw * ldo_bytes + 4 * (int64_t)pw, (short)0,
+      (int)(128u * (uint32_t)ldo_bytes), 0x00020000);
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
@@ -565,6 +580,15 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
       asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
                    "+v"(v[6]), "+v"(v[7]));
       if constexpr (F32) {
+        if (interior) {
+          // row 2*pass + h of each group of four, 16 bytes per lane
+          const uint32_t voff = (2u * (uint32_t)pass + h) * (uint32_t)ldo_bytes + 16u * l32;
+#pragma unroll
+          for (uint32_t u = 0; u < 8u; ++u)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[u]), rows, voff,
+                                                   4u * (t0 + u) * (uint32_t)ldo_bytes, kCacheNT);
+          continue;
+        }
 #pragma unroll
         for (uint32_t u = 0; u < 8u; ++u) {
           const uint32_t q = q0 + wq * 128u + 4u * (t0 + u) + 2u * (uint32_t)pass + h;
@@ -672,10 +696,21 @@ __device__ __forceinline__ void epilogue_bf16(Smem& sm, const v16f (&acc)[4][4],
                                               uint32_t qend, uint32_t p0, uint32_t pend) {
   stage_bf16_tile(sm, acc);
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t wave = wave_id();
   const uint32_t c = lane & 31u;
   const uint32_t p = p0 + 8u * c;
   const uint8_t* st = &sm.ring[0][0];
+  // A wave whose 64 rows and 256 columns all lie inside the output stores
+  // through one buffer descriptor based at its first row: a per-lane offset
+  // fixed for the tile plus a scalar row offset per store, no guards.
+  const uint32_t qw = q0 + 64u * wave;
+  const bool interior = qw >= qbeg && qw + 64u <= qend && p0 + 256u <= pend &&
+                        ((reinterpret_cast<uintptr_t>(out) | (uintptr_t)ldo_bytes) & 15u) == 0 &&
+                        ldo_bytes < (int64_t)1 << 25;
+  const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
+      out + (int64_t)qw * ldo_bytes + 2 * (int64_t)p0, (short)0,
+      (int)(64u * (uint32_t)ldo_bytes), 0x00020000);
+  const uint32_t voff = (lane >> 5) * (uint32_t)ldo_bytes + 16u * c;
 #pragma unroll
   for (uint32_t i0 = 0; i0 < 32u; i0 += 8u) {
     u32x4 v[8];
@@ -687,6 +722,13 @@ __device__ __forceinline__ void epilogue_bf16(Smem& sm, const v16f (&acc)[4][4],
     // keep the reads here instead of letting them sink into the guarded stores
     asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
                  "+v"(v[6]), "+v"(v[7]));
+    if (interior) {
+#pragma unroll
+      for (uint32_t u = 0; u < 8u; ++u)
+        __builtin_amdgcn_raw_buffer_store_b128(v[u], rows, voff,
+                                               2u * (i0 + u) * (uint32_t)ldo_bytes, kCacheNT);
+      continue;
+    }
 #pragma unroll
     for (uint32_t u = 0; u < 8u; ++u) {
       const uint32_t q = q0 + 64u * wave + 2u * (i0 + u) + (lane >> 5);
