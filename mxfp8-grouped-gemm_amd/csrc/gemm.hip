@@ -443,8 +443,11 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
   read_tail<0>(sm.ring[0], fa, f0);
   // Past the last stage the loads fetch zeros into a slot nobody reads again,
   // and the final head read fetches a stale slot that is never used, so the
-  // loop body has no branches.
-  for (uint32_t s = 0; s < nst; ++s) {
+  // loop body has no branches.  nst >= 1 here (kend > klo); written as a
+  // do-while because a loop that may run zero times made the compiler zero
+  // the 256 accumulators twice per tile, once for the zero-trip path.
+  uint32_t s = 0;
+  do {
     uint8_t* cur = sm.ring[s & 1u];
     uint8_t* nxt = sm.ring[(s & 1u) ^ 1u];
     uint32_t bp, bq;
@@ -499,7 +502,7 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
     mfma1<3, 1>(f1, acc); st.template load_scale<0>(cur, P, k2); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
     mfma1<3, 2>(f1, acc); st.template load_scale<1>(cur, Q, k2); read_p<0>(nxt, fa, f0, 2); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
     mfma1<3, 3>(f1, acc); read_p<0>(nxt, fa, f0, 3); MXGG_FENCE();
-  }
+  } while (++s < nst);
   // Drain the loads past the end before the next tile's prologue reuses the slots.
   wait_barrier<0>();
 }
