@@ -797,6 +797,21 @@ __device__ __forceinline__ void band_decode(uint32_t lid, uint32_t m_tiles, uint
   mt = first + (in - nt * width);
 }
 
+// Largest index i < n with a[i] <= v in a non-decreasing LDS array (a[0] <= v),
+// found by the whole wave at once: one LDS read and a ballot per 64 entries
+// instead of a chain of dependent reads.
+__device__ __forceinline__ int last_le(const int32_t* a, int n, uint32_t v) {
+  const int lane = (int)(threadIdx.x & 63u);
+  int best = 0;
+  for (int base = 0; base < n; base += 64) {
+    const int i = base + lane;
+    const uint64_t m = __ballot(i < n && (uint32_t)a[i] <= v);
+    if (m != 0) best = base + 63 - __clzll((long long)m);
+    if (m != ~0ull) break;
+  }
+  return best;
+}
+
 // Position in the global tile order processed by this workgroup at round
 // `base`: each XCD (workgroups are dealt to the 8 XCDs round-robin) takes a
 // contiguous slice of the round.
@@ -910,12 +925,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
     uint32_t mt, nt;
     band_decode(tile, m_tiles, n_tiles, gm, mt, nt);
     // group of m-tile mt: last g with sched[g] <= mt
-    int lo = 0, hi = E - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if ((uint32_t)sm.sched[mid] <= mt) lo = mid; else hi = mid - 1;
-    }
-    const int g = lo;
+    const int g = last_le(sm.sched, E, mt);
     int32_t gb, ge;
     group_range(sm.gend, g, gb, ge);
     const uint32_t q0 = (uint32_t)(gb & ~3) + (mt - (uint32_t)sm.sched[g]) * kTileQ;
@@ -1101,12 +1111,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
     const uint32_t lid = xcd_slice(base);
     if (lid >= total) break;
     // rank of item lid: last r with items[r] <= lid
-    int lo = 0, hi = E - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if ((uint32_t)sm.items[mid] <= lid) lo = mid; else hi = mid - 1;
-    }
-    const int rank = lo;
+    const int rank = last_le(sm.items, E, lid);
     const int g = sm.order[rank];
     const uint32_t local = lid - (uint32_t)sm.items[rank];
     const uint32_t chunk = local / per_expert;  // consecutive items share a token range
