@@ -199,6 +199,29 @@ def test_rows_outside_groups_untouched_and_each_row_written(gpu):
     assert torch.isnan(out[137:]).all()
 
 
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("col0,pad", [(0, 8), (0, 4), (4, 4)])
+def test_output_inside_a_wider_buffer(gpu, out_dtype, col0, pad):
+    """out as a column slice of a wider buffer.  Waves whose rows and columns
+    lie inside the output store through one buffer range at the output's row
+    stride when rows start 16-byte aligned; bf16 rows off that alignment (pad 4
+    makes the stride 8 mod 16 bytes, col0 4 moves the base) and the waves at
+    ragged group ends or the last column tile (N = 576) take the guarded
+    stores.  Every layout gives the contiguous result bit for bit and leaves
+    the columns outside [col0, col0 + N) untouched."""
+    sizes = [300, 0, 700, 25]
+    M, N, K = sum(sizes), 576, 256
+    a_q, a_s = _rand_q((M, K), gpu, 41)
+    w_q, w_s = _rand_q((len(sizes), N, K), gpu, 42)
+    ends = torch.tensor(np.cumsum(sizes), dtype=torch.int32, device=gpu)
+    args = (a_q.view(torch.float8_e4m3fn), w_q.view(torch.float8_e4m3fn), ends, a_s, w_s)
+    ref = ops.grouped_mm(*args, out_dtype=out_dtype)
+    big = torch.full((M, col0 + N + pad), float("nan"), dtype=out_dtype, device=gpu)
+    got = ops.grouped_mm(*args, out_dtype=out_dtype, out=big[:, col0:col0 + N])
+    assert torch.equal(got.contiguous().view(torch.uint8), ref.view(torch.uint8))
+    assert torch.isnan(big[:, :col0]).all() and torch.isnan(big[:, col0 + N:]).all()
+
+
 def test_scale_bump_doubles_output_exactly(gpu):
     x, w, sizes = workloads.c1(gpu)
     xq, xs = mxfp8gg.to_mxfp8_dim0(x)
