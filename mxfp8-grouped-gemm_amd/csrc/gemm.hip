@@ -569,7 +569,8 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
     }
     // This wave's LDS writes complete before its reads (in-order LDS queue).
     // Reads go out eight at a time, unconditionally (they are always in
-    // bounds), so their latency overlaps; only the global stores are guarded.
+    // bounds), so their latency overlaps; only the global stores of a
+    // boundary wave are guarded.
 #pragma unroll
     for (uint32_t t0 = 0; t0 < 32u; t0 += 8u) {
       v4f v[8];
