@@ -11,9 +11,12 @@ value = 2 * tokens * N * K / step time, in TFLOPS.
 The same run also times, as secondary components: the C3 down-projection
 forward, the C4 weight gradient (fp32 dW), the bf16->MXFP8 casts, and the
 reference's CPU path (dequantise + per-group fp32 matmul with torch on the
-host cores) on a bounded sample of C2.
+host cores) on a bounded sample of C2.  Last, roofline.traffic (HBM bytes per
+C2 launch) is measured by four rocprofv3 counter passes in child processes
+(FETCH_SIZE and WRITE_SIZE over `--only fwd` and over a 1 GiB copy, which
+calibrates both counters); --no-traffic skips them.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-traffic]
                       [--only fwd|wgrad|copy|ref8|refwgrad|c5|routing|dense|small|traffic|hbm]
 """
 import argparse
@@ -463,7 +466,7 @@ def _pmc_pass(only, counter, out_dir):
     import shutil
     import subprocess
     shutil.rmtree(out_dir, ignore_errors=True)
-    cmd = ["timeout", "-s", "KILL", "90", "rocprofv3", "--pmc", counter, "--output-format", "csv",
+    cmd = ["timeout", "-s", "KILL", "75", "rocprofv3", "--pmc", counter, "--output-format", "csv",
            "-d", str(out_dir), "-o", "p", "--", sys.executable, str(ROOT / "bench.py"),
            "--only", only, "--steps", "3", "--warmup", "1", "--no-cpu"]
     log("traffic pass: " + " ".join(cmd))
@@ -484,12 +487,14 @@ def measure_traffic():
     """HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE and
     WRITE_SIZE passes (KiB per dispatch), each scaled by what the same counter
     reads for a 1 GiB device copy, written to profiles/ with the hash of the
-    kernel source it was measured on."""
+    kernel source it was measured on.  Raises if a pass yields no counters."""
     base = ROOT / "gpurun_out" / "traffic"
     res = {}
     for only in ("fwd", "copy"):
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
             res[(only, counter)] = _pmc_pass(only, counter, base / f"{only}_{counter}")
+            if not res[(only, counter)]:
+                raise RuntimeError(f"rocprofv3 {counter} pass over --only {only} gave no counters")
     fwd = {c: next(v for k, v in res[("fwd", c)].items() if "k_grouped_fwd" in k)
            for c in ("FETCH_SIZE", "WRITE_SIZE")}
     cp = {c: max(res[("copy", c)].values()) for c in ("FETCH_SIZE", "WRITE_SIZE")}
@@ -579,6 +584,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 counter passes behind roofline.traffic")
     ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "refwgrad", "c5",
                                        "routing", "dense", "small", "traffic", "hbm"],
                     default="all",
@@ -741,7 +748,20 @@ def main():
         log("C5 as a routed top-8 layer (dispatch, combine)")
         components["routing_c5"] = routing_c5(torch, mxfp8gg, workloads, dev)
 
-    traffic, traffic_note = stored_traffic()
+    traffic, traffic_note = None, "not measured (--no-traffic or a partial run)"
+    if args.only == "all" and not args.no_traffic:
+        # measured in this run: four rocprofv3 counter passes in child processes,
+        # after every timed region above
+        log("roofline traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes of C2 and a copy")
+        try:
+            traffic = measure_traffic()["hbm_bytes_per_launch"]
+            traffic_note = ("measured in this run: rocprofv3 FETCH_SIZE + WRITE_SIZE of the "
+                            "C2 launch, each scaled by the same counter over a 1 GiB copy")
+        except Exception as exc:  # profiler missing or refused: fall back, say so
+            log(f"traffic passes failed: {exc}")
+            traffic, traffic_note = stored_traffic()
+    elif args.only != "all":
+        traffic, traffic_note = stored_traffic()
 
     cpu = None
     if not args.no_cpu and args.only == "all":
