@@ -194,6 +194,18 @@ __device__ __forceinline__ uint2 encode_chunk8(const uint4& v, uint32_t b) {
       encode4_sel<MODE, SW, ANY>(bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w), b));
 }
 
+// Sixteen scale bytes b[0..15] (one per word) written to p..p+15 as one
+// 16-byte store at any byte alignment: gfx9 global stores take unaligned
+// addresses (the compiler lowers a 16-byte memcpy to one global_store_dwordx4
+// for this target), where byte stores would cost 16 store instructions.
+__device__ __forceinline__ void store_scale_bytes16(uint8_t* p, const uint32_t (&b)[16]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    w[k] = b[4 * k] | (b[4 * k + 1] << 8) | (b[4 * k + 2] << 16) | (b[4 * k + 3] << 24);
+  __builtin_memcpy(p, w, 16);
+}
+
 // Two floats rounded to bf16 (round to nearest even, v_cvt_pk_bf16_f32) and
 // packed into one word, `lo` in bits 0-15.  Finite and infinite values round as
 // torch's float -> bfloat16 conversion does; a NaN stays a NaN.

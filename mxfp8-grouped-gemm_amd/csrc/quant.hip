@@ -334,12 +334,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATHER ? 4 
       row_payload<MODE, SW, false>(v, rb, qrow, ro.ldq, ntok);
     if ((fg & 3) == 0 && ntok > 0) {
       uint8_t* sp = ro.s + tok0 * ro.s_row + (int64_t)(f >> 5) * ro.s_blk;
-      if (ro.s_row == 1 && ntok == 16 && (reinterpret_cast<uintptr_t>(sp) & 15u) == 0) {
-        uint32_t w[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          w[k] = rb[4 * k] | (rb[4 * k + 1] << 8) | (rb[4 * k + 2] << 16) | (rb[4 * k + 3] << 24);
-        *reinterpret_cast<uint4*>(sp) = make_uint4(w[0], w[1], w[2], w[3]);
+      if (ro.s_row == 1 && ntok == 16) {
+        store_scale_bytes16(sp, rb);
       } else {
 #pragma unroll
         for (int i = 0; i < 16; ++i)

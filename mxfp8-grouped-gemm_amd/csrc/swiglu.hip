@@ -241,15 +241,12 @@ __device__ __forceinline__ void row_wise_payload(const uint2 (&v)[16], const uin
 }
 
 // Writes n <= 16 scale bytes b[j] at p[j * stride], as one 16-byte store when
-// all sixteen are contiguous and aligned.
+// all sixteen are contiguous (at any alignment: a run of 16 tokens starts
+// wherever its group does).
 __device__ __forceinline__ void store_scale16(uint8_t* p, int64_t stride, const uint32_t (&b)[16],
                                               int n) {
-  if (stride == 1 && n == 16 && (reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
-    uint32_t w[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      w[k] = b[4 * k] | (b[4 * k + 1] << 8) | (b[4 * k + 2] << 16) | (b[4 * k + 3] << 24);
-    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  if (stride == 1 && n == 16) {
+    store_scale_bytes16(p, b);
   } else {
 #pragma unroll
     for (int j = 0; j < 16; ++j)
