@@ -71,8 +71,19 @@ __device__ __forceinline__ void swiglu_dim0_store(const uint4 (&a)[4], const uin
     const uint2 o = encode_chunk8<MODE, SW, ANY>(a[k], b[k]);
     if (col_ok && r < rows) {
       *reinterpret_cast<uint2*>(q + r * ldq + (int64_t)cc * 8) = o;
-      if ((lane & 3) == 0) s[r * s_row + (int64_t)(cc >> 2) * s_blk] = (uint8_t)b[k];
       if (a_out != nullptr) *reinterpret_cast<uint4*>(a_out + r * lda + (int64_t)cc * 8) = a[k];
+    }
+  }
+  // the quad's scale bytes of rows r0 .. r0+3: contiguous in block-major
+  // storage (one 4-byte store), else one byte per row
+  if (col_ok && (lane & 3) == 0) {
+    uint8_t* sp = s + (int64_t)(cc >> 2) * s_blk;
+    if (s_row == 1 && r0 + 4 <= rows && (reinterpret_cast<uintptr_t>(sp + r0) & 3u) == 0) {
+      *reinterpret_cast<uint32_t*>(sp + r0) = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (r0 + k < rows) sp[(r0 + k) * s_row] = (uint8_t)b[k];
     }
   }
 }
