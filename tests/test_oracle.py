@@ -51,7 +51,8 @@ def _enc(vals):
 def test_e4m3_encode_all_bf16_patterns():
     bits = np.arange(65536, dtype=np.uint32) << 16
     vals = bits.view(np.float32)
-    got = _enc(vals.astype(np.float64))
+    with np.errstate(invalid="ignore"):  # the sweep includes every NaN pattern
+        got = _enc(vals.astype(np.float64))
     ref = torch_e4m3(vals)
     assert np.array_equal(got, ref)
 
