@@ -488,13 +488,14 @@ def measure_traffic():
     WRITE_SIZE passes (KiB per dispatch), each scaled by what the same counter
     reads for a 1 GiB device copy, written to profiles/ with the hash of the
     kernel source it was measured on.  Raises if a pass yields no counters."""
-    base = ROOT / "gpurun_out" / "traffic"
+    import tempfile
     res = {}
-    for only in ("fwd", "copy"):
-        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-            res[(only, counter)] = _pmc_pass(only, counter, base / f"{only}_{counter}")
-            if not res[(only, counter)]:
-                raise RuntimeError(f"rocprofv3 {counter} pass over --only {only} gave no counters")
+    with tempfile.TemporaryDirectory(prefix="mxgg_traffic_", dir="/tmp") as tmp:
+        for only in ("fwd", "copy"):
+            for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+                res[(only, counter)] = _pmc_pass(only, counter, Path(tmp) / f"{only}_{counter}")
+                if not res[(only, counter)]:
+                    raise RuntimeError(f"rocprofv3 {counter} pass over --only {only} gave no counters")
     fwd = {c: next(v for k, v in res[("fwd", c)].items() if "k_grouped_fwd" in k)
            for c in ("FETCH_SIZE", "WRITE_SIZE")}
     cp = {c: max(res[("copy", c)].values()) for c in ("FETCH_SIZE", "WRITE_SIZE")}
