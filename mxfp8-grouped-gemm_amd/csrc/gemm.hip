@@ -938,7 +938,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
     P.ld = (uint32_t)args.ldw;
     P.row0 = p0;
     P.hi = SWIGLU ? (uint32_t)args.N / 2u : 128u;
-    Q.data = make_desc(args.a, (uint32_t)((int64_t)(M - 1) * args.lda + K));
+    // The A range ends at the group's last row (ge >= 1: empty groups have no
+    // tiles), so the rows of a partial m-tile past the group end load as zeros
+    // instead of the next expert's rows: no fetch, and the matrix cores run
+    // on zeros there (C2 +2%, C3 +1%; those rows are never stored).
+    Q.data = make_desc(args.a, (uint32_t)((int64_t)(__builtin_amdgcn_readfirstlane(ge) - 1) *
+                                              args.lda + K));
     Q.ld = (uint32_t)args.lda;
     Q.row0 = q0;
     Q.hi = 128u;
