@@ -199,6 +199,29 @@ def test_rows_outside_groups_untouched_and_each_row_written(gpu):
     assert torch.isnan(out[137:]).all()
 
 
+@pytest.mark.parametrize("scaled", [True, False])
+def test_rows_past_the_last_group_never_reach_the_output(gpu, scaled):
+    # A's rows past the last group end hold NaN codes (0x7F) and NaN scales
+    # (0xFF); the last group's partial m-tile spans them.  Every row inside a
+    # group matches the oracle on the clean rows, and the rows past the end
+    # keep the sentinel.
+    sizes = [100, 37]
+    M, N, K = 300, 256, 256
+    a_q, a_s = _rand_q((M, K), gpu, 33)
+    w_q, w_s = _rand_q((2, N, K), gpu, 34)
+    a_q[137:] = 0x7F
+    a_s[137:] = 0xFF
+    ends = workloads.ends_of(sizes)
+    out = torch.full((M, N), 7.0, dtype=torch.bfloat16, device=gpu)
+    ops.grouped_mm(a_q.view(torch.float8_e4m3fn), w_q.view(torch.float8_e4m3fn),
+                   torch.from_numpy(ends).to(gpu), a_s if scaled else None,
+                   w_s if scaled else None, out=out)
+    ref = O.grouped_fwd(u8(a_q[:137]), u8(a_s[:137]) if scaled else None, u8(w_q),
+                        u8(w_s) if scaled else None, ends)
+    assert_close_to_oracle(out[:137], ref)
+    assert torch.all(out[137:] == 7.0)
+
+
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("col0,pad", [(0, 8), (0, 4), (4, 4)])
 def test_output_inside_a_wider_buffer(gpu, out_dtype, col0, pad):
