@@ -396,6 +396,28 @@ int mxgg_grouped_wgrad_split(const void* go_t, int64_t ldgo, const void* go_scal
                              void* dw, int out_dtype, int64_t split_tokens,
                              void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * mxgg_grouped_wgrad (workspace == NULL) or mxgg_grouped_wgrad_split
+ * (workspace != NULL) writing dW[g][n][k] at element
+ * g * ld_dw_expert + n * ld_dw_row + k of dw instead of a contiguous
+ * [E, N, K] (ld_dw_row >= K, ld_dw_expert >= (N - 1) * ld_dw_row + K when
+ * num_groups > 1, both multiples of 4).  A call over a range of feature rows
+ * (rows n0.. of go_t and its scales, or rows k0.. of ia_t and its scales)
+ * writes exactly that slice of a larger dW, which is how operands past the
+ * 2 GiB buffer range are run: in feature-row chunks, each a whole contraction
+ * over every token, so the result equals one launch's.  Replaces the same
+ * reference interface, wgrad_fused.py:34-71 (whose per-group restacking,
+ * :44-62, has no operand-size limit).
+ */
+int mxgg_grouped_wgrad_strided(const void* go_t, int64_t ldgo, const void* go_scales_t,
+                               int64_t ldgos, const void* ia_t, int64_t ldia,
+                               const void* ia_scales_t, int64_t ldias,
+                               const int32_t* group_ends, int64_t num_groups,
+                               int64_t M, int64_t N, int64_t K,
+                               void* dw, int64_t ld_dw_expert, int64_t ld_dw_row,
+                               int out_dtype, int64_t split_tokens,
+                               void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Token routing of a top-k MoE layer on one GPU (the layer's dispatch and
  * combine around the expert GEMMs).  A slot is one (token, k) pair,

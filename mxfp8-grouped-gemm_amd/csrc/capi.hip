@@ -626,8 +626,8 @@ int mxgg_grouped_fwd_split_noalloc(const void* a, int64_t lda, const void* a_sca
 static int grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, int64_t ldgos,
                          const void* ia_t, int64_t ldia, const void* ia_scales_t, int64_t ldias,
                          const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t N,
-                         int64_t K, void* dw, int out_dtype, int64_t split_tokens,
-                         void* workspace, void* stream) {
+                         int64_t K, void* dw, int64_t ldw_e, int64_t ldw_n, int out_dtype,
+                         int64_t split_tokens, void* workspace, void* stream) {
   if (out_dtype != MXGG_OUT_BF16 && out_dtype != MXGG_OUT_F32)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_wgrad: unknown out_dtype %d", out_dtype);
   if (M < 0 || N < 0 || K < 0)
@@ -675,6 +675,13 @@ static int grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t
   const int esz = out_dtype == MXGG_OUT_F32 ? 4 : 2;
   if ((reinterpret_cast<uintptr_t>(dw) % (esz * 4)) != 0 || K % 4 != 0)
     return set_error(MXGG_ERR_ALIGNMENT, "grouped_wgrad: dw must be vector aligned, K % 4 == 0");
+  if (ldw_n < K || ldw_e < 0 || (num_groups > 1 && ldw_e < (N - 1) * ldw_n + K))
+    return set_error(MXGG_ERR_SHAPE,
+                     "grouped_wgrad: dW strides (expert %lld, row %lld) overlap an [N=%lld, "
+                     "K=%lld] block",
+                     (long long)ldw_e, (long long)ldw_n, (long long)N, (long long)K);
+  if (ldw_n % 4 != 0 || ldw_e % 4 != 0)
+    return set_error(MXGG_ERR_ALIGNMENT, "grouped_wgrad: dW strides must be multiples of 4");
   if ((N - 1) * ldgo + M > kMaxBufferBytes || (K - 1) * ldia + M > kMaxBufferBytes)
     return set_error(MXGG_ERR_UNSUPPORTED, "grouped_wgrad: operand larger than 2 GiB");
   if (ldgo > kMaxRowStride || ldia > kMaxRowStride)
@@ -692,6 +699,8 @@ static int grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t
   args.ldgos = scaled ? ldgos : 0;
   args.ldia = ldia;
   args.ldias = scaled ? ldias : 0;
+  args.ldw_e = ldw_e;
+  args.ldw_n = ldw_n;
   args.M = (int32_t)M;
   args.N = (int32_t)N;
   args.K = (int32_t)K;
@@ -709,8 +718,8 @@ int mxgg_grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t, 
                        const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t N,
                        int64_t K, void* dw, int out_dtype, int64_t split_tokens, void* stream) {
   return grouped_wgrad(go_t, ldgo, go_scales_t, ldgos, ia_t, ldia, ia_scales_t, ldias,
-                       group_ends, num_groups, M, N, K, dw, out_dtype, split_tokens, nullptr,
-                       stream);
+                       group_ends, num_groups, M, N, K, dw, N * K, K, out_dtype, split_tokens,
+                       nullptr, stream);
 }
 
 int64_t mxgg_grouped_wgrad_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t num_groups,
@@ -719,12 +728,13 @@ int64_t mxgg_grouped_wgrad_workspace_bytes(int64_t M, int64_t N, int64_t K, int6
   return wgrad_split_workspace_bytes(M, N, K, num_groups, split_tokens);
 }
 
-int mxgg_grouped_wgrad_split(const void* go_t, int64_t ldgo, const void* go_scales_t,
-                             int64_t ldgos, const void* ia_t, int64_t ldia,
-                             const void* ia_scales_t, int64_t ldias, const int32_t* group_ends,
-                             int64_t num_groups, int64_t M, int64_t N, int64_t K, void* dw,
-                             int out_dtype, int64_t split_tokens, void* workspace,
-                             int64_t workspace_bytes, void* stream) {
+static int grouped_wgrad_split(const void* go_t, int64_t ldgo, const void* go_scales_t,
+                               int64_t ldgos, const void* ia_t, int64_t ldia,
+                               const void* ia_scales_t, int64_t ldias,
+                               const int32_t* group_ends, int64_t num_groups, int64_t M,
+                               int64_t N, int64_t K, void* dw, int64_t ldw_e, int64_t ldw_n,
+                               int out_dtype, int64_t split_tokens, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
   if (split_tokens <= 0 || split_tokens % 128 != 0 || split_tokens > INT32_MAX)
     return set_error(MXGG_ERR_INVALID_ARGUMENT,
                      "grouped_wgrad_split: split_tokens=%lld must be a positive multiple of 128",
@@ -739,8 +749,35 @@ int mxgg_grouped_wgrad_split(const void* go_t, int64_t ldgo, const void* go_scal
   if (!aligned16(workspace))
     return set_error(MXGG_ERR_ALIGNMENT, "grouped_wgrad_split: workspace must be 16-byte aligned");
   return grouped_wgrad(go_t, ldgo, go_scales_t, ldgos, ia_t, ldia, ia_scales_t, ldias,
-                       group_ends, num_groups, M, N, K, dw, out_dtype, split_tokens, workspace,
-                       stream);
+                       group_ends, num_groups, M, N, K, dw, ldw_e, ldw_n, out_dtype, split_tokens,
+                       workspace, stream);
+}
+
+int mxgg_grouped_wgrad_split(const void* go_t, int64_t ldgo, const void* go_scales_t,
+                             int64_t ldgos, const void* ia_t, int64_t ldia,
+                             const void* ia_scales_t, int64_t ldias, const int32_t* group_ends,
+                             int64_t num_groups, int64_t M, int64_t N, int64_t K, void* dw,
+                             int out_dtype, int64_t split_tokens, void* workspace,
+                             int64_t workspace_bytes, void* stream) {
+  return grouped_wgrad_split(go_t, ldgo, go_scales_t, ldgos, ia_t, ldia, ia_scales_t, ldias,
+                             group_ends, num_groups, M, N, K, dw, N * K, K, out_dtype,
+                             split_tokens, workspace, workspace_bytes, stream);
+}
+
+int mxgg_grouped_wgrad_strided(const void* go_t, int64_t ldgo, const void* go_scales_t,
+                               int64_t ldgos, const void* ia_t, int64_t ldia,
+                               const void* ia_scales_t, int64_t ldias,
+                               const int32_t* group_ends, int64_t num_groups, int64_t M,
+                               int64_t N, int64_t K, void* dw, int64_t ld_dw_expert,
+                               int64_t ld_dw_row, int out_dtype, int64_t split_tokens,
+                               void* workspace, int64_t workspace_bytes, void* stream) {
+  if (workspace == nullptr)
+    return grouped_wgrad(go_t, ldgo, go_scales_t, ldgos, ia_t, ldia, ia_scales_t, ldias,
+                         group_ends, num_groups, M, N, K, dw, ld_dw_expert, ld_dw_row, out_dtype,
+                         split_tokens, nullptr, stream);
+  return grouped_wgrad_split(go_t, ldgo, go_scales_t, ldgos, ia_t, ldia, ia_scales_t, ldias,
+                             group_ends, num_groups, M, N, K, dw, ld_dw_expert, ld_dw_row,
+                             out_dtype, split_tokens, workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -1171,13 +1171,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
       epilogue<true>(sm, acc, slot, 1024, 0u, 0u, 256u, 0u, 256u);
       continue;
     }
-    char* out = reinterpret_cast<char*>(args.dw) +
-                (int64_t)g * args.N * args.K * (F32 ? 4 : 2);
+    char* out = reinterpret_cast<char*>(args.dw) + (int64_t)g * args.ldw_e * (F32 ? 4 : 2);
     if constexpr (F32)
-      epilogue<true>(sm, acc, out, (int64_t)args.K * 4, q0, 0u, (uint32_t)args.N, p0,
+      epilogue<true>(sm, acc, out, args.ldw_n * 4, q0, 0u, (uint32_t)args.N, p0,
                      (uint32_t)args.K, split > 0 && !staged);
     else
-      epilogue_bf16(sm, acc, out, (int64_t)args.K * 2, q0, 0u, (uint32_t)args.N, p0,
+      epilogue_bf16(sm, acc, out, args.ldw_n * 2, q0, 0u, (uint32_t)args.N, p0,
                     (uint32_t)args.K);
   }
 }
@@ -1189,7 +1188,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
 // 4-column group), 4 per thread a grid-stride apart, loads before adds.
 __global__ __launch_bounds__(256) void k_wgrad_split_reduce(const float* __restrict__ ws,
                                                             void* __restrict__ dw, int32_t N,
-                                                            int32_t K, int32_t out_f32) {
+                                                            int32_t K, int64_t ldw_e,
+                                                            int64_t ldw_n, int32_t out_f32) {
   const int32_t* hdr = reinterpret_cast<const int32_t*>(ws);
   const int32_t E = hdr[0], per_expert = hdr[1], n_tiles = hdr[2], k_tiles = hdr[3];
   const uint32_t gm = (uint32_t)hdr[4];
@@ -1219,7 +1219,7 @@ __global__ __launch_bounds__(256) void k_wgrad_split_reduce(const float* __restr
       band_decode((uint32_t)t, (uint32_t)n_tiles, (uint32_t)k_tiles, gm, nt, kt);
       const int32_t n = (int32_t)nt * 256 + row, k = (int32_t)kt * 256 + c;
       if (n >= N || k >= K) continue;
-      dsto[u] = ((int64_t)rh[0] * N + n) * K + k;
+      dsto[u] = (int64_t)rh[0] * ldw_e + (int64_t)n * ldw_n + k;
       pcol[u] = k;
       if (chunks == 0) continue;
       const float* src = part + ((int64_t)rh[1] + t) * 65536 + row * 256 + c;
@@ -1343,7 +1343,7 @@ hipError_t launch_grouped_wgrad(const WgradArgs& a, hipStream_t stream) {
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   hipLaunchKernelGGL(k_wgrad_split_reduce, dim3(4 * grid.x), dim3(256), 0, stream, a.split_ws,
-                     a.dw, a.N, a.K, a.out_f32);
+                     a.dw, a.N, a.K, a.ldw_e, a.ldw_n, a.out_f32);
   return hipGetLastError();
 }
 

@@ -181,8 +181,9 @@ struct WgradArgs {
   const uint8_t* ia;   // [K, M]
   const uint8_t* ias;  // block-major [M/32][ldias]
   const int32_t* group_ends;
-  void* dw;            // [E, N, K]
+  void* dw;            // dW[g][n][k] at element g * ldw_e + n * ldw_n + k
   int64_t ldgo, ldgos, ldia, ldias;
+  int64_t ldw_e, ldw_n;  // elements; N * K and K for a contiguous [E, N, K]
   int32_t M, N, K, E;
   int32_t split;       // tokens per split-K chunk (multiple of 128), 0 = whole groups
   int32_t out_f32;

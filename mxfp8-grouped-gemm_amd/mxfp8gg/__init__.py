@@ -9,6 +9,7 @@ the current stream.
 """
 from ._lib import MxggError, load as load_library
 from .ops import (
+    GroupEnds,
     _best_config,
     fused_grouped_fwd,
     fwd_ge,
@@ -64,7 +65,7 @@ __all__ = [
     "grouped_mm", "grouped_mm_swiglu_quant", "grouped_wgrad", "grouped_dgrad", "quant_weight_for_dgrad",
     "quant_weight_dual", "swiglu_quant", "swiglu_backward_quant",
     "fused_grouped_fwd", "fwd_ge", "wgrad_fused", "wgrad_prepare", "wgrad_kernel",
-    "offs_to_group_ends", "zero_rows_past_groups",
+    "offs_to_group_ends", "zero_rows_past_groups", "GroupEnds",
     "triton_to_mxfp8_dim0", "triton_to_mxfp8_dim1",
     "triton_mxfp8_grouped_mm", "triton_mxfp8_wgrad", "triton_mxfp8_wgrad_v2", "apply",
     "WeightCastCache",

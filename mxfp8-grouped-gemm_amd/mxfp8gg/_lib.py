@@ -100,6 +100,11 @@ SIGNATURES = {
         [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I, _I64, _P,
          _I64, _P],
     ),
+    "mxgg_grouped_wgrad_strided": (
+        _I,
+        [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I,
+         _I64, _P, _I64, _P],
+    ),
     "mxgg_route_plan": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
     "mxgg_gather_rows": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P]),
     "mxgg_gather_quant_dual": (

@@ -89,13 +89,72 @@ def _group_ends(offs: torch.Tensor, num_groups: int, device) -> torch.Tensor:
     return offs.contiguous()
 
 
+class GroupEnds(torch.Tensor):
+    """int32 cumulative group ends that this library wrote: the padded ends of
+    its token-axis casts and of SwiGLU backward, routing plans, and
+    offs_to_group_ends.  The reference-named wgrad entry points always read a
+    GroupEnds as ends, never as group sizes (a degenerate routing, every token
+    in the first expert, can make padded ends look like sizes).
+
+    The type is part of the tensor, so it survives what copies the values
+    unchanged: clone, copy.deepcopy, detach, to / cpu / cuda / int / long,
+    contiguous, pin_memory, and torch.cat / torch.stack of GroupEnds only.  Anything
+    else (arithmetic, indexing, diff) returns a plain tensor: the library no
+    longer knows what its values mean."""
+
+    _KEEP = frozenset({
+        torch.Tensor.clone, torch.clone, torch.Tensor.detach, torch.detach,
+        torch.Tensor.to, torch.Tensor.cpu, torch.Tensor.cuda, torch.Tensor.int,
+        torch.Tensor.long, torch.Tensor.contiguous, torch.Tensor.pin_memory,
+        torch.Tensor.share_memory_,
+    })
+    _JOIN = frozenset({torch.cat, torch.concat, torch.stack})
+
+    def __deepcopy__(self, memo):
+        out = self.as_subclass(torch.Tensor).clone().as_subclass(GroupEnds)
+        memo[id(self)] = out
+        return out
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        with torch._C.DisableTorchFunctionSubclass():
+            out = func(*args, **kwargs)
+        if not isinstance(out, torch.Tensor):
+            return out
+        if func in cls._KEEP:
+            return out.as_subclass(cls)
+        if func in cls._JOIN:
+            parts = args[0] if args else kwargs.get("tensors", ())
+            if parts and all(isinstance(t, cls) for t in parts):
+                return out.as_subclass(cls)
+        return out
+
+
 def _mark_ends(t):
-    """Tag a tensor this library wrote as cumulative group ends (the padded
-    ends of the token-axis casts, routing plans), so the reference-named wgrad
-    entry points never read it as group sizes."""
-    if t is not None:
-        t._mxgg_group_ends = True
-    return t
+    """Mark a tensor this library wrote as cumulative group ends (GroupEnds)."""
+    if t is None or isinstance(t, GroupEnds):
+        return t
+    return t.as_subclass(GroupEnds)
+
+
+def _warn_if_ambiguous(offs: torch.Tensor, tokens: int) -> None:
+    """With MXGG_CHECK_OFFS=1: warn when an "auto" offs vector fits both
+    readings (non-decreasing, so valid as ends, and adding up to exactly
+    `tokens` with its last entry below it, so valid as sizes).  Off by default:
+    the check reads offs back to the host, which the library otherwise never
+    does."""
+    import os
+    import warnings
+
+    if os.environ.get("MXGG_CHECK_OFFS", "0") in ("", "0"):
+        return
+    v = offs.detach().to("cpu", torch.int64)
+    if v.numel() > 1 and bool((v[1:] >= v[:-1]).all()) and int(v.sum()) == tokens \
+            and int(v[-1]) < tokens:
+        warnings.warn(f"offs {v.tolist()} reads as group sizes and as cumulative ends for "
+                      f"{tokens} tokens; the auto rule takes sizes, pass offs_kind= to choose",
+                      RuntimeWarning, stacklevel=3)
 
 
 _OFFS_KINDS = {"ends": _lib.OFFS_ENDS, "sizes": _lib.OFFS_SIZES, "auto": _lib.OFFS_AUTO}
@@ -108,14 +167,18 @@ def offs_to_group_ends(offs: torch.Tensor, tokens: int, offs_kind: str = "auto")
     below `tokens`, ends otherwise), decided on the device by one small kernel
     (mxgg_offs_to_group_ends), with no host sync.  Tensors this library
     returned as group ends (the padded ends of its token-axis casts, routing
-    plans) are always read as ends."""
+    plans: GroupEnds, also after clone() / to() / cpu()) are always read as
+    ends.  Set MXGG_CHECK_OFFS=1 to be warned when an "auto" vector fits both
+    readings (costs a device-to-host read)."""
     if offs_kind not in _OFFS_KINDS:
         raise ValueError(f"offs_kind must be one of {sorted(_OFFS_KINDS)}, got {offs_kind!r}")
-    if getattr(offs, "_mxgg_group_ends", False):
+    if isinstance(offs, GroupEnds):
         offs_kind = "ends"
     if not isinstance(offs, torch.Tensor) or offs.dim() != 1:
         raise ValueError("offs must be a 1-D tensor")
     _need_gpu(offs, "offs")
+    if offs_kind == "auto":
+        _warn_if_ambiguous(offs, tokens)
     src = offs.to(torch.int32).contiguous()
     out = torch.empty_like(src)
     _lib.check(_lib.load().mxgg_offs_to_group_ends(src.data_ptr(), src.numel(), int(tokens),
@@ -518,6 +581,15 @@ def _small_launch(M: int, N: int, E: int, device) -> bool:
 _MAX_OPERAND_BYTES = 0x7FFFFFF0   # the C ABI's bound on (rows - 1) * ld + K
 
 
+def _feature_rows_per_launch(ld: int, rows: int, M: int) -> int:
+    """Feature rows of a token-axis wgrad operand [rows, M] (row stride ld
+    bytes) one launch may take: all when it fits the 32-bit buffer range,
+    else the largest multiple of 256 that does."""
+    if rows == 0 or (rows - 1) * ld + M <= _MAX_OPERAND_BYTES:
+        return max(rows, 1)
+    return max(256, ((_MAX_OPERAND_BYTES - M) // ld + 1) // 256 * 256)
+
+
 def _rows_per_launch(lda: int, K: int, M: int) -> int:
     """Rows of A one forward launch may take: all M when A fits the 32-bit
     buffer range, else the largest multiple of 256 that does."""
@@ -730,7 +802,9 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
     group end must be a multiple of 32 (the layout to_mxfp8_dim1 produces): an
     expert whose bounds are not is written as NaN, since a scale block would
     span two experts.  Without scales the ends may be any token index.
-    Empty groups yield zeros.
+    Empty groups yield zeros.  An operand past the 2 GiB buffer range of one
+    launch (e.g. X^T at K = 7168 from 299593 tokens) runs as launches over
+    chunks of its feature rows, each writing its slice of dW.
     split_tokens: split-K chunk in tokens (multiple of 128), 0 for none, None
     to choose from the shapes (wgrad_split_tokens).  A split call writes the
     fp32 partial tiles to a workspace and adds them in chunk order
@@ -755,13 +829,42 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
         si, ldis = _scales_2d(ia_scales, K, M // 32, "ia_scales")
     E = offs.numel()
     ends = _group_ends(offs, E, go.device)
-    if split_tokens is None:
-        split_tokens = wgrad_split_tokens(M, N, K, E, _cu_count(go.device))
     if out is None:
         out = torch.empty((E, N, K), dtype=out_dtype, device=go.device)
     elif out.shape != (E, N, K) or out.dtype != out_dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous [E, N, K] tensor of out_dtype")
     lib = _lib.load()
+    nc = _feature_rows_per_launch(g8.stride(0), N, M)
+    kc = _feature_rows_per_launch(i8.stride(0), K, M)
+    if nc < N or kc < K:
+        # An operand past the 32-bit buffer range: launches over chunks of its
+        # feature rows (256-row multiples), each contracting every token and
+        # writing its own slice of dW (mxgg_grouped_wgrad_strided), so the
+        # result is the one-launch result.
+        esz = out.element_size()
+        for n0 in range(0, N, nc):
+            for k0 in range(0, K, kc):
+                n, k = min(nc, N - n0), min(kc, K - k0)
+                st = wgrad_split_tokens(M, n, k, E, _cu_count(go.device)) \
+                    if split_tokens is None else int(split_tokens)
+                ws, nbytes = None, 0
+                if st:
+                    nbytes = int(lib.mxgg_grouped_wgrad_workspace_bytes(M, n, k, E, st))
+                    if nbytes < 0:
+                        raise ValueError(f"split_tokens={st} must be a positive multiple of 128")
+                    ws = torch.empty(nbytes, dtype=torch.uint8, device=go.device)
+                _lib.check(lib.mxgg_grouped_wgrad_strided(
+                    g8.data_ptr() + n0 * g8.stride(0), g8.stride(0),
+                    sg.data_ptr() + n0 if sg is not None else None, ldgs,
+                    i8.data_ptr() + k0 * i8.stride(0), i8.stride(0),
+                    si.data_ptr() + k0 if si is not None else None, ldis,
+                    ends.data_ptr(), E, M, n, k,
+                    out.data_ptr() + (n0 * K + k0) * esz, N * K, K, _out_code(out_dtype), st,
+                    ws.data_ptr() if ws is not None else None, nbytes, _stream_ptr(go)),
+                    "grouped_wgrad_strided")
+        return out
+    if split_tokens is None:
+        split_tokens = wgrad_split_tokens(M, N, K, E, _cu_count(go.device))
     args = (g8.data_ptr(), g8.stride(0),
             sg.data_ptr() if sg is not None else None, ldgs,
             i8.data_ptr(), i8.stride(0),
@@ -808,10 +911,7 @@ def _wgrad_offs(offs, tokens: int, offs_kind: str, device):
     if offs.dim() != 1 or offs.numel() < 1:
         raise ValueError(f"offs must be a non-empty 1-D tensor, got shape {tuple(offs.shape)}")
     if offs.device != device:
-        marked = getattr(offs, "_mxgg_group_ends", False)
-        offs = offs.to(device, non_blocking=True)
-        if marked:
-            _mark_ends(offs)
+        offs = offs.to(device, non_blocking=True)   # a GroupEnds stays one
     return offs_to_group_ends(offs, tokens, offs_kind)
 
 
@@ -826,7 +926,7 @@ def wgrad_fused(go, ia, offs, go_scales=None, ia_scales=None, *, offs_kind="auto
     offs_kind="auto" (default) offs is read as sizes when its entries add up
     to exactly M and its last entry is below M, as cumulative ends otherwise;
     "sizes" / "ends" force one reading (offs_to_group_ends).  Group ends from
-    this library's token-axis casts are always read as ends.  No restacking:
+    this library's token-axis casts (GroupEnds) are always read as ends.  No restacking:
     the kernel contracts each group's token range in place.  Returns
     (E, N, K), bf16 by default like the reference; pass
     out_dtype=torch.float32 for fp32 grads.  Scales are used only when both

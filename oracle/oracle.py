@@ -163,6 +163,15 @@ def group_bounds(ends, rows: int):
     return out
 
 
+def rows_in_groups(ends, rows: int) -> np.ndarray:
+    """Boolean mask over `rows` rows: True for the rows that belong to a group
+    under group_bounds (the rows a grouped forward writes)."""
+    mask = np.zeros(rows, dtype=bool)
+    for b, e in group_bounds(ends, rows):
+        mask[b:e] = True
+    return mask
+
+
 # ---------------------------------------------------------------------------
 # GEMM references (float64)
 # ---------------------------------------------------------------------------

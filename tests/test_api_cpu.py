@@ -186,3 +186,31 @@ def test_offs_helpers_reject_cpu_tensors():
         mxfp8gg.offs_to_group_ends(t, 8, "cumulative")
     with pytest.raises(ValueError, match="ROCm GPU only"):
         mxfp8gg.zero_rows_past_groups(torch.zeros(4, 8), t)
+
+
+def test_group_ends_type_survives_copies_only():
+    t = ops._mark_ends(torch.tensor([64, 64, 64, 64], dtype=torch.int32))
+    assert isinstance(t, mxfp8gg.GroupEnds)
+    import copy
+    kept = [t.clone(), t.detach(), t.to(torch.int64), t.cpu(), t.contiguous(), t.int(),
+            copy.deepcopy(t), torch.cat([t, t.clone()]), torch.stack([t, t])]
+    assert all(isinstance(k, mxfp8gg.GroupEnds) for k in kept)
+    assert all(k.flatten()[:4].tolist() == [64, 64, 64, 64] for k in kept)
+    # arithmetic, indexing and mixed concatenation give plain tensors
+    dropped = [t + 1, t[1:], t.diff(), torch.cat([t, torch.tensor([1], dtype=torch.int32)])]
+    assert not any(isinstance(d, mxfp8gg.GroupEnds) for d in dropped)
+
+
+def test_ambiguous_offs_warning_is_opt_in(monkeypatch):
+    import warnings
+
+    amb = torch.tensor([64, 64, 64, 64], dtype=torch.int32)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        monkeypatch.delenv("MXGG_CHECK_OFFS", raising=False)
+        ops._warn_if_ambiguous(amb, 256)                 # off by default
+        monkeypatch.setenv("MXGG_CHECK_OFFS", "1")
+        ops._warn_if_ambiguous(torch.tensor([64, 128, 192, 256]), 256)   # ends only
+        ops._warn_if_ambiguous(torch.tensor([100, 50, 106]), 256)        # sizes only
+        with pytest.raises(RuntimeWarning, match="reads as group sizes and as cumulative"):
+            ops._warn_if_ambiguous(amb, 256)

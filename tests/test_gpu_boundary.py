@@ -59,8 +59,16 @@ def test_library_group_ends_are_never_read_as_sizes(gpu):
     offs = torch.tensor([64, 64, 64, 64], dtype=torch.int32, device=gpu)
     _, _, pad = mxfp8gg.to_mxfp8_dim1(dy, offs)
     assert pad.tolist() == [64, 64, 64, 64] and mxfp8gg.padded_token_capacity(64, 4) == 256
+    assert isinstance(pad, mxfp8gg.GroupEnds)
     assert mxfp8gg.offs_to_group_ends(pad, 256).tolist() == [64, 64, 64, 64]
-    assert mxfp8gg.offs_to_group_ends(pad.clone(), 256).tolist() == [64, 128, 192, 256]
+    # copies keep the meaning: clone, a host round trip, a concatenation
+    for copy in (pad.clone(), pad.cpu().to(gpu), pad.detach().contiguous(),
+                 torch.cat([pad.clone()])):
+        assert mxfp8gg.offs_to_group_ends(copy, 256).tolist() == [64, 64, 64, 64]
+    # a plain tensor with the same values fits both readings: auto takes sizes
+    plain = torch.tensor(pad.tolist(), dtype=torch.int32, device=gpu)
+    assert mxfp8gg.offs_to_group_ends(plain, 256).tolist() == [64, 128, 192, 256]
+    assert mxfp8gg.offs_to_group_ends(plain, 256, "ends").tolist() == [64, 64, 64, 64]
 
 
 @pytest.mark.parametrize("E,mg", [(4, 512), (8, 384)])

@@ -314,6 +314,47 @@ def test_forward_above_2gib_runs_in_row_chunks(gpu):
     assert not torch.isnan(y[ri].float()).any()
 
 
+def test_wgrad_above_2gib_runs_in_feature_row_chunks(gpu):
+    # dY^T and X^T of 300032 padded tokens x 7168 features are 2.15 GB each,
+    # past the 32-bit buffer range of one launch: grouped_wgrad runs 2 x 2
+    # launches over chunks of 6912 feature rows of each operand, each writing
+    # its slice of dW (mxgg_grouped_wgrad_strided).  The C ABI refuses the
+    # whole operand in one launch; sampled dW entries on both sides of both
+    # chunk boundaries match the oracle for every expert.
+    N = K = 7168
+    M = 300032
+    sizes = [100032, 0, 170016, 29984]          # multiples of 32, an empty expert
+    g = torch.Generator(device=gpu).manual_seed(57)
+
+    def operand(rows):
+        q = torch.randint(0, 0x7E, (rows, M), generator=g, device=gpu, dtype=torch.uint8)
+        q |= torch.randint(0, 2, (rows, M), generator=g, device=gpu, dtype=torch.uint8) << 7
+        s = torch.randint(120, 134, (M // 32, rows), generator=g, device=gpu, dtype=torch.uint8)
+        return q, s.t()                        # scales as a block-major view [rows, M/32]
+
+    go, gos = operand(N)
+    ia, ias = operand(K)
+    assert ops._feature_rows_per_launch(M, N, M) == 6912
+    ends = torch.tensor(np.cumsum(sizes), dtype=torch.int32, device=gpu)
+    f8 = torch.float8_e4m3fn
+    lib = mxfp8gg.load_library()
+    dw_one = torch.empty((4, N, K), dtype=torch.float32, device=gpu)
+    assert lib.mxgg_grouped_wgrad(go.data_ptr(), M, gos.data_ptr(), N, ia.data_ptr(), M,
+                                  ias.data_ptr(), K, ends.data_ptr(), 4, M, N, K,
+                                  dw_one.data_ptr(), 1, 0, None) == mxfp8gg._lib.ERR_UNSUPPORTED
+    del dw_one
+    dw = ops.grouped_wgrad(go.view(f8), ia.view(f8), ends, gos, ias, out_dtype=torch.float32)
+    pick = np.array([0, 255, 6911, 6912, 7000, 7167])
+    pi = torch.from_numpy(pick).to(gpu)
+    ref = O.grouped_wgrad(u8(go[pi]), u8(gos[pi]), u8(ia[pi]), u8(ias[pi]), np.cumsum(sizes))
+    got = dw[:, pi][:, :, pi]
+    for e, sz in enumerate(sizes):
+        if sz:
+            assert_close_to_oracle(got[e], ref[e])
+        else:
+            assert torch.all(dw[e] == 0)
+
+
 @pytest.mark.parametrize("cfg", ["c2", "c3"])
 def test_full_size_forward_sampled_rows(gpu, cfg):
     x, w, sizes = getattr(workloads, cfg)(gpu)
@@ -325,22 +366,41 @@ def test_full_size_forward_sampled_rows(gpu, cfg):
     y = ops.grouped_mm(xq, wq, ends, xs, ws)
     y_again = ops.grouped_mm(xq, wq, ends, xs, ws)
     assert torch.equal(y, y_again)  # deterministic
-    # sampled rows from four experts (first rows, last rows, interior)
-    rows = []
-    for g in (0, 5, 17, 31):
-        b = 0 if g == 0 else int(ends_np[g - 1])
-        e = int(ends_np[g])
-        if e > b:
-            rows += sorted({b, (b + e) // 2, e - 1})
-    rows = np.array(sorted(set(rows)))
-    idx = torch.from_numpy(rows).to(gpu)
-    a_rows, as_rows = u8(xq[idx]), u8(xs[idx])
-    ref = np.empty((rows.size, wq.shape[1]))
-    for g in sorted({int(np.searchsorted(ends_np, r, side="right")) for r in rows}):
-        sel = np.nonzero(np.searchsorted(ends_np, rows, side="right") == g)[0]
-        wdq = O.dequant(u8(wq[g]), u8(ws[g]))
-        ref[sel] = O.dequant(a_rows[sel], as_rows[sel]) @ wdq.T
-    assert_close_to_oracle(y[idx], ref)
+    # every non-empty expert: its first and last row and two random rows
+    rng = np.random.default_rng(61)
+    checked = 0
+    for g, (b, e) in enumerate(O.group_bounds(ends_np, xq.shape[0])):
+        if e <= b:
+            continue
+        rows = np.unique(np.r_[b, e - 1, rng.integers(b, e, 2)])
+        idx = torch.from_numpy(rows).to(gpu)
+        ref = O.dequant(u8(xq[idx]), u8(xs[idx])) @ O.dequant(u8(wq[g]), u8(ws[g])).T
+        assert_close_to_oracle(y[idx], ref)
+        checked += 1
+    assert checked == int(np.count_nonzero(sizes))
+
+
+@pytest.mark.parametrize("scaled", [True, False])
+def test_nan_row_inside_a_group_is_compared(gpu, scaled):
+    # A NaN payload code inside a group makes that output row NaN in the
+    # oracle; the comparison covers it (only the rows outside every group are
+    # masked out, by oracle.rows_in_groups) and the kernel gives NaN there too.
+    sizes = [100, 0, 37]
+    M, N, K = 200, 256, 128
+    a_q, a_s = _rand_q((M, K), gpu, 35)
+    w_q, w_s = _rand_q((3, N, K), gpu, 36)
+    a_q[42, 5] = 0x7F
+    ends = workloads.ends_of(sizes)
+    out = torch.full((M, N), 7.0, dtype=torch.float32, device=gpu)
+    ops.grouped_mm(a_q.view(torch.float8_e4m3fn), w_q.view(torch.float8_e4m3fn),
+                   torch.from_numpy(ends).to(gpu), a_s if scaled else None,
+                   w_s if scaled else None, out_dtype=torch.float32, out=out)
+    ref = O.grouped_fwd(u8(a_q), u8(a_s) if scaled else None, u8(w_q),
+                        u8(w_s) if scaled else None, ends)
+    mask = O.rows_in_groups(ends, M)
+    assert np.isnan(ref[42]).all() and mask.sum() == 137
+    assert_close_to_oracle(out, ref, rows=mask)
+    assert torch.all(out[torch.from_numpy(~mask).to(gpu)] == 7.0)
 
 
 # ---------------------------------------------------------------------------

@@ -73,6 +73,34 @@ def test_moe_ffn_c5_matches_composed_oracle(gpu):
     check_layer(x, wgu, wd, dy, sizes, rows, n_feat, f_feat, m_feat, k_feat, got)
 
 
+def test_moe_ffn_past_2gib_matches_composed_oracle(gpu):
+    # 300000 tokens x hidden 7168: X, its casts, dY and the token-axis
+    # operands of both weight gradients are past the 2 GiB buffer range of one
+    # launch, so the forward and dgrad run in row chunks and both weight
+    # gradients in feature-row chunks (dY^T of the down projection along its
+    # rows, X^T of the gate+up projection along its rows).
+    sizes = np.array([120000, 0, 150000, 30000])
+    E, H, F = 4, 7168, 2048
+    M = int(sizes.sum())
+    assert mxfp8gg.padded_token_capacity(M, E) * H > 2 ** 31
+    print(f"layer step past 2 GiB: {M} tokens, E={E}", flush=True)
+    x, wgu, wd, dy = _layer(gpu, sizes, H, F, 91)
+    got = _run(x, wgu, wd, dy, sizes)
+    ends = workloads.ends_of(sizes)
+    starts = ends - sizes
+    rng = np.random.default_rng(9)
+    rows = []
+    for e in (0, 2, 3):
+        b, t = int(starts[e]), int(ends[e])
+        rows += [b, t - 1] + rng.integers(b, t, 3).tolist()
+    rows = np.unique(np.array(rows))
+    n_feat = np.unique(np.r_[0, 6911, 6912, 7167, rng.integers(0, H, 3)])
+    f_feat = np.unique(np.r_[0, 2047, rng.integers(0, F, 4)])
+    m_feat = np.unique(np.r_[0, F - 1, F, 2 * F - 1, rng.integers(0, 2 * F, 3)])
+    k_feat = np.unique(np.r_[0, 6911, 6912, 7167, rng.integers(0, H, 3)])
+    check_layer(x, wgu, wd, dy, sizes, rows, n_feat, f_feat, m_feat, k_feat, got)
+
+
 def test_layer_rows_past_the_groups_are_zero(gpu):
     # offs[-1] < M: rows past the last group end get zero output and zero dX
     sizes = [64, 96, 32]

@@ -220,6 +220,42 @@ def test_group_bounds_running_max_rule(seed):
     assert O.group_bounds(ok, rows) == list(zip(np.r_[0, ok[:-1]].tolist(), ok.tolist()))
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_rows_in_groups_is_the_union_of_the_group_ranges(seed):
+    rng = np.random.default_rng(100 + seed)
+    rows = int(rng.integers(1, 400))
+    ends = rng.integers(-20, rows + 40, int(rng.integers(1, 10)))
+    m = np.clip(np.maximum.accumulate(ends.astype(np.int64)), 0, rows)
+    want = np.arange(rows) < m[-1]      # the groups tile [0, last running max)
+    assert np.array_equal(O.rows_in_groups(ends, rows), want)
+
+
+def test_gemm_comparison_checks_nan_rows_and_masks_only_what_it_is_told():
+    # the comparison used by every GPU GEMM test: a reference row holding a
+    # NaN is compared (the output must hold NaN at the same places), and rows
+    # are skipped only through an explicit mask
+    from tests._helpers import assert_close_to_oracle
+
+    ref = np.arange(12, dtype=np.float64).reshape(4, 3) + 1.0
+    ref[1, 2] = np.nan
+    y = torch.from_numpy(ref.copy()).float()
+    assert_close_to_oracle(y, ref)
+    y_bad = y.clone()
+    y_bad[1, 2] = 5.0
+    with pytest.raises(AssertionError):
+        assert_close_to_oracle(y_bad, ref)
+    y_bad = y.clone()
+    y_bad[3, 0] = float("nan")
+    with pytest.raises(AssertionError):
+        assert_close_to_oracle(y_bad, ref)
+    y_off = y.clone()
+    y_off[0] += 1.0
+    with pytest.raises(AssertionError):
+        assert_close_to_oracle(y_off, ref)
+    assert_close_to_oracle(y_off, ref, rows=np.array([False, True, True, True]))
+    assert_close_to_oracle(y_off, ref, rows=np.array([1, 2, 3]))
+
+
 @pytest.mark.parametrize("ends", [[30, 10, 50], [80, 0, 80, 0], [-3, 20, 5, 200]])
 def test_dim1_decreasing_ends_equal_their_running_max(ends):
     g = torch.Generator().manual_seed(7)
