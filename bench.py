@@ -451,12 +451,21 @@ def routing_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):
 
 
 GEMM_SOURCE = ROOT / "mxfp8-grouped-gemm_amd" / "csrc" / "gemm.hip"
+# every file the GEMM translation unit includes from the tree, so an edit to a
+# shared device helper also marks a stored traffic figure stale
+GEMM_HEADERS = [ROOT / "mxfp8-grouped-gemm_amd" / "csrc" / "mx_device.h",
+                ROOT / "mxfp8-grouped-gemm_amd" / "csrc" / "mxgg_internal.h",
+                ROOT / "include" / "mxgg.h"]
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_grouped_fwd_c2.json"
+HEADLINE_KERNEL = "k_grouped_fwd"   # the C2 launch: k_grouped_fwd<true, 0> (scaled, bf16 out)
 
 
 def _source_hash():
     import hashlib
-    return hashlib.sha256(GEMM_SOURCE.read_bytes()).hexdigest()
+    h = hashlib.sha256()
+    for f in [GEMM_SOURCE] + GEMM_HEADERS:
+        h.update(f.name.encode() + b"\0" + f.read_bytes())
+    return h.hexdigest()
 
 
 def _pmc_pass(only, counter, out_dir):
@@ -496,8 +505,9 @@ def measure_traffic():
                 res[(only, counter)] = _pmc_pass(only, counter, Path(tmp) / f"{only}_{counter}")
                 if not res[(only, counter)]:
                     raise RuntimeError(f"rocprofv3 {counter} pass over --only {only} gave no counters")
-    fwd = {c: next(v for k, v in res[("fwd", c)].items() if "k_grouped_fwd" in k)
-           for c in ("FETCH_SIZE", "WRITE_SIZE")}
+    names = {c: next(k for k in res[("fwd", c)] if HEADLINE_KERNEL in k)
+             for c in ("FETCH_SIZE", "WRITE_SIZE")}
+    fwd = {c: res[("fwd", c)][names[c]] for c in ("FETCH_SIZE", "WRITE_SIZE")}
     cp = {c: max(res[("copy", c)].values()) for c in ("FETCH_SIZE", "WRITE_SIZE")}
     nbytes = 1 << 30
     ff = nbytes / (cp["FETCH_SIZE"][0] * 1024)
@@ -505,8 +515,8 @@ def measure_traffic():
     rd = fwd["FETCH_SIZE"][0] * 1024 * ff
     wr = fwd["WRITE_SIZE"][0] * 1024 * wf
     out = {
-        "kernel": "k_grouped_fwd<true,false> on C2 (65536 tokens, 32 experts, K=7168, N=4096)",
-        "kernel_source": str(GEMM_SOURCE.relative_to(ROOT)),
+        "kernel": names["FETCH_SIZE"] + " on C2 (65536 tokens, 32 experts, K=7168, N=4096)",
+        "kernel_source": [str(f.relative_to(ROOT)) for f in [GEMM_SOURCE] + GEMM_HEADERS],
         "kernel_source_sha256": _source_hash(),
         "hbm_bytes_per_launch": int(rd + wr),
         "hbm_read_bytes": int(rd), "hbm_write_bytes": int(wr),
@@ -532,6 +542,13 @@ def stored_traffic():
     if t.get("kernel_source_sha256") != _source_hash():
         return None, "stale: kernel source changed since the measurement (bench.py --only traffic)"
     return t.get("hbm_bytes_per_launch"), "rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated"
+
+
+def stored_traffic_kernel():
+    """Kernel name the stored traffic figure was counted on (None if absent)."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    return json.loads(TRAFFIC_FILE.read_text()).get("kernel")
 
 
 def cpu_baseline(xq, xs, wq, ws, ends_np, n, k, gpu_out=None, budget_s=12.0):
@@ -750,19 +767,23 @@ def main():
         components["routing_c5"] = routing_c5(torch, mxfp8gg, workloads, dev)
 
     traffic, traffic_note = None, "not measured (--no-traffic or a partial run)"
+    traffic_kernel = None
     if args.only == "all" and not args.no_traffic:
         # measured in this run: four rocprofv3 counter passes in child processes,
         # after every timed region above
         log("roofline traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes of C2 and a copy")
         try:
-            traffic = measure_traffic()["hbm_bytes_per_launch"]
+            measured = measure_traffic()
+            traffic, traffic_kernel = measured["hbm_bytes_per_launch"], measured["kernel"]
             traffic_note = ("measured in this run: rocprofv3 FETCH_SIZE + WRITE_SIZE of the "
                             "C2 launch, each scaled by the same counter over a 1 GiB copy")
         except Exception as exc:  # profiler missing or refused: fall back, say so
             log(f"traffic passes failed: {exc}")
             traffic, traffic_note = stored_traffic()
+            traffic_kernel = stored_traffic_kernel() if traffic is not None else None
     elif args.only != "all":
         traffic, traffic_note = stored_traffic()
+        traffic_kernel = stored_traffic_kernel() if traffic is not None else None
 
     cpu = None
     if not args.no_cpu and args.only == "all":
@@ -796,7 +817,7 @@ def main():
             "frac": round(tflops / PEAK_MXFP8_TFLOPS, 4),
             "traffic": traffic,
             "traffic_source": traffic_note,
-            "kernel": "k_grouped_fwd<true,false> (one launch per step)",
+            "kernel": traffic_kernel or "k_grouped_fwd<true, 0> (one launch per step)",
         },
         "cpu_baseline": cpu,
         "components": components,
