@@ -578,6 +578,16 @@ def _small_launch(M: int, N: int, E: int, device) -> bool:
     return m_tiles * ((N + 255) // 256) <= units // 2
 
 
+def _full_rounds(M: int, N: int, device) -> bool:
+    """True when the forward has at least one full round of 256x256 tiles for
+    any group sizes (ceil(M / 256) m-tiles at least).  Such a launch takes the
+    split entry: the kernel cuts a last round that fills at most half of the
+    units along K (at most 8 ranges) and leaves any other last round alone;
+    the fixed-order reduction then costs one short launch."""
+    units = (_split_workspace_bytes(device) - 16384) // (256 * 256 * 4)
+    return ((M + 255) // 256) * ((N + 255) // 256) >= units
+
+
 _MAX_OPERAND_BYTES = 0x7FFFFFF0   # the C ABI's bound on (rows - 1) * ld + K
 
 
@@ -610,10 +620,11 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
     Rows after the last group end are left untouched.  split_tail: run a
     launch whose tiles fill at most half of the compute units split along K
     over the idle units (mxgg_grouped_fwd_split; deterministic, equal to the
-    unsplit result up to fp32 summation order).  None (default): only when
-    the launch is that small whatever the group sizes are; True: always take
-    the split entry point (it splits a sparse last round of any launch);
-    False: never.
+    unsplit result up to fp32 summation order).  None (default): when the
+    launch is that small whatever the group sizes are, and when it has at
+    least one full round of tiles (the kernel then splits its last round only
+    if that round fills at most half of the units); True: always take the
+    split entry point; False: never.
     """
     _need_gpu(a, "a")
     _need_gpu(w, "w")
@@ -661,7 +672,8 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
                 e.data_ptr() if e is not None else None, E,
                 m, N, K, out.data_ptr() + r0 * out.stride(0) * esz, out.stride(0),
                 _out_code(out_dtype))
-        split = _small_launch(m, N, E, a.device) if split_tail is None else split_tail
+        split = (_small_launch(m, N, E, a.device) or _full_rounds(m, N, a.device)) \
+            if split_tail is None else split_tail
         if split and m > 0 and N > 0:
             ws = _split_workspace(a.device)
             _lib.check(lib.mxgg_grouped_fwd_split(*args, ws.data_ptr(), ws.numel(), stream),

@@ -72,7 +72,7 @@ def _expect_split(G, tiles, K):
     nst = (K + 127) // 128
     if rem == 0 or rem > G // 2 or nst < 2:
         return 0
-    S = min(G // rem, nst, 16)
+    S = min(G // rem, nst, 16 if tiles < G else 8)
     chunk = -(-nst // S)
     return rem, -(-nst // chunk)
 
