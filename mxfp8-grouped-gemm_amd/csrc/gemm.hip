@@ -157,12 +157,17 @@ __device__ __forceinline__ void wait_barrier() {
 // emits in these kernels (the generated code writes M0 only here).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma_x4(const desc_t& d, uint32_t lds_addr, uint32_t voff) {
+// soff: a wave-uniform byte offset added in the instruction's scalar offset
+// field.  The buffer range check covers voff + soff (measured on gfx950: a
+// scalar offset alone past num_records reads zero), so a per-load row step
+// can ride there instead of costing a vector add per load.
+__device__ __forceinline__ void dma_x4(const desc_t& d, uint32_t lds_addr, uint32_t voff,
+                                       uint32_t soff = 0) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds"
       :
-      : "s"(lds_addr), "v"(voff), "s"(d)
+      : "s"(lds_addr), "v"(voff), "s"(d), "s"(soff)
       : "memory", "m0");
 }
 __device__ __forceinline__ void dma_x1(const desc_t& d, uint32_t lds_addr, uint32_t voff) {
@@ -227,12 +232,12 @@ struct Stream {
 
   __device__ __forceinline__ void load_p(uint8_t* stage, const Operand& P, uint32_t bp,
                                          uint32_t i) const {
-    dma_x4(P.data, lds_offset(stage) + 4096u * i + 1024u * wave_id(), bp + step(i, P));
+    dma_x4(P.data, lds_offset(stage) + 4096u * i + 1024u * wave_id(), bp, step(i, P));
   }
   __device__ __forceinline__ void load_q(uint8_t* stage, const Operand& Q, uint32_t bq,
                                          uint32_t i) const {
     dma_x4(Q.data, lds_offset(stage) + kOpBytes + 4096u * i + 1024u * wave_id(),
-           bq + step(i, Q));
+           bq, step(i, Q));
   }
   // Scale rows of k-block k0/32 + wave; operand X = P (OP 0) or Q (OP 1).
   template <int OP>
