@@ -17,7 +17,8 @@ C2 launch) is measured by four rocprofv3 counter passes in child processes
 calibrates both counters); --no-traffic skips them.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-traffic]
-                      [--only fwd|wgrad|copy|ref8|refwgrad|c5|routing|dense|small|traffic|hbm]
+                      [--only fwd|wgrad|copy|ref8|refwgrad|c5|routing|dense|dense_clock|small|
+                              traffic|hbm]
 """
 import argparse
 import json
@@ -187,6 +188,79 @@ def dense_c2_shape(torch, mxfp8gg, dev, steps=10, warmup=3):
             except Exception as ex:  # the vendor paths are a comparison only
                 best[name] = "unavailable: " + str(ex)[:120]
     res.update(best)
+    return res
+
+
+def _sclk_mhz():
+    """Current shader clock of card 0 from rocm-smi (MHz), or None."""
+    import re
+    import subprocess
+    try:
+        r = subprocess.run(["rocm-smi", "-d", "0", "--showclocks", "--json"],
+                           capture_output=True, text=True, timeout=20)
+        card = json.loads(r.stdout)["card0"]
+        return int(re.search(r"(\d+)", card["sclk clock speed:"]).group(1))
+    except Exception:  # the clock is context for the rates, not a result
+        return None
+
+
+def dense_sustained(torch, mxfp8gg, dev, seconds=5.0):
+    """The dense C2 shape run back to back for `seconds` per case (this
+    library's kernel with and without E8M0 scales, hipBLASLt's tensorwise fp8
+    kernel through torch._scaled_mm), with the shader clock sampled by rocm-smi
+    while each runs.  Under sustained load the chip is power-limited, so the
+    clock (and TFLOPS per GHz) separates cycles from clock."""
+    import threading
+    M, N, K = 65536, 4096, 7168
+    gen = torch.Generator(device=dev).manual_seed(0)
+    xq, xs = mxfp8gg.to_mxfp8_dim0(torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16))
+    wq, ws = mxfp8gg.to_mxfp8_dim0(
+        (torch.randn((1, N, K), generator=gen, device=dev) * 0.006).to(torch.bfloat16))
+    ends = torch.tensor([M], dtype=torch.int32, device=dev)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    one = torch.ones((), device=dev)
+    fl = 2 * M * N * K
+    cases = {
+        "mxgg_scaled": lambda: mxfp8gg.grouped_mm(xq, wq, ends, xs, ws, out=out),
+        "mxgg_unscaled": lambda: mxfp8gg.grouped_mm(xq, wq, ends, out=out),
+        "hipblaslt_fp8_tensorwise":
+            lambda: torch._scaled_mm(xq, wq[0].t(), one, one, out_dtype=torch.bfloat16)}
+    res = {"M": M, "N": N, "K": K, "seconds_per_case": seconds, "cases": {}}
+    for name, fn in cases.items():
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        clocks, done = [], threading.Event()
+
+        def sample():
+            if not done.wait(1.5):           # past the clock's settling time
+                while not done.is_set():
+                    c = _sclk_mhz()
+                    if c is not None:
+                        clocks.append(c)
+                    done.wait(0.3)
+        th = threading.Thread(target=sample)
+        th.start()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        n, t0 = 0, time.time()
+        start.record()
+        while time.time() - t0 < seconds:
+            for _ in range(50):
+                fn()
+            n += 50
+            torch.cuda.synchronize()
+        stop.record()
+        torch.cuda.synchronize()
+        done.set()
+        th.join()
+        ms = start.elapsed_time(stop) / n
+        tf = fl / ms / 1e9
+        clocks.sort()
+        mhz = clocks[len(clocks) // 2] if clocks else None
+        res["cases"][name] = {"launches": n, "ms": round(ms, 4), "tflops": round(tf, 1),
+                              "sclk_mhz_median": mhz, "sclk_samples": len(clocks),
+                              "tflops_per_ghz": round(tf / (mhz / 1000), 1) if mhz else None}
     return res
 
 
@@ -605,7 +679,8 @@ def main():
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 counter passes behind roofline.traffic")
     ap.add_argument("--only", choices=["all", "fwd", "wgrad", "copy", "ref8", "refwgrad", "c5",
-                                       "routing", "dense", "small", "traffic", "hbm"],
+                                       "routing", "dense", "dense_clock", "small", "traffic",
+                                       "hbm"],
                     default="all",
                     help="fwd / wgrad: time only that GEMM (for profiler runs); copy: a plain "
                          "1 GiB device-to-device copy, the reference for HBM byte counters; "
@@ -613,6 +688,8 @@ def main():
                          "wgrad shapes only; c5: the full "
                          "expert-FFN layer step only; routing: C5 as a routed top-8 layer; "
                          "dense: C2's shape as one dense GEMM, with hipBLASLt beside it; "
+                         "dense_clock: the same back to back for 5 s per case with the "
+                         "shader clock sampled; "
                          "small: launches with fewer tiles than compute units, split or not; "
                          "hbm: plain-kernel HBM rates beside the casts; "
                          "traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes of fwd and copy "
@@ -647,6 +724,9 @@ def main():
         return
     if args.only == "dense":
         print(json.dumps(dense_c2_shape(torch, mxfp8gg, dev)), flush=True)
+        return
+    if args.only == "dense_clock":
+        print(json.dumps(dense_sustained(torch, mxfp8gg, dev)), flush=True)
         return
     if args.only == "ref8":
         print(json.dumps(ref_equal_shapes(torch, mxfp8gg, workloads, dev)), flush=True)

@@ -781,8 +781,9 @@ __device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4
     uint32_t am = amax16_of_chunk(a);
     am = quad_max(am);
     const uint32_t b = e8m0_from_amax16<MODE>(am);
-    const uint2 o = __any(b == 255u) ? encode_chunk8<MODE, false, true>(a, b)
-                                     : encode_chunk8<MODE, false, false>(a, b);
+    const uint2 o = __any(needs_full_encoder<MODE, false>(b))
+                        ? encode_chunk8<MODE, false, true>(a, b)
+                        : encode_chunk8<MODE, false, false>(a, b);
     const uint32_t tok = q0 + q;
     if (tok >= qbeg && tok < qend) {
       *reinterpret_cast<uint2*>(aq + (int64_t)tok * ldq + pg + 8u * k) = o;

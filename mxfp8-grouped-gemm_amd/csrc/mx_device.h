@@ -171,9 +171,9 @@ __device__ __forceinline__ uint32_t encode4_any(float x0, float x1, float x2, fl
   return e4m3_pack4<SW>(y[0], y[1], y[2], y[3]);
 }
 
-// Compile-time choice: ANY = the wave holds a NaN block somewhere (callers
-// test that once per wave with __any, so the common case has no per-lane
-// branch and no NaN handling).
+// Compile-time choice: ANY = some block of the wave needs the full encoder
+// (needs_full_encoder; callers test that once per wave with __any, so the
+// common case has no per-lane branch and no NaN or Inf handling).
 template <int MODE, bool SW, bool ANY>
 __device__ __forceinline__ uint32_t encode4_sel(float x0, float x1, float x2, float x3,
                                                 uint32_t b) {
@@ -185,13 +185,52 @@ __device__ __forceinline__ uint32_t encode4_sel(float x0, float x1, float x2, fl
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
+// Scale bytes whose blocks the short encoder must not take (callers reduce
+// this over the wave and pick ANY = true when any lane has one): NaN blocks
+// (255) in every configuration, and for RCEIL with the hardware converter also
+// blocks holding an infinity (254, which no finite amax reaches: the largest
+// finite bf16 gives 247), since v_cvt_scalef32_pk_fp8_bf16 does not clamp and
+// would turn inf into the NaN code instead of 448.
+template <int MODE, bool SW>
+__device__ __forceinline__ bool needs_full_encoder(uint32_t b) {
+  return (MODE == kModeRceil && !SW) ? b >= 254u : b == 255u;
+}
+
+// Payload bytes of the four bf16 values in words w0 (bytes 0, 1) and w1
+// (bytes 2, 3) of a block with scale byte b.  RCEIL through the hardware
+// converter: v_cvt_scalef32_pk_fp8_bf16 divides a bf16 pair by the scale
+// 2^(b-127) and rounds to nearest even, which is exactly x * 2^(127-b) rounded
+// as the f32 path rounds it.  RCEIL picks b so that amax <= 448 * 2^(b-127),
+// so no value of a finite block needs the clamp; b == 0 means a multiplier of
+// 1.  Checked bit for bit against the f32 path over every bf16 pattern and
+// scale byte; the GPU cast tests repeat that through the oracle.
+template <int MODE, bool SW, bool ANY>
+__device__ __forceinline__ uint32_t encode4_words(uint32_t w0, uint32_t w1, uint32_t b) {
+  if constexpr (MODE == kModeRceil && !SW && !ANY) {
+    typedef short i16x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const float s = b == 0u ? 1.0f : __uint_as_float(b << 23);
+    i16x2 o = {0, 0};
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(bf16x2, w0), s, false);
+    o = __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(bf16x2, w1), s, true);
+    return __builtin_bit_cast(uint32_t, o);
+  } else {
+    return encode4_sel<MODE, SW, ANY>(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), b);
+  }
+}
+
+// Word of bf16 values lo16(a) | lo16(b) << 16 (HI: the high halves).
+template <bool HI>
+__device__ __forceinline__ uint32_t pair_halves(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, HI ? 0x07060302u : 0x05040100u);
+}
+
 // Payload bytes of the eight bf16 values of a chunk under block byte b
-// (ANY: NaN blocks possible, see encode4_sel).
+// (ANY: see encode4_sel).
 template <int MODE, bool SW, bool ANY>
 __device__ __forceinline__ uint2 encode_chunk8(const uint4& v, uint32_t b) {
-  return make_uint2(
-      encode4_sel<MODE, SW, ANY>(bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y), b),
-      encode4_sel<MODE, SW, ANY>(bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w), b));
+  return make_uint2(encode4_words<MODE, SW, ANY>(v.x, v.y, b),
+                    encode4_words<MODE, SW, ANY>(v.z, v.w, b));
 }
 
 // Sixteen scale bytes b[0..15] (one per word) written to p..p+15 as one

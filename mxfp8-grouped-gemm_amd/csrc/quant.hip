@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void k_quant_dim0(const uint16_t* __restrict__
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         b[u] = e8m0_from_amax16<MODE>(quad_max(amax16_of_chunk(v[4 * h + u])));
-        nan |= b[u] == 255u;
+        nan |= needs_full_encoder<MODE, SW>(b[u]);
       }
       sw[h] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
       const bool any_nan = __any(nan);
@@ -203,14 +203,16 @@ __device__ __forceinline__ void token_payload(const uint4 (&v)[16], const uint32
     uint32_t o[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      float y[4];
+      uint32_t w[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int i = 4 * k + u;
-        const uint32_t w = (j >> 1) == 0 ? v[i].x : (j >> 1) == 1 ? v[i].y : (j >> 1) == 2 ? v[i].z : v[i].w;
-        y[u] = (j & 1) ? bf16_hi(w) : bf16_lo(w);
+        w[u] = (j >> 1) == 0 ? v[i].x : (j >> 1) == 1 ? v[i].y : (j >> 1) == 2 ? v[i].z : v[i].w;
       }
-      o[k] = encode4_sel<MODE, SW, ANY>(y[0], y[1], y[2], y[3], bytes[j]);
+      // feature j of positions 4k .. 4k+3, paired into two bf16 words
+      const uint32_t p0 = (j & 1) ? pair_halves<true>(w[0], w[1]) : pair_halves<false>(w[0], w[1]);
+      const uint32_t p1 = (j & 1) ? pair_halves<true>(w[2], w[3]) : pair_halves<false>(w[2], w[3]);
+      o[k] = encode4_words<MODE, SW, ANY>(p0, p1, bytes[j]);
     }
     // whole 128-byte lines (eight lanes): streaming stores (measured +1..4%;
     // the row-wise payload, 64-byte pieces of a line, is slower streamed)
@@ -325,7 +327,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATHER ? 4 
       m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x4E, 0xF, 0xF, false));
       rb[2 * t] = e8m0_from_amax16<MODE>(m & 0xFFFFu);
       rb[2 * t + 1] = e8m0_from_amax16<MODE>(m >> 16);
-      nan |= (rb[2 * t] == 255u) | (rb[2 * t + 1] == 255u);
+      nan |= needs_full_encoder<MODE, SW>(rb[2 * t]) ||
+             needs_full_encoder<MODE, SW>(rb[2 * t + 1]);
     }
     uint8_t* qrow = ro.q + tok0 * ro.ldq + f;
     if (__any(nan))
@@ -361,7 +364,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATHER ? 4 
     m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x128, 0xF, 0xF, false));
     bytes[2 * k] = e8m0_from_amax16<MODE>(m & 0xFFFFu);
     bytes[2 * k + 1] = e8m0_from_amax16<MODE>(m >> 16);
-    tnan |= (bytes[2 * k] == 255u) | (bytes[2 * k + 1] == 255u);
+    tnan |= needs_full_encoder<MODE, SW>(bytes[2 * k]) ||
+            needs_full_encoder<MODE, SW>(bytes[2 * k + 1]);
   }
   if (__any(tnan))
     token_payload<MODE, SW, true>(v, bytes, qt + (int64_t)f * ldqt + P, ldqt, out_ok);

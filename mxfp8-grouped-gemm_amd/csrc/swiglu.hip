@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void k_swiglu_dim0(
       uint32_t am = amax16_of_chunk(a[k]);
       am = quad_max(am);
       b[k] = e8m0_from_amax16<MODE>(am);
-      nan |= b[k] == 255u;
+      nan |= needs_full_encoder<MODE, SW>(b[k]);
     }
     if (__any(nan))
       swiglu_dim0_store<MODE, SW, true>(a, b, a_out, lda, q, ldq, s, s_row, s_blk, r0, rows, cc,
@@ -172,15 +172,10 @@ struct SwigluBwdArgs {
   int32_t cols, E;
 };
 
-__device__ __forceinline__ float half_f(const uint2& v, int j) {
-  const uint32_t w = (j >> 1) == 0 ? v.x : v.y;
-  return (j & 1) ? bf16_hi(w) : bf16_lo(w);
-}
-
 // Token-axis cast of the lane's 4 features x 16 positions held in v[0..15]:
 // feature j goes to row j of `qrow` (16 payload bytes; qrow already points at
 // column P of the lane's first feature row).  ANY: some block of the wave
-// holds a NaN (decided once per wave, so the common case runs the short
+// needs the full encoder (decided once per wave, so the common case runs the short
 // encoder without per-lane branches).
 template <int MODE, bool SW, bool ANY>
 __device__ __forceinline__ void token_axis_payload(const uint2 (&v)[16], const uint32_t (&bytes)[4],
@@ -189,9 +184,16 @@ __device__ __forceinline__ void token_axis_payload(const uint2 (&v)[16], const u
   for (int j = 0; j < 4; ++j) {
     uint32_t o[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      o[k] = encode4_sel<MODE, SW, ANY>(half_f(v[4 * k], j), half_f(v[4 * k + 1], j),
-                                        half_f(v[4 * k + 2], j), half_f(v[4 * k + 3], j), bytes[j]);
+    for (int k = 0; k < 4; ++k) {
+      // feature j of positions 4k .. 4k+3, paired into two bf16 words
+      const uint32_t w0 = (j >> 1) == 0 ? v[4 * k].x : v[4 * k].y;
+      const uint32_t w1 = (j >> 1) == 0 ? v[4 * k + 1].x : v[4 * k + 1].y;
+      const uint32_t w2 = (j >> 1) == 0 ? v[4 * k + 2].x : v[4 * k + 2].y;
+      const uint32_t w3 = (j >> 1) == 0 ? v[4 * k + 3].x : v[4 * k + 3].y;
+      const uint32_t p0 = (j & 1) ? pair_halves<true>(w0, w1) : pair_halves<false>(w0, w1);
+      const uint32_t p1 = (j & 1) ? pair_halves<true>(w2, w3) : pair_halves<false>(w2, w3);
+      o[k] = encode4_words<MODE, SW, ANY>(p0, p1, bytes[j]);
+    }
     if (out_ok) *reinterpret_cast<uint4*>(qrow + j * ldqt) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
@@ -220,8 +222,9 @@ __device__ __forceinline__ void emit_token_axis(const uint2 (&v)[16], uint8_t* q
   bytes[1] = e8m0_from_amax16<MODE>(mx >> 16);
   bytes[2] = e8m0_from_amax16<MODE>(my & 0xFFFFu);
   bytes[3] = e8m0_from_amax16<MODE>(my >> 16);
-  const bool nan = (bytes[0] == 255u) | (bytes[1] == 255u) | (bytes[2] == 255u) |
-                   (bytes[3] == 255u);
+  const bool nan = needs_full_encoder<MODE, SW>(bytes[0]) ||
+                   needs_full_encoder<MODE, SW>(bytes[1]) ||
+                   needs_full_encoder<MODE, SW>(bytes[2]) || needs_full_encoder<MODE, SW>(bytes[3]);
   if (__any(nan))
     token_axis_payload<MODE, SW, true>(v, bytes, qrow, ldqt, out_ok);
   else
@@ -245,8 +248,7 @@ __device__ __forceinline__ void row_wise_payload(const uint2 (&v)[16], const uin
                                                  uint8_t* qrow, int64_t ldq, int ntok) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const uint32_t o = encode4_sel<MODE, SW, ANY>(bf16_lo(v[i].x), bf16_hi(v[i].x),
-                                                  bf16_lo(v[i].y), bf16_hi(v[i].y), bytes[i]);
+    const uint32_t o = encode4_words<MODE, SW, ANY>(v[i].x, v[i].y, bytes[i]);
     if (i < ntok) __builtin_nontemporal_store(o, reinterpret_cast<uint32_t*>(qrow + i * ldq));
   }
 }
@@ -285,7 +287,8 @@ __device__ __forceinline__ void emit_row_wise(const uint2 (&v)[16], uint8_t* qro
     m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x128, 0xF, 0xF, false));
     bytes[2 * t] = e8m0_from_amax16<MODE>(m & 0xFFFFu);
     bytes[2 * t + 1] = e8m0_from_amax16<MODE>(m >> 16);
-    nan |= (bytes[2 * t] == 255u) | (bytes[2 * t + 1] == 255u);
+    nan |= needs_full_encoder<MODE, SW>(bytes[2 * t]) ||
+           needs_full_encoder<MODE, SW>(bytes[2 * t + 1]);
   }
   if (__any(nan))
     row_wise_payload<MODE, SW, true>(v, bytes, qrow, ldq, ntok);
