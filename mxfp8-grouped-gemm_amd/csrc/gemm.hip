@@ -170,12 +170,13 @@ __device__ __forceinline__ void dma_x4(const desc_t& d, uint32_t lds_addr, uint3
       : "s"(lds_addr), "v"(voff), "s"(d), "s"(soff)
       : "memory", "m0");
 }
-__device__ __forceinline__ void dma_x1(const desc_t& d, uint32_t lds_addr, uint32_t voff) {
+__device__ __forceinline__ void dma_x1(const desc_t& d, uint32_t lds_addr, uint32_t voff,
+                                       uint32_t soff = 0) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
-      "buffer_load_dword %1, %2, 0 offen lds"
+      "buffer_load_dword %1, %2, %3 offen lds"
       :
-      : "s"(lds_addr), "v"(voff), "s"(d)
+      : "s"(lds_addr), "v"(voff), "s"(d), "s"(soff)
       : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -246,8 +247,10 @@ struct Stream {
     const uint32_t wave = wave_id();
     const uint32_t blk = (k0 >> 5) + wave;
     const bool ok = blk >= (klo >> 5) && blk < (kend >> 5);
-    dma_x1(X.scale, lds_offset(stage) + kScaleOff + 512u * wave + 256u * OP,
-           ok ? blk * X.lds + (OP ? sq : sp) : kOobOffset);
+    // the block's row offset is wave-uniform: it rides in the scalar offset,
+    // and an out-of-range block moves the whole load past num_records
+    dma_x1(X.scale, lds_offset(stage) + kScaleOff + 512u * wave + 256u * OP, OP ? sq : sp,
+           ok ? blk * X.lds : kOobOffset);
   }
 
   // The 16 data loads of one stage, back to back (prologue only).

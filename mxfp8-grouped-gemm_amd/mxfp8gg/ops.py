@@ -578,14 +578,23 @@ def _small_launch(M: int, N: int, E: int, device) -> bool:
     return m_tiles * ((N + 255) // 256) <= units // 2
 
 
-def _full_rounds(M: int, N: int, device) -> bool:
+def _full_rounds(M: int, N: int, E: int, device) -> bool:
     """True when the forward has at least one full round of 256x256 tiles for
-    any group sizes (ceil(M / 256) m-tiles at least).  Such a launch takes the
-    split entry: the kernel cuts a last round that fills at most half of the
-    units along K (at most 8 ranges) and leaves any other last round alone;
-    the fixed-order reduction then costs one short launch."""
+    any group sizes and some group sizes could leave its last round at most
+    half full.  Such a launch takes the split entry: the kernel cuts a last
+    round that fills at most half of the units along K (at most 8 ranges) and
+    leaves any other last round alone; the fixed-order reduction then costs
+    one short launch.  The m-tile count lies between ceil(M / 256) and
+    floor((M + 3(E-1) + 255 E) / 256) (see _small_launch), so a launch whose
+    every possible tile count fills its last round more than half (one
+    expert over whole rounds, for instance) skips that launch."""
     units = (_split_workspace_bytes(device) - 16384) // (256 * 256 * 4)
-    return ((M + 255) // 256) * ((N + 255) // 256) >= units
+    n_tiles = (N + 255) // 256
+    m_lo = (M + 255) // 256
+    m_hi = max(m_lo, (M + 3 * (E - 1) + 255 * E) // 256)
+    if m_lo * n_tiles < units:
+        return False
+    return any(0 < (m * n_tiles) % units <= units // 2 for m in range(m_lo, m_hi + 1))
 
 
 _MAX_OPERAND_BYTES = 0x7FFFFFF0   # the C ABI's bound on (rows - 1) * ld + K
@@ -622,9 +631,9 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
     over the idle units (mxgg_grouped_fwd_split; deterministic, equal to the
     unsplit result up to fp32 summation order).  None (default): when the
     launch is that small whatever the group sizes are, and when it has at
-    least one full round of tiles (the kernel then splits its last round only
-    if that round fills at most half of the units); True: always take the
-    split entry point; False: never.
+    least one full round of tiles and some group sizes could leave its last
+    round at most half full (the kernel then splits that round only if it
+    does); True: always take the split entry point; False: never.
     """
     _need_gpu(a, "a")
     _need_gpu(w, "w")
@@ -672,7 +681,7 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
                 e.data_ptr() if e is not None else None, E,
                 m, N, K, out.data_ptr() + r0 * out.stride(0) * esz, out.stride(0),
                 _out_code(out_dtype))
-        split = (_small_launch(m, N, E, a.device) or _full_rounds(m, N, a.device)) \
+        split = (_small_launch(m, N, E, a.device) or _full_rounds(m, N, E, a.device)) \
             if split_tail is None else split_tail
         if split and m > 0 and N > 0:
             ws = _split_workspace(a.device)

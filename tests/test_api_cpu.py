@@ -124,6 +124,26 @@ def test_wgrad_split_choice():
     assert ops.wgrad_split_tokens(4096, 256, 256, 2, 256) == 0
 
 
+def test_forward_split_entry_choice(monkeypatch):
+    # a workspace of 256 partials: a round is 256 tiles
+    monkeypatch.setattr(ops, "_split_workspace_bytes", lambda device: 16384 + 256 * 256 * 4 * 256)
+    # one expert over exactly 16 rounds: no last round to cut, no reduce launch
+    assert not ops._full_rounds(65536, 4096, 1, None)
+    assert not ops._small_launch(65536, 4096, 1, None)
+    # one more m-tile: a last round of 16 tiles, cut along K
+    assert ops._full_rounds(65536 + 1, 4096, 1, None)
+    # 32 ragged experts (C2): 256..287 m-tiles, some counts leave <= 128 tiles
+    assert ops._full_rounds(65536, 4096, 32, None)
+    # 5 experts over 6400 rows: 25..30 m-tiles x 16 n-tiles = 400..480 tiles,
+    # a last round of 144..224 tiles whatever the sizes: no split entry
+    assert not ops._full_rounds(6400, 4096, 5, None)
+    # 8 experts: up to 33 m-tiles, and 528 tiles leave a last round of 16
+    assert ops._full_rounds(6400, 4096, 8, None)
+    # less than a round: the small-launch rule decides
+    assert not ops._full_rounds(512, 2048, 1, None)
+    assert ops._small_launch(512, 2048, 1, None)
+
+
 # ---------------------------------------------------------------------------
 # weight-cast cache (host logic only: a stub stands in for the GPU cast)
 # ---------------------------------------------------------------------------
