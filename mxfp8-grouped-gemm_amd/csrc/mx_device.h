@@ -264,19 +264,64 @@ __device__ __forceinline__ float div_nr(float a, float b) {
   return q1 == q1 ? q1 : q;
 }
 
+// div_nr for finite a and finite b >= 1, where the residual step cannot
+// produce a NaN: the same operations without the fallback test.
+__device__ __forceinline__ float div_nr_finite(float a, float b) {
+  const float r = __builtin_amdgcn_rcpf(b);
+  const float q = a * r;
+  return __builtin_fmaf(__builtin_fmaf(-q, b, a), r, q);
+}
+
+// exp(x) for |x| <= 88, where neither overflow nor underflow can occur.
+// Cody-Waite reduction: x * log2(e) = n + f, with log2(e) split into a float
+// and the float of the remainder, n = rint, 2^f from v_exp_f32 and n put back
+// by ldexp.  These are the steps and the order of operations that the
+// device library's expf compiles to on gfx950 for such x, so the bits agree;
+// that function also tests x against its overflow and underflow bounds,
+// which this one leaves out.
+__device__ __forceinline__ float exp_moderate(float x) {
+  // no contraction: ph must be rounded before n is subtracted from it
+#pragma clang fp contract(off)
+  constexpr float kLog2eHi = 0x1.715476p+0f;
+  constexpr float kLog2eLo = 0x1.4ae0bep-26f;
+  const float ph = x * kLog2eHi;
+  const float pl = __builtin_fmaf(x, kLog2eLo, __builtin_fmaf(x, kLog2eHi, -ph));
+  const float n = __builtin_rintf(ph);
+  return __builtin_ldexpf(__builtin_amdgcn_exp2f((ph - n) + pl), (int)n);
+}
+
+// bf16 bit pattern of 88.0: |g| at or below it keeps exp(-g) and 1 + exp(-g)
+// finite and non-zero, the domain of exp_moderate and div_nr_finite.
+constexpr uint32_t kBf16Moderate = 0x42B0u;
+
 // SwiGLU of the two bf16 values of a word of gate and of up:
 // a = bf16(bf16(g / (1 + exp(-g))) * u), packed (torch's eager bf16
 // F.silu(gate) * up).  Shared by the standalone SwiGLU kernels and the
 // gate+up GEMM epilogue, so both give the same bits.
+// MOD: |g| <= 88 (kBf16Moderate) for both values, so exp(-g) and the quotient
+// need no range or NaN tests (same results on that domain).
+template <bool MOD>
 __device__ __forceinline__ uint32_t swiglu_a_word(uint32_t gw, uint32_t uw) {
   const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
-  const uint32_t sw = pack_bf16x2(div_nr(g0, 1.0f + expf(-g0)), div_nr(g1, 1.0f + expf(-g1)));
+  const uint32_t sw =
+      MOD ? pack_bf16x2(div_nr_finite(g0, 1.0f + exp_moderate(-g0)),
+                        div_nr_finite(g1, 1.0f + exp_moderate(-g1)))
+          : pack_bf16x2(div_nr(g0, 1.0f + expf(-g0)), div_nr(g1, 1.0f + expf(-g1)));
   return pack_bf16x2(bf16_lo(sw) * bf16_lo(uw), bf16_hi(sw) * bf16_hi(uw));
 }
 
+// SwiGLU of a 16-byte chunk (eight values).  Activations almost always have
+// |gate| <= 88: a chunk whose gate values are all in that range in every lane
+// of the wave takes the math without range tests (one vote, no per-lane
+// branch).  Callers run it with the whole wave active.
 __device__ __forceinline__ uint4 swiglu_a_chunk(const uint4& g, const uint4& u) {
-  return make_uint4(swiglu_a_word(g.x, u.x), swiglu_a_word(g.y, u.y), swiglu_a_word(g.z, u.z),
-                    swiglu_a_word(g.w, u.w));
+  const uint32_t gm = pk_max_u16(pk_max_u16(abs_bf16x2(g.x), abs_bf16x2(g.y)),
+                                 pk_max_u16(abs_bf16x2(g.z), abs_bf16x2(g.w)));
+  if (__all(max(gm & 0xFFFFu, gm >> 16) <= kBf16Moderate))
+    return make_uint4(swiglu_a_word<true>(g.x, u.x), swiglu_a_word<true>(g.y, u.y),
+                      swiglu_a_word<true>(g.z, u.z), swiglu_a_word<true>(g.w, u.w));
+  return make_uint4(swiglu_a_word<false>(g.x, u.x), swiglu_a_word<false>(g.y, u.y),
+                    swiglu_a_word<false>(g.z, u.z), swiglu_a_word<false>(g.w, u.w));
 }
 
 // Group tables of the token-axis casts, staged in LDS by every workgroup:

@@ -32,25 +32,66 @@ struct ActWord {
   uint32_t a, dg, du;  // two packed bf16 results each
 };
 
+// exp(-g) and a / b; MOD: |g| <= 88 (kBf16Moderate) holds for every value, so
+// the overflow, underflow and NaN tests of the general forms can be left out
+// (same results on that domain).
+template <bool MOD>
+__device__ __forceinline__ float exp_neg(float g) {
+  return MOD ? exp_moderate(-g) : expf(-g);
+}
+template <bool MOD>
+__device__ __forceinline__ float quot(float a, float b) {
+  return MOD ? div_nr_finite(a, b) : div_nr(a, b);
+}
+
+template <bool MOD>
 __device__ __forceinline__ float dsilu_term(float ds, float g, float ex) {
-  const float sig = div_nr(1.0f, 1.0f + ex);
+  const float sig = quot<MOD>(1.0f, 1.0f + ex);
   return ds * sig * (1.0f + g * (1.0f - sig));
 }
 
 // a, d_gate and d_up for the two values of a word of gate, up and grad_a.
+template <bool MOD>
 __device__ __forceinline__ ActWord swiglu_bwd_word(uint32_t gw, uint32_t uw, uint32_t dw) {
   const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
   const float u0 = bf16_lo(uw), u1 = bf16_hi(uw);
   const float d0 = bf16_lo(dw), d1 = bf16_hi(dw);
-  const float e0 = expf(-g0), e1 = expf(-g1);
-  const uint32_t sw = pack_bf16x2(div_nr(g0, 1.0f + e0), div_nr(g1, 1.0f + e1));  // s = bf16(silu(g))
+  const float e0 = exp_neg<MOD>(g0), e1 = exp_neg<MOD>(g1);
+  const uint32_t sw = pack_bf16x2(quot<MOD>(g0, 1.0f + e0),
+                                  quot<MOD>(g1, 1.0f + e1));  // s = bf16(silu(g))
   const uint32_t dsw = pack_bf16x2(d0 * u0, d1 * u1);                   // bf16(grad_a * up)
   const float s0 = bf16_lo(sw), s1 = bf16_hi(sw);
   ActWord r;
   r.a = pack_bf16x2(s0 * u0, s1 * u1);
   r.du = pack_bf16x2(d0 * s0, d1 * s1);
-  r.dg = pack_bf16x2(dsilu_term(bf16_lo(dsw), g0, e0), dsilu_term(bf16_hi(dsw), g1, e1));
+  r.dg = pack_bf16x2(dsilu_term<MOD>(bf16_lo(dsw), g0, e0),
+                     dsilu_term<MOD>(bf16_hi(dsw), g1, e1));
   return r;
+}
+
+// a, d_gate and d_up of a lane's 16 token rows x 4 features, in place of
+// gate, up and grad_a, one token at a time (interleaving all 32 exp/div
+// chains would need far more registers than this streaming kernel can hold).
+// Activations almost always have |gate| <= 88: a token row whose gate values
+// are all in that range in every lane of the wave takes the math without
+// range tests (one vote per row, no per-lane branch).
+__device__ __forceinline__ void swiglu_bwd_rows(uint2 (&A)[16], uint2 (&DG)[16], uint2 (&DU)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const uint32_t gm = pk_max_u16(abs_bf16x2(A[i].x), abs_bf16x2(A[i].y));
+    ActWord r0, r1;
+    if (__all(max(gm & 0xFFFFu, gm >> 16) <= kBf16Moderate)) {
+      r0 = swiglu_bwd_word<true>(A[i].x, DG[i].x, DU[i].x);
+      r1 = swiglu_bwd_word<true>(A[i].y, DG[i].y, DU[i].y);
+    } else {
+      r0 = swiglu_bwd_word<false>(A[i].x, DG[i].x, DU[i].x);
+      r1 = swiglu_bwd_word<false>(A[i].y, DG[i].y, DU[i].y);
+    }
+    A[i] = make_uint2(r0.a, r1.a);
+    DG[i] = make_uint2(r0.dg, r1.dg);
+    DU[i] = make_uint2(r0.du, r1.du);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -336,8 +377,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
   const uint16_t* upp = p.up + tok0 * p.ldh + f;
   const uint16_t* dp = p.da + tok0 * p.ldda + f;
   // gate, up and da are loaded into A, DG, DU and replaced there by a,
-  // d_gate and d_up, one token at a time (interleaving all 32 exp/div chains
-  // would need far more registers than this streaming kernel can hold)
+  // d_gate and d_up
   uint2 A[16], DG[16], DU[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -348,15 +388,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
       DU[i] = *reinterpret_cast<const uint2*>(dp + i * p.ldda);
     }
   }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const ActWord r0 = swiglu_bwd_word(A[i].x, DG[i].x, DU[i].x);
-    const ActWord r1 = swiglu_bwd_word(A[i].y, DG[i].y, DU[i].y);
-    A[i] = make_uint2(r0.a, r1.a);
-    DG[i] = make_uint2(r0.dg, r1.dg);
-    DU[i] = make_uint2(r0.du, r1.du);
-    __builtin_amdgcn_sched_barrier(0);
-  }
+  swiglu_bwd_rows(A, DG, DU);
 
   const int64_t cols = p.cols;
   store_bf16_rows(DG, p.dh, tok0 * p.lddh + f, p.lddh, ntok);
