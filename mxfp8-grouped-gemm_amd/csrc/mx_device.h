@@ -225,6 +225,11 @@ __device__ __forceinline__ uint32_t pair_halves(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, HI ? 0x07060302u : 0x05040100u);
 }
 
+// max of the two 16-bit halves of a, and of b, packed: low half from a.
+__device__ __forceinline__ uint32_t half_max_pair(uint32_t a, uint32_t b) {
+  return pk_max_u16(pair_halves<false>(a, b), pair_halves<true>(a, b));
+}
+
 // Payload bytes of the eight bf16 values of a chunk under block byte b
 // (ANY: see encode4_sel).
 template <int MODE, bool SW, bool ANY>

@@ -320,9 +320,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATHER ? 4 
     bool nan = false;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
-      const uint32_t m0 = amax16_of_chunk(v[2 * t]);
-      const uint32_t m1 = amax16_of_chunk(v[2 * t + 1]);
-      uint32_t m = m0 | (m1 << 16);
+      // packed |x| maxima of the two chunks, then each chunk's two halves
+      const uint32_t p0 = pk_max_u16(pk_max_u16(abs_bf16x2(v[2 * t].x), abs_bf16x2(v[2 * t].y)),
+                                     pk_max_u16(abs_bf16x2(v[2 * t].z), abs_bf16x2(v[2 * t].w)));
+      const uint32_t p1 =
+          pk_max_u16(pk_max_u16(abs_bf16x2(v[2 * t + 1].x), abs_bf16x2(v[2 * t + 1].y)),
+                     pk_max_u16(abs_bf16x2(v[2 * t + 1].z), abs_bf16x2(v[2 * t + 1].w)));
+      uint32_t m = half_max_pair(p0, p1);
       m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0xB1, 0xF, 0xF, false));
       m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x4E, 0xF, 0xF, false));
       rb[2 * t] = e8m0_from_amax16<MODE>(m & 0xFFFFu);

@@ -320,7 +320,7 @@ __device__ __forceinline__ void emit_row_wise(const uint2 (&v)[16], uint8_t* qro
   for (int t = 0; t < 8; ++t) {
     const uint32_t m0 = pk_max_u16(abs_bf16x2(v[2 * t].x), abs_bf16x2(v[2 * t].y));
     const uint32_t m1 = pk_max_u16(abs_bf16x2(v[2 * t + 1].x), abs_bf16x2(v[2 * t + 1].y));
-    uint32_t m = max(m0 & 0xFFFFu, m0 >> 16) | (max(m1 & 0xFFFFu, m1 >> 16) << 16);
+    uint32_t m = half_max_pair(m0, m1);
     // the block's eight lanes are those of one 16-lane row with the same
     // parity: rotations by 2, 4 and 8 within the row reach all of them
     m = pk_max_u16(m, (uint32_t)__builtin_amdgcn_update_dpp((int)m, (int)m, 0x122, 0xF, 0xF, false));
