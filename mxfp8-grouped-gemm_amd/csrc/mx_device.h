@@ -259,18 +259,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
-// a / b from the hardware reciprocal and one Newton step on the residual
-// (fma), the classic correction that returns the correctly rounded quotient
-// except in rare near-tie cases; infinities and NaN fall back to a * rcp(b).
-__device__ __forceinline__ float div_nr(float a, float b) {
-  const float r = __builtin_amdgcn_rcpf(b);
-  const float q = a * r;
-  const float q1 = __builtin_fmaf(__builtin_fmaf(-q, b, a), r, q);
-  return q1 == q1 ? q1 : q;
-}
-
-// div_nr for finite a and finite b >= 1, where the residual step cannot
-// produce a NaN: the same operations without the fallback test.
+// a / b for finite a and 1 <= b < 2^126, from the hardware reciprocal and one
+// Newton step on the residual (fma): the classic correction that returns the
+// correctly rounded quotient except in rare near-tie cases.  Outside that
+// domain (b = inf, or a reciprocal below the normal range, which v_rcp_f32
+// flushes to zero) callers divide with the compiler's IEEE division.
 __device__ __forceinline__ float div_nr_finite(float a, float b) {
   const float r = __builtin_amdgcn_rcpf(b);
   const float q = a * r;
@@ -295,28 +288,30 @@ __device__ __forceinline__ float exp_moderate(float x) {
   return __builtin_ldexpf(__builtin_amdgcn_exp2f((ph - n) + pl), (int)n);
 }
 
-// bf16 bit pattern of 88.0: |g| at or below it keeps exp(-g) and 1 + exp(-g)
-// finite and non-zero, the domain of exp_moderate and div_nr_finite.
-constexpr uint32_t kBf16Moderate = 0x42B0u;
+// bf16 bit pattern of 87.0: |g| at or below it keeps exp(-g) finite and
+// 1 + exp(-g) below 2^126 (e^87 = 6.1e37 < 8.5e37), the domain of
+// exp_moderate and div_nr_finite.
+constexpr uint32_t kBf16Moderate = 0x42AEu;
 
 // SwiGLU of the two bf16 values of a word of gate and of up:
 // a = bf16(bf16(g / (1 + exp(-g))) * u), packed (torch's eager bf16
 // F.silu(gate) * up).  Shared by the standalone SwiGLU kernels and the
 // gate+up GEMM epilogue, so both give the same bits.
-// MOD: |g| <= 88 (kBf16Moderate) for both values, so exp(-g) and the quotient
-// need no range or NaN tests (same results on that domain).
+// MOD: |g| <= 87 (kBf16Moderate) for both values, so exp(-g) needs no range
+// tests and the quotient can come from the corrected reciprocal; otherwise
+// IEEE division, exact for every input.
 template <bool MOD>
 __device__ __forceinline__ uint32_t swiglu_a_word(uint32_t gw, uint32_t uw) {
   const float g0 = bf16_lo(gw), g1 = bf16_hi(gw);
   const uint32_t sw =
       MOD ? pack_bf16x2(div_nr_finite(g0, 1.0f + exp_moderate(-g0)),
                         div_nr_finite(g1, 1.0f + exp_moderate(-g1)))
-          : pack_bf16x2(div_nr(g0, 1.0f + expf(-g0)), div_nr(g1, 1.0f + expf(-g1)));
+          : pack_bf16x2(g0 / (1.0f + expf(-g0)), g1 / (1.0f + expf(-g1)));
   return pack_bf16x2(bf16_lo(sw) * bf16_lo(uw), bf16_hi(sw) * bf16_hi(uw));
 }
 
 // SwiGLU of a 16-byte chunk (eight values).  Activations almost always have
-// |gate| <= 88: a chunk whose gate values are all in that range in every lane
+// |gate| <= 87: a chunk whose gate values are all in that range in every lane
 // of the wave takes the math without range tests (one vote, no per-lane
 // branch).  Callers run it with the whole wave active.
 __device__ __forceinline__ uint4 swiglu_a_chunk(const uint4& g, const uint4& u) {

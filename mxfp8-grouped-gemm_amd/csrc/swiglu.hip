@@ -11,9 +11,10 @@
 //
 // Arithmetic is torch's eager bf16 semantics for the same expression
 // (F.silu(gate) * up with autograd), so the fused path equals the unfused one
-// (bit for bit on the GPU in the tests; the quotients below come from a
-// corrected reciprocal, which matches the IEEE quotient except in rare
-// near-tie cases, and bf16 rounding is the hardware round-to-nearest-even):
+// (bit for bit on the GPU in the tests; for gates with |g| <= 87 the
+// quotients below come from a corrected reciprocal, which matches the IEEE
+// quotient except in rare near-tie cases, beyond that from IEEE division, and
+// bf16 rounding is the hardware round-to-nearest-even):
 //   s      = bf16(g / (1 + exp(-g)))                 (silu, fp32 inside)
 //   a      = bf16(s * u)
 //   d_up   = bf16(da * s)
@@ -32,16 +33,17 @@ struct ActWord {
   uint32_t a, dg, du;  // two packed bf16 results each
 };
 
-// exp(-g) and a / b; MOD: |g| <= 88 (kBf16Moderate) holds for every value, so
-// the overflow, underflow and NaN tests of the general forms can be left out
-// (same results on that domain).
+// exp(-g) and a / b; MOD: |g| <= 87 (kBf16Moderate) holds for every value, so
+// exp needs no overflow or underflow tests and the quotient can come from
+// the corrected reciprocal; otherwise expf and IEEE division, exact for
+// every input.
 template <bool MOD>
 __device__ __forceinline__ float exp_neg(float g) {
   return MOD ? exp_moderate(-g) : expf(-g);
 }
 template <bool MOD>
 __device__ __forceinline__ float quot(float a, float b) {
-  return MOD ? div_nr_finite(a, b) : div_nr(a, b);
+  return MOD ? div_nr_finite(a, b) : a / b;
 }
 
 template <bool MOD>
@@ -72,7 +74,7 @@ __device__ __forceinline__ ActWord swiglu_bwd_word(uint32_t gw, uint32_t uw, uin
 // a, d_gate and d_up of a lane's 16 token rows x 4 features, in place of
 // gate, up and grad_a, one token at a time (interleaving all 32 exp/div
 // chains would need far more registers than this streaming kernel can hold).
-// Activations almost always have |gate| <= 88: a token row whose gate values
+// Activations almost always have |gate| <= 87: a token row whose gate values
 // are all in that range in every lane of the wave takes the math without
 // range tests (one vote per row, no per-lane branch).
 __device__ __forceinline__ void swiglu_bwd_rows(uint2 (&A)[16], uint2 (&DG)[16], uint2 (&DU)[16]) {

@@ -56,6 +56,15 @@ def _h(gpu, M, F, seed, specials=False):
         h[5, 3] = float("inf")
         h[6, F + 7] = float("-inf")
         h[7, 40] = float("nan")
+    if specials and M > 10:
+        # the kernels' range-test-free math takes rows whose gates all lie in
+        # |g| <= 87: both edges of that domain; gates past it where
+        # 1 + exp(-g) >= 2^126 has a reciprocal below the normal range
+        # (-88.7 < g < -87.3); gates where exp(-g) overflows (g < -88.7) or
+        # underflows to a denormal or zero (g > 87)
+        h[8, :6] = torch.tensor([87.0, -87.0, 87.5, -87.5, 88.0, -88.0])
+        h[9, :6] = torch.tensor([88.5, -88.5, 100.0, -100.0, 104.0, -104.0])
+        h[10, 1::7] = -87.0
     return h.to(torch.bfloat16)
 
 
