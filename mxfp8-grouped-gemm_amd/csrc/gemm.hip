@@ -406,24 +406,29 @@ __device__ __forceinline__ void release_barrier() {
 //
 // Stage s lives in slot s%2; f0 holds k-step 0 and f1 k-step 1 of a stage.
 // A DMA instruction holds up its wave's issue until the address unit takes
-// it, so the 18 loads of a stage are spread one per MFMA.  Per stage, with the
-// MFMA count reached at each point:
-//    0  MFMA rows 0-1 of f0 while all of k-step 1 is read into f1
+// it, so the 18 loads of a stage are spread three on every four MFMAs.  Per
+// stage, with the MFMA count reached at each point:
+//    0  MFMA rows 0-1 of f0 while the rest of k-step 1 (Q fragments, P
+//       fragments 2-3, scales) is read into f1
 //    8  release barrier: every wave has read all of slot s%2 -> MFMA rows 2-3
-//       of f0 and rows 0-1 of f1, each followed by one data load of stage s+2
-//       into that slot (8 P, then 8 Q)
-//   24  publish barrier: everything older than those 16 loads, i.e. all of
-//       stage s+1, has landed -> MFMA rows 2-3 of f1 with the two scale loads
-//       of stage s+2 and all of stage s+1's k-step 0 read into f0 (18 reads
-//       in each of the two read phases)
-// so every load has at least 31 MFMAs of compute to land in.  The wait counts
-// do not depend on whether scales are loaded: the scale loads of a stage come
-// after its data loads, and the publish wait keeps exactly the 16 newest
-// (data) loads in flight.
+//       of f0, with the first 6 loads of stage s+2 into that slot
+//   16  publish barrier: everything older than those 6 loads, i.e. all of
+//       stage s+1, has landed -> MFMA rows 0-3 of f1 with the other 12 loads
+//       of stage s+2 (the two scale loads last), while stage s+1's k-step 0
+//       is read into f0 and its P fragments 0-1 of k-step 1 into f1 once the
+//       MFMAs that used those registers have issued
+// A stage's fragment reads thus spread over the 24 MFMAs from one publish to
+// the next release.  With the publish at MFMA 24 they had 16, and the LDS,
+// which also takes the DMA's writes, had no slack left in them.  Every load
+// has at least 18 MFMAs to land in.  The wait counts do not depend on whether
+// scales are loaded: the scale loads of a stage come after its data loads, and
+// the publish wait leaves exactly the 6 newest (data) loads in flight.
 // MASK (unscaled only): [klo, kend) may have any bounds; chunks that straddle
 // them are loaded whole and the bytes outside are zeroed in registers before
 // they reach an MFMA.  Only experts whose token range is not a multiple of 16
-// take this path.
+// take this path.  It keeps the publish barrier at MFMA 24 (12 loads of
+// stage s+2 before it, the fragment reads of stage s+1 after it), under which
+// its masking registers do not spill.
 template <bool SCALED, bool MASK = false>
 __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Operand& Q,
                                          uint32_t klo, uint32_t kend, v16f (&acc)[4][4]) {
@@ -454,6 +459,10 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
   Frags f0, f1;
   read_head<SCALED, 0>(sm.ring[0], fa, f0);
   read_tail<0>(sm.ring[0], fa, f0);
+  if constexpr (!MASK) {
+    read_p<1>(sm.ring[0], fa, f1, 0);
+    read_p<1>(sm.ring[0], fa, f1, 1);
+  }
   // Past the last stage the loads fetch zeros into a slot nobody reads again,
   // and the final head read fetches a stale slot that is never used, so the
   // loop body has no branches.  nst >= 1 here (kend > klo); written as a
@@ -469,52 +478,105 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
       mask_frags<0>(f0, kbeg + s * kStageK, klo, kend);
       MXGG_FENCE();
     }
-    // MFMA 0-7: rows 0-1 of f0 while k-step 1 of stage s is read into f1
-    mfma1<0, 0>(f0, acc); read_q<1>(cur, fa, f1, 0); MXGG_FENCE();
-    mfma1<0, 1>(f0, acc); read_q<1>(cur, fa, f1, 1); MXGG_FENCE();
-    mfma1<0, 2>(f0, acc); read_q<1>(cur, fa, f1, 2); MXGG_FENCE();
-    mfma1<0, 3>(f0, acc); read_q<1>(cur, fa, f1, 3); MXGG_FENCE();
-    mfma1<1, 0>(f0, acc); read_p<1>(cur, fa, f1, 0); MXGG_FENCE();
-    mfma1<1, 1>(f0, acc); read_p<1>(cur, fa, f1, 1); MXGG_FENCE();
-    mfma1<1, 2>(f0, acc); read_p<1>(cur, fa, f1, 2); MXGG_FENCE();
-    mfma1<1, 3>(f0, acc); read_p<1>(cur, fa, f1, 3); read_scales<SCALED, 1>(cur, fa, f1); MXGG_FENCE();
-    release_barrier();
-    MXGG_FENCE();
     if constexpr (MASK) {
-      mask_frags<1>(f1, kbeg + s * kStageK, klo, kend);
+      // the masked loop keeps the publish barrier at MFMA 24 (the schedule
+      // below makes its extra masking registers spill)
+      // MFMA 0-7: rows 0-1 of f0 while k-step 1 of stage s is read into f1
+      mfma1<0, 0>(f0, acc); read_q<1>(cur, fa, f1, 0); MXGG_FENCE();
+      mfma1<0, 1>(f0, acc); read_q<1>(cur, fa, f1, 1); MXGG_FENCE();
+      mfma1<0, 2>(f0, acc); read_q<1>(cur, fa, f1, 2); MXGG_FENCE();
+      mfma1<0, 3>(f0, acc); read_q<1>(cur, fa, f1, 3); MXGG_FENCE();
+      mfma1<1, 0>(f0, acc); read_p<1>(cur, fa, f1, 0); MXGG_FENCE();
+      mfma1<1, 1>(f0, acc); read_p<1>(cur, fa, f1, 1); MXGG_FENCE();
+      mfma1<1, 2>(f0, acc); read_p<1>(cur, fa, f1, 2); MXGG_FENCE();
+      mfma1<1, 3>(f0, acc); read_p<1>(cur, fa, f1, 3); read_scales<SCALED, 1>(cur, fa, f1); MXGG_FENCE();
+      release_barrier();
       MXGG_FENCE();
+      if constexpr (MASK) {
+        mask_frags<1>(f1, kbeg + s * kStageK, klo, kend);
+        MXGG_FENCE();
+      }
+      // MFMA 8-31: the 18 loads of stage s+2, three on every four MFMAs
+      mfma1<2, 0>(f0, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
+      mfma1<2, 1>(f0, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
+      mfma1<2, 2>(f0, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
+      mfma1<2, 3>(f0, acc); MXGG_FENCE();
+      mfma1<3, 0>(f0, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
+      mfma1<3, 1>(f0, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
+      mfma1<3, 2>(f0, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
+      mfma1<3, 3>(f0, acc); MXGG_FENCE();
+      mfma1<0, 0>(f1, acc); st.load_p(cur, P, bp, 6); MXGG_FENCE();
+      mfma1<0, 1>(f1, acc); st.load_p(cur, P, bp, 7); MXGG_FENCE();
+      mfma1<0, 2>(f1, acc); st.load_q(cur, Q, bq, 0); MXGG_FENCE();
+      mfma1<0, 3>(f1, acc); MXGG_FENCE();
+      mfma1<1, 0>(f1, acc); st.load_q(cur, Q, bq, 1); MXGG_FENCE();
+      mfma1<1, 1>(f1, acc); st.load_q(cur, Q, bq, 2); MXGG_FENCE();
+      mfma1<1, 2>(f1, acc); st.load_q(cur, Q, bq, 3); MXGG_FENCE();
+      mfma1<1, 3>(f1, acc); MXGG_FENCE();
+      // MFMA 24-31: stage s+1 published (all but the 12 loads above have
+      // landed); the remaining 6 loads of stage s+2 and the head of stage s+1's
+      // k-step 0 into f0
+      wait_barrier<12>();
+      MXGG_FENCE();
+      const uint32_t k2 = kbeg + (s + 2) * kStageK;
+      mfma1<2, 0>(f1, acc); st.load_q(cur, Q, bq, 4); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
+      mfma1<2, 1>(f1, acc); st.load_q(cur, Q, bq, 5); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
+      mfma1<2, 2>(f1, acc); st.load_q(cur, Q, bq, 6); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
+      mfma1<2, 3>(f1, acc); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
+      mfma1<3, 0>(f1, acc); st.load_q(cur, Q, bq, 7); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
+      mfma1<3, 1>(f1, acc); st.template load_scale<0>(cur, P, k2); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
+      mfma1<3, 2>(f1, acc); st.template load_scale<1>(cur, Q, k2); read_p<0>(nxt, fa, f0, 2); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
+      mfma1<3, 3>(f1, acc); read_p<0>(nxt, fa, f0, 3); MXGG_FENCE();
+    } else {
+      // MFMA 0-7: rows 0-1 of f0 while the rest of k-step 1 of stage s (Q
+      // fragments, P fragments 2-3, scales) is read into f1
+      mfma1<0, 0>(f0, acc); read_q<1>(cur, fa, f1, 0); MXGG_FENCE();
+      mfma1<0, 1>(f0, acc); read_q<1>(cur, fa, f1, 1); MXGG_FENCE();
+      mfma1<0, 2>(f0, acc); read_q<1>(cur, fa, f1, 2); MXGG_FENCE();
+      mfma1<0, 3>(f0, acc); read_q<1>(cur, fa, f1, 3); MXGG_FENCE();
+      mfma1<1, 0>(f0, acc); read_p<1>(cur, fa, f1, 2); MXGG_FENCE();
+      mfma1<1, 1>(f0, acc); read_p<1>(cur, fa, f1, 3); MXGG_FENCE();
+      mfma1<1, 2>(f0, acc); read_scales<SCALED, 1>(cur, fa, f1); MXGG_FENCE();
+      mfma1<1, 3>(f0, acc); MXGG_FENCE();
+      release_barrier();
+      MXGG_FENCE();
+      if constexpr (MASK) {
+        mask_frags<1>(f1, kbeg + s * kStageK, klo, kend);
+        MXGG_FENCE();
+      }
+      // MFMA 8-15: rows 2-3 of f0; the first 6 loads of stage s+2
+      mfma1<2, 0>(f0, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
+      mfma1<2, 1>(f0, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
+      mfma1<2, 2>(f0, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
+      mfma1<2, 3>(f0, acc); MXGG_FENCE();
+      mfma1<3, 0>(f0, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
+      mfma1<3, 1>(f0, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
+      mfma1<3, 2>(f0, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
+      mfma1<3, 3>(f0, acc); MXGG_FENCE();
+      // MFMA 16-31: stage s+1 published (all but the 6 loads above have
+      // landed); rows 0-3 of f1 with the other 12 loads of stage s+2, all of
+      // stage s+1's k-step 0 read into f0 and its P fragments 0-1 of k-step 1
+      // into f1 once rows 0 and 1 of f1 are done
+      wait_barrier<6>();
+      MXGG_FENCE();
+      const uint32_t k2 = kbeg + (s + 2) * kStageK;
+      mfma1<0, 0>(f1, acc); st.load_p(cur, P, bp, 6); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
+      mfma1<0, 1>(f1, acc); st.load_p(cur, P, bp, 7); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
+      mfma1<0, 2>(f1, acc); st.load_q(cur, Q, bq, 0); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
+      mfma1<0, 3>(f1, acc); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
+      mfma1<1, 0>(f1, acc); st.load_q(cur, Q, bq, 1); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
+      mfma1<1, 1>(f1, acc); st.load_q(cur, Q, bq, 2); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
+      mfma1<1, 2>(f1, acc); st.load_q(cur, Q, bq, 3); read_p<0>(nxt, fa, f0, 2); MXGG_FENCE();
+      mfma1<1, 3>(f1, acc); read_p<0>(nxt, fa, f0, 3); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
+      mfma1<2, 0>(f1, acc); st.load_q(cur, Q, bq, 4); read_p<1>(nxt, fa, f1, 0); MXGG_FENCE();
+      mfma1<2, 1>(f1, acc); st.load_q(cur, Q, bq, 5); read_p<1>(nxt, fa, f1, 1); MXGG_FENCE();
+      mfma1<2, 2>(f1, acc); st.load_q(cur, Q, bq, 6); MXGG_FENCE();
+      mfma1<2, 3>(f1, acc); MXGG_FENCE();
+      mfma1<3, 0>(f1, acc); st.load_q(cur, Q, bq, 7); MXGG_FENCE();
+      mfma1<3, 1>(f1, acc); st.template load_scale<0>(cur, P, k2); MXGG_FENCE();
+      mfma1<3, 2>(f1, acc); st.template load_scale<1>(cur, Q, k2); MXGG_FENCE();
+      mfma1<3, 3>(f1, acc); MXGG_FENCE();
     }
-    // MFMA 8-31: the 18 loads of stage s+2, three on every four MFMAs
-    mfma1<2, 0>(f0, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
-    mfma1<2, 1>(f0, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
-    mfma1<2, 2>(f0, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
-    mfma1<2, 3>(f0, acc); MXGG_FENCE();
-    mfma1<3, 0>(f0, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
-    mfma1<3, 1>(f0, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
-    mfma1<3, 2>(f0, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
-    mfma1<3, 3>(f0, acc); MXGG_FENCE();
-    mfma1<0, 0>(f1, acc); st.load_p(cur, P, bp, 6); MXGG_FENCE();
-    mfma1<0, 1>(f1, acc); st.load_p(cur, P, bp, 7); MXGG_FENCE();
-    mfma1<0, 2>(f1, acc); st.load_q(cur, Q, bq, 0); MXGG_FENCE();
-    mfma1<0, 3>(f1, acc); MXGG_FENCE();
-    mfma1<1, 0>(f1, acc); st.load_q(cur, Q, bq, 1); MXGG_FENCE();
-    mfma1<1, 1>(f1, acc); st.load_q(cur, Q, bq, 2); MXGG_FENCE();
-    mfma1<1, 2>(f1, acc); st.load_q(cur, Q, bq, 3); MXGG_FENCE();
-    mfma1<1, 3>(f1, acc); MXGG_FENCE();
-    // MFMA 24-31: stage s+1 published (all but the 12 loads above have
-    // landed); the remaining 6 loads of stage s+2 and the head of stage s+1's
-    // k-step 0 into f0
-    wait_barrier<12>();
-    MXGG_FENCE();
-    const uint32_t k2 = kbeg + (s + 2) * kStageK;
-    mfma1<2, 0>(f1, acc); st.load_q(cur, Q, bq, 4); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
-    mfma1<2, 1>(f1, acc); st.load_q(cur, Q, bq, 5); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
-    mfma1<2, 2>(f1, acc); st.load_q(cur, Q, bq, 6); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
-    mfma1<2, 3>(f1, acc); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
-    mfma1<3, 0>(f1, acc); st.load_q(cur, Q, bq, 7); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
-    mfma1<3, 1>(f1, acc); st.template load_scale<0>(cur, P, k2); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
-    mfma1<3, 2>(f1, acc); st.template load_scale<1>(cur, Q, k2); read_p<0>(nxt, fa, f0, 2); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
-    mfma1<3, 3>(f1, acc); read_p<0>(nxt, fa, f0, 3); MXGG_FENCE();
   } while (++s < nst);
   // Drain the loads past the end before the next tile's prologue reuses the slots.
   wait_barrier<0>();
