@@ -292,6 +292,28 @@ int mxgg_grouped_fwd_swiglu_quant(const void* a, int64_t lda, const void* a_scal
                                   int64_t lds, int scale_layout, int scale_mode, void* stream);
 
 /*
+ * mxgg_grouped_fwd_swiglu_quant for the training forward: also writes the
+ * bf16 gate+up projection h [M, 2F] (gate columns 0..F-1, up columns F..2F-1;
+ * row stride ldh elements, ldh >= 2F, ldh % 8 == 0, h 16-byte aligned) that
+ * the SwiGLU backward (mxgg_swiglu_bwd_quant) re-reads.  h equals
+ * mxgg_grouped_fwd's bf16 output bit for bit and q / scales equal
+ * mxgg_grouped_fwd_swiglu_quant's, on the rows inside the groups; rows past
+ * the last group end are not written.  Saves the standalone SwiGLU cast's
+ * re-read of h.
+ * Replaces the reference's training layer step gate/up GEMMs, eager
+ * `silu(hg) * hu` (whose inputs autograd keeps for the backward) and
+ * `.to(float8)` (e2e_bench.py:56-61).
+ */
+int mxgg_grouped_fwd_swiglu_quant_keep_h(const void* a, int64_t lda, const void* a_scales,
+                                         int64_t ldas, const void* w, int64_t w_group_stride,
+                                         int64_t ldw, const void* w_scales,
+                                         int64_t ws_group_stride, int64_t ldws,
+                                         const int32_t* group_ends, int64_t num_groups, int64_t M,
+                                         int64_t F, int64_t K, void* h, int64_t ldh, void* q,
+                                         int64_t ldq, void* scales, int64_t lds, int scale_layout,
+                                         int scale_mode, void* stream);
+
+/*
  * mxgg_grouped_fwd with a caller-owned workspace of at least
  * mxgg_grouped_fwd_workspace_bytes() bytes (16-byte aligned; contents need no
  * initialisation and are scratch after the call).  When the tiles of the

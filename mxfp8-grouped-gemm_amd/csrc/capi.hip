@@ -550,12 +550,12 @@ int mxgg_grouped_fwd(const void* a, int64_t lda, const void* a_scales, int64_t l
 
 int64_t mxgg_grouped_fwd_workspace_bytes(void) { return fwd_split_workspace_bytes(); }
 
-int mxgg_grouped_fwd_swiglu_quant(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
-                                  const void* w, int64_t w_group_stride, int64_t ldw,
-                                  const void* w_scales, int64_t ws_group_stride, int64_t ldws,
-                                  const int32_t* group_ends, int64_t num_groups, int64_t M,
-                                  int64_t F, int64_t K, void* q, int64_t ldq, void* scales,
-                                  int64_t lds, int scale_layout, int scale_mode, void* stream) {
+static int grouped_fwd_swiglu(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                              const void* w, int64_t w_group_stride, int64_t ldw,
+                              const void* w_scales, int64_t ws_group_stride, int64_t ldws,
+                              const int32_t* group_ends, int64_t num_groups, int64_t M, int64_t F,
+                              int64_t K, void* h, int64_t ldh, void* q, int64_t ldq, void* scales,
+                              int64_t lds, int scale_layout, int scale_mode, void* stream) {
   if (scale_mode != MXGG_SCALE_RCEIL && scale_mode != MXGG_SCALE_FLOOR)
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd_swiglu_quant: unknown scale_mode %d",
                      scale_mode);
@@ -578,11 +578,42 @@ int mxgg_grouped_fwd_swiglu_quant(const void* a, int64_t lda, const void* a_scal
     if ((reinterpret_cast<uintptr_t>(q) & 7u) != 0 || ldq % 8 != 0)
       return set_error(MXGG_ERR_ALIGNMENT,
                        "grouped_fwd_swiglu_quant: q must be 8-byte aligned with ldq %% 8 == 0");
+    if (h && ldh < 2 * F)
+      return set_error(MXGG_ERR_SHAPE, "grouped_fwd_swiglu_quant: ldh smaller than 2F");
+    if (h && (!aligned16(h) || ldh % 8 != 0))
+      return set_error(MXGG_ERR_ALIGNMENT,
+                       "grouped_fwd_swiglu_quant: h must be 16-byte aligned with ldh %% 8 == 0");
   }
   const SwigluOut sw{q, ldq, scales, lds, scale_layout, scale_mode};
   return grouped_fwd(a, lda, a_scales, ldas, w, w_group_stride, ldw, w_scales, ws_group_stride,
-                     ldws, group_ends, num_groups, M, 2 * F, K, nullptr, 0, MXGG_OUT_BF16, nullptr,
-                     stream, &sw);
+                     ldws, group_ends, num_groups, M, 2 * F, K, h, h ? ldh : 0, MXGG_OUT_BF16,
+                     nullptr, stream, &sw);
+}
+
+int mxgg_grouped_fwd_swiglu_quant(const void* a, int64_t lda, const void* a_scales, int64_t ldas,
+                                  const void* w, int64_t w_group_stride, int64_t ldw,
+                                  const void* w_scales, int64_t ws_group_stride, int64_t ldws,
+                                  const int32_t* group_ends, int64_t num_groups, int64_t M,
+                                  int64_t F, int64_t K, void* q, int64_t ldq, void* scales,
+                                  int64_t lds, int scale_layout, int scale_mode, void* stream) {
+  return grouped_fwd_swiglu(a, lda, a_scales, ldas, w, w_group_stride, ldw, w_scales,
+                            ws_group_stride, ldws, group_ends, num_groups, M, F, K, nullptr, 0, q,
+                            ldq, scales, lds, scale_layout, scale_mode, stream);
+}
+
+int mxgg_grouped_fwd_swiglu_quant_keep_h(const void* a, int64_t lda, const void* a_scales,
+                                         int64_t ldas, const void* w, int64_t w_group_stride,
+                                         int64_t ldw, const void* w_scales,
+                                         int64_t ws_group_stride, int64_t ldws,
+                                         const int32_t* group_ends, int64_t num_groups, int64_t M,
+                                         int64_t F, int64_t K, void* h, int64_t ldh, void* q,
+                                         int64_t ldq, void* scales, int64_t lds, int scale_layout,
+                                         int scale_mode, void* stream) {
+  if (M > 0 && F > 0 && !h)
+    return set_error(MXGG_ERR_INVALID_ARGUMENT, "grouped_fwd_swiglu_quant: null h");
+  return grouped_fwd_swiglu(a, lda, a_scales, ldas, w, w_group_stride, ldw, w_scales,
+                            ws_group_stride, ldws, group_ends, num_groups, M, F, K, h, ldh, q, ldq,
+                            scales, lds, scale_layout, scale_mode, stream);
 }
 
 int mxgg_grouped_fwd_split(const void* a, int64_t lda, const void* a_scales, int64_t ldas,

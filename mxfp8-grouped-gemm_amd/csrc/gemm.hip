@@ -825,11 +825,15 @@ __device__ __forceinline__ void epilogue_bf16(Smem& sm, const v16f (&acc)[4][4],
   __syncthreads();
 }
 
-template <int MODE>
+// KEEP: the bf16 gate and up values are also stored, as h[tok][pg + c] and
+// h[tok][F + pg + c] (ldh elements per row), for a backward that re-reads h:
+// the same bits epilogue_bf16 writes for the unfused projection.
+template <int MODE, bool KEEP>
 __device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4], uint8_t* aq,
                                                 int64_t ldq, uint8_t* sc, int64_t s_row,
                                                 int64_t s_blk, uint32_t q0, uint32_t qbeg,
-                                                uint32_t qend, uint32_t pg) {
+                                                uint32_t qend, uint32_t pg, uint16_t* h,
+                                                int64_t ldh, uint32_t F) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
   uint8_t* st = &sm.ring[0][0];
@@ -842,6 +846,13 @@ __device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4
     const uint8_t* row = st + q * 512u;
     const uint4 g = *reinterpret_cast<const uint4*>(row + ((k ^ sw) << 4));
     const uint4 u = *reinterpret_cast<const uint4*>(row + ((16u + (k ^ sw)) << 4));
+    const uint32_t tok = q0 + q;
+    // h first: its stores drain while the activation is computed
+    if (KEEP && tok >= qbeg && tok < qend) {
+      uint16_t* hr = h + (int64_t)tok * ldh + pg + 8u * k;
+      __builtin_nontemporal_store(u32x4{g.x, g.y, g.z, g.w}, reinterpret_cast<u32x4*>(hr));
+      __builtin_nontemporal_store(u32x4{u.x, u.y, u.z, u.w}, reinterpret_cast<u32x4*>(hr + F));
+    }
     const uint4 a = swiglu_a_chunk(g, u);
     uint32_t am = amax16_of_chunk(a);
     am = quad_max(am);
@@ -849,7 +860,6 @@ __device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4
     const uint2 o = __any(needs_full_encoder<MODE, false>(b))
                         ? encode_chunk8<MODE, false, true>(a, b)
                         : encode_chunk8<MODE, false, false>(a, b);
-    const uint32_t tok = q0 + q;
     if (tok >= qbeg && tok < qend) {
       *reinterpret_cast<uint2*>(aq + (int64_t)tok * ldq + pg + 8u * k) = o;
       if ((k & 3u) == 0)
@@ -942,13 +952,24 @@ __device__ __forceinline__ void group_range(const int32_t* gend, int g, int32_t&
 // but not stored.
 // ---------------------------------------------------------------------------
 // Output of the forward: bf16 or fp32 out[m][n], or (SWIGLU_*) the MXFP8
-// cast of SiLU(gate) * up for a weight holding [gate; up] rows.
-enum { kOutBf16 = 0, kOutF32 = 1, kOutSwigluRceil = 2, kOutSwigluFloor = 3 };
+// cast of SiLU(gate) * up for a weight holding [gate; up] rows, with
+// (SWIGLU_KEEP_*) or without the bf16 [gate | up] rows in `out`.
+enum {
+  kOutBf16 = 0,
+  kOutF32 = 1,
+  kOutSwigluRceil = 2,
+  kOutSwigluFloor = 3,
+  kOutSwigluKeepRceil = 4,
+  kOutSwigluKeepFloor = 5
+};
 
 template <bool SCALED, int OUT>
 __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint32_t gm) {
   constexpr bool F32 = OUT == kOutF32;
   constexpr bool SWIGLU = OUT >= kOutSwigluRceil;
+  constexpr bool KEEP = OUT >= kOutSwigluKeepRceil;
+  constexpr int SW_MODE =
+      (OUT == kOutSwigluRceil || OUT == kOutSwigluKeepRceil) ? kModeRceil : kModeFloor;
   __shared__ Smem sm;
   const int E = args.group_ends ? args.E : 1;
   const int32_t M = args.M;
@@ -1047,9 +1068,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
       epilogue<true>(sm, acc, slot, 1024, 0u, 0u, 256u, 0u, 256u);
     } else if constexpr (SWIGLU) {
       mainloop<SCALED>(sm, P, Q, 0u, K, acc);
-      epilogue_swiglu<OUT == kOutSwigluRceil ? kModeRceil : kModeFloor>(
-          sm, acc, args.aq, args.ldaq, args.as_out, args.as_row, args.as_blk, q0, (uint32_t)gb,
-          (uint32_t)ge, p0);
+      epilogue_swiglu<SW_MODE, KEEP>(sm, acc, args.aq, args.ldaq, args.as_out, args.as_row,
+                                     args.as_blk, q0, (uint32_t)gb, (uint32_t)ge, p0,
+                                     static_cast<uint16_t*>(args.out), args.ldo,
+                                     (uint32_t)args.N / 2u);
     } else {
       mainloop<SCALED>(sm, P, Q, 0u, K, acc);
       const int64_t ldo_bytes = args.ldo * (F32 ? 4 : 2);
@@ -1377,8 +1399,9 @@ hipError_t launch_grouped_fwd(const FwdArgs& a, hipStream_t stream) {
   if (a.M == 0 || a.N == 0) return hipSuccess;
   const dim3 grid(persistent_grid()), block(kThreads);
   const uint32_t gm = 8;
-  const int out = a.swiglu_mode == MXGG_SCALE_RCEIL   ? kOutSwigluRceil
-                  : a.swiglu_mode == MXGG_SCALE_FLOOR ? kOutSwigluFloor
+  const bool keep = a.out != nullptr;
+  const int out = a.swiglu_mode == MXGG_SCALE_RCEIL   ? (keep ? kOutSwigluKeepRceil : kOutSwigluRceil)
+                  : a.swiglu_mode == MXGG_SCALE_FLOOR ? (keep ? kOutSwigluKeepFloor : kOutSwigluFloor)
                   : a.out_f32                         ? kOutF32
                                                       : kOutBf16;
 #define MXGG_FWD(S, O) hipLaunchKernelGGL((k_grouped_fwd<S, O>), grid, block, 0, stream, a, gm)
@@ -1387,6 +1410,8 @@ hipError_t launch_grouped_fwd(const FwdArgs& a, hipStream_t stream) {
     case kOutF32: MXGG_FWD(S, kOutF32); break;                    \
     case kOutSwigluRceil: MXGG_FWD(S, kOutSwigluRceil); break;    \
     case kOutSwigluFloor: MXGG_FWD(S, kOutSwigluFloor); break;    \
+    case kOutSwigluKeepRceil: MXGG_FWD(S, kOutSwigluKeepRceil); break; \
+    case kOutSwigluKeepFloor: MXGG_FWD(S, kOutSwigluKeepFloor); break; \
     default: MXGG_FWD(S, kOutBf16); break;                        \
   }
   if (a.scaled) {

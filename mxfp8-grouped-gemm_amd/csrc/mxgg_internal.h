@@ -160,9 +160,11 @@ struct FwdArgs {
   // sparse round of tiles are then split along K over the idle CUs.
   float* split_ws;
   // Fused SwiGLU output (swiglu_mode = MXGG_SCALE_RCEIL / _FLOOR, -1 = off):
-  // w holds [gate; up] (N = 2F rows), and instead of `out` the kernel writes
-  // the row-wise MXFP8 cast of a = SiLU(gate) * up: payload aq [M, F] (row
-  // stride ldaq bytes), scale byte (m, b) at as_out[m * as_row + b * as_blk].
+  // w holds [gate; up] (N = 2F rows), and the kernel writes the row-wise
+  // MXFP8 cast of a = SiLU(gate) * up: payload aq [M, F] (row stride ldaq
+  // bytes), scale byte (m, b) at as_out[m * as_row + b * as_blk].  `out` is
+  // then either nullptr or the bf16 [gate | up] rows h [M, 2F] (row stride ldo
+  // elements, 16-byte aligned rows).
   int32_t swiglu_mode;
   uint8_t* aq;
   uint8_t* as_out;

@@ -80,6 +80,11 @@ SIGNATURES = {
         [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
          _P, _I64, _P, _I64, _I, _I, _P],
     ),
+    "mxgg_grouped_fwd_swiglu_quant_keep_h": (
+        _I,
+        [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,
+         _P, _I64, _P, _I64, _P, _I64, _I, _I, _P],
+    ),
     "mxgg_grouped_fwd_split": (
         _I,
         [_P, _I64, _P, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64,

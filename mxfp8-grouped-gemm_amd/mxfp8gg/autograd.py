@@ -103,8 +103,8 @@ class MXFP8ExpertFFN(torch.autograd.Function):
 
     forward : x and both weights cast both ways from one read each (the
               token-axis / N-blocked casts are kept for backward) -> gate+up
-              GEMM -> h = [gate | up] (bf16, kept) -> SwiGLU + cast of a in
-              one kernel -> down GEMM
+              GEMM writing h = [gate | up] (bf16, kept) and the cast of
+              SwiGLU(h) from its epilogue -> down GEMM
     backward: dY cast both ways; dA = dY . Wd (MXFP8 dgrad); one kernel turns
               (h, dA) into the row-wise and token-axis casts of dh =
               [d_gate | d_up] and the token-axis cast of a; then dWd = dY^T . a,
@@ -117,8 +117,7 @@ class MXFP8ExpertFFN(torch.autograd.Function):
         wcast = weight_cache.get if weight_cache is not None else ops.quant_weight_dual
         xq, xs, xqt, xst, _ = ops.to_mxfp8_dual(x, ends, scaling_mode)
         (wq, ws), (wgt, wgts) = wcast(w_gate_up, scaling_mode)
-        h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
-        aq, as_ = ops.swiglu_quant(h, scaling_mode)
+        aq, as_, h = _gate_up_act(xq, xs, wq, ws, ends, scaling_mode, keep_h=True)
         (dq, ds), (wdt, wdts) = wcast(w_down, scaling_mode)
         y = ops.zero_rows_past_groups(ops.grouped_mm(aq, dq, ends, as_, ds, out_dtype=torch.bfloat16),
                                       ends)
@@ -167,17 +166,19 @@ def _weight_dim0(w, scaling_mode, weight_cache):
     return ops.to_mxfp8_dim0(w, scaling_mode)
 
 
-def _gate_up_act(xq, xs, wq, ws, ends, scaling_mode):
-    """MXFP8 cast of SiLU(gate) * up of the gate+up projection: one fused
-    kernel when the intermediate size allows (F % 128 == 0, activations under
-    2 GiB), else the GEMM's bf16 output through the standalone SwiGLU cast
-    (the same bits either way)."""
+def _gate_up_act(xq, xs, wq, ws, ends, scaling_mode, keep_h=False):
+    """MXFP8 cast of SiLU(gate) * up of the gate+up projection (and, with
+    keep_h, the bf16 projection h itself as a third result): one fused kernel
+    when the intermediate size allows (F % 128 == 0, activations under 2 GiB),
+    else the GEMM's bf16 output through the standalone SwiGLU cast (the same
+    bits either way, on the rows inside the groups)."""
     F2 = wq.shape[1]
     if F2 % 256 == 0 and (xq.shape[0] == 0 or
                           (xq.shape[0] - 1) * xq.stride(0) + xq.shape[1] <= ops._MAX_OPERAND_BYTES):
-        return ops.grouped_mm_swiglu_quant(xq, wq, ends, xs, ws, scaling_mode)
+        return ops.grouped_mm_swiglu_quant(xq, wq, ends, xs, ws, scaling_mode, return_h=keep_h)
     h = ops.grouped_mm(xq, wq, ends, xs, ws, out_dtype=torch.bfloat16)
-    return ops.swiglu_quant(h, scaling_mode)
+    aq, as_ = ops.swiglu_quant(h, scaling_mode)
+    return (aq, as_, h) if keep_h else (aq, as_)
 
 
 def _ffn_forward_only(x, w_gate_up, w_down, offs, scaling_mode, weight_cache=None):

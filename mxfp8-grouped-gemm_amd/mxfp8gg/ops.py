@@ -694,18 +694,22 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
 
 def grouped_mm_swiglu_quant(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
                             a_scales: torch.Tensor | None = None,
-                            w_scales: torch.Tensor | None = None, scaling_mode="rceil"):
+                            w_scales: torch.Tensor | None = None, scaling_mode="rceil",
+                            return_h: bool = False):
     """The gate+up projection, SiLU(gate) * up and its row-wise MXFP8 cast in
-    one kernel (mxgg_grouped_fwd_swiglu_quant), for forward-only passes.
+    one kernel (mxgg_grouped_fwd_swiglu_quant).
 
     a: e4m3 [M, K]; w: e4m3 [E, 2F, K] with gate rows first (the fused gate+up
     weight); scales and offs as for grouped_mm.  F % 128 == 0.  Returns
     (q float8_e4m3fn [M, F], scales uint8 [M, F/32] view of block-major
     storage), equal to swiglu_quant(grouped_mm(a, w, ...)) on the rows inside
-    the groups (rows past the last group end are not written); the bf16
-    [M, 2F] projection output is never materialised.  The reference runs the
-    gate and up GEMMs, eager SiLU * up and the fp8 cast separately
-    (e2e_bench.py:56-61)."""
+    the groups (rows past the last group end are not written).  Without
+    return_h the bf16 [M, 2F] projection is never materialised (forward-only
+    passes); with it (the training forward, mxgg_grouped_fwd_swiglu_quant_keep_h)
+    the kernel also writes h = grouped_mm(a, w, ...) for the backward and
+    returns (q, scales, h); rows of h past the last group end are zero.  The
+    reference runs the gate and up GEMMs, eager SiLU * up and the fp8 cast
+    separately (e2e_bench.py:56-61)."""
     _need_gpu(a, "a")
     _need_gpu(w, "w")
     if a.dim() != 2 or w.dim() != 3:
@@ -736,13 +740,22 @@ def grouped_mm_swiglu_quant(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor
     q = torch.empty((M, F), dtype=_FP8, device=a.device)
     buf = _block_major_buffer(M, F // 32, a.device)
     lib = _lib.load()
-    _lib.check(lib.mxgg_grouped_fwd_swiglu_quant(
-        a8.data_ptr(), a8.stride(0), sa.data_ptr() if sa is not None else None, ldas,
-        w8.data_ptr(), w8.stride(0), w8.stride(1), sw.data_ptr() if sw is not None else None,
-        wsg, ldws, ends.data_ptr() if ends is not None else None, E, M, F, K,
-        q.data_ptr(), F, buf.data_ptr(), buf.stride(0), _lib.SCALES_BLOCK_MAJOR,
-        _mode(scaling_mode), _stream_ptr(a)), "grouped_fwd_swiglu_quant")
-    return q, buf[:, :M].t()
+    head = (a8.data_ptr(), a8.stride(0), sa.data_ptr() if sa is not None else None, ldas,
+            w8.data_ptr(), w8.stride(0), w8.stride(1), sw.data_ptr() if sw is not None else None,
+            wsg, ldws, ends.data_ptr() if ends is not None else None, E, M, F, K)
+    tail = (q.data_ptr(), F, buf.data_ptr(), buf.stride(0), _lib.SCALES_BLOCK_MAJOR,
+            _mode(scaling_mode), _stream_ptr(a))
+    if not return_h:
+        _lib.check(lib.mxgg_grouped_fwd_swiglu_quant(*head, *tail), "grouped_fwd_swiglu_quant")
+        return q, buf[:, :M].t()
+    # rows past the last group end are not written by the kernel: zero them
+    # as the library's grouped_mm + zero_rows_past_groups would give
+    h = torch.empty((M, 2 * F), dtype=torch.bfloat16, device=a.device)
+    _lib.check(lib.mxgg_grouped_fwd_swiglu_quant_keep_h(*head, h.data_ptr(), 2 * F, *tail),
+               "grouped_fwd_swiglu_quant_keep_h")
+    if ends is not None:
+        zero_rows_past_groups(h, ends)
+    return q, buf[:, :M].t(), h
 
 
 def fused_grouped_fwd(a_fp8, w_fp8, offs, a_scales=None, w_scales=None,

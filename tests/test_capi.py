@@ -297,6 +297,50 @@ def test_swiglu_quant_dim0_empty_is_noop(lib):
     assert _swiglu0(lib, rows=0, g=None, u=None, q=None, s=None) == _lib.OK
 
 
+def _fwd_swiglu(lib, keep_h, **kw):
+    a = dict(a=FAKE, lda=256, a_s=None, ldas=0, w=FAKE, wg=512 * 256, ldw=256, w_s=None, wsg=0,
+             ldws=0, ends=None, E=1, M=64, F=256, K=256, h=FAKE, ldh=512, q=FAKE, ldq=256,
+             s=FAKE, lds=64, layout=BM, mode=0)
+    a.update(kw)
+    head = (a["a"], a["lda"], a["a_s"], a["ldas"], a["w"], a["wg"], a["ldw"], a["w_s"], a["wsg"],
+            a["ldws"], a["ends"], a["E"], a["M"], a["F"], a["K"])
+    tail = (a["q"], a["ldq"], a["s"], a["lds"], a["layout"], a["mode"], None)
+    if keep_h:
+        return lib.mxgg_grouped_fwd_swiglu_quant_keep_h(*head, a["h"], a["ldh"], *tail)
+    return lib.mxgg_grouped_fwd_swiglu_quant(*head, *tail)
+
+
+@pytest.mark.parametrize("keep_h", [False, True])
+@pytest.mark.parametrize("kw,status", [
+    (dict(mode=4), _lib.ERR_INVALID_ARGUMENT),
+    (dict(layout=2), _lib.ERR_INVALID_ARGUMENT),
+    (dict(F=192), _lib.ERR_SHAPE),                   # F % 128 != 0
+    (dict(q=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ldq=128), _lib.ERR_SHAPE),                 # ldq < F
+    (dict(lds=32), _lib.ERR_SHAPE),                  # block-major ld < M
+    (dict(q=FAKE + 4), _lib.ERR_ALIGNMENT),
+    (dict(K=100), _lib.ERR_SHAPE),
+    (dict(a=None), _lib.ERR_INVALID_ARGUMENT),
+])
+def test_grouped_fwd_swiglu_quant_rejects(lib, keep_h, kw, status):
+    assert _fwd_swiglu(lib, keep_h, **kw) == status
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(h=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ldh=384), _lib.ERR_SHAPE),                 # ldh < 2F
+    (dict(h=FAKE + 8), _lib.ERR_ALIGNMENT),
+    (dict(ldh=516), _lib.ERR_ALIGNMENT),             # ldh % 8 != 0
+])
+def test_grouped_fwd_swiglu_quant_keep_h_rejects(lib, kw, status):
+    assert _fwd_swiglu(lib, True, **kw) == status
+
+
+def test_grouped_fwd_swiglu_quant_empty_is_noop(lib):
+    for keep_h in (False, True):
+        assert _fwd_swiglu(lib, keep_h, M=0, a=None, h=None, q=None, s=None) == _lib.OK
+
+
 def _swiglu_bwd(lib, **kw):
     a = dict(g=FAKE, u=FAKE + 128, ldh=128, da=FAKE, ldga=64, rows=64, cols=64, ends=FAKE, E=2,
              cap=128, dq=FAKE, lddq=128, ds=FAKE, ldds=64, dqt=FAKE, lddqt=128, dst=FAKE,

@@ -1,13 +1,16 @@
 """GPU parity of the gate+up GEMM fused with SwiGLU and the MXFP8 cast
-(mxgg_grouped_fwd_swiglu_quant) through the C ABI.
+(mxgg_grouped_fwd_swiglu_quant, and mxgg_grouped_fwd_swiglu_quant_keep_h,
+which also writes the bf16 projection h for the training backward) through
+the C ABI.
 
-The fused kernel must give the same bytes as the unfused path it replaces --
-the grouped GEMM's bf16 output h followed by the standalone SwiGLU cast, each
-pinned against the oracle by tests/test_gpu_gemm.py and
+The fused kernels must give the same bytes as the unfused path they replace
+-- the grouped GEMM's bf16 output h followed by the standalone SwiGLU cast,
+each pinned against the oracle by tests/test_gpu_gemm.py and
 tests/test_gpu_swiglu.py -- on every row inside the groups, for both scale
 modes, both scale layouts, scaled and unscaled operands, ragged and empty
-groups, and at C5's full shape.  An independent check against the oracle's
-float64 GEMM and float64 SiLU * up pins the pairing of gate and up columns."""
+groups, and at C5's full shape; the kept h equals the GEMM's bf16 output bit
+for bit.  An independent check against the oracle's float64 GEMM and float64
+SiLU * up pins the pairing of gate and up columns."""
 import numpy as np
 import pytest
 import torch
@@ -57,6 +60,46 @@ def test_fused_gate_up_equals_unfused(gpu, sizes, F, K, scaled, mode):
     assert q.shape == rq.shape and s.shape == rs.shape
     assert torch.equal(q.view(torch.uint8)[ins], rq.view(torch.uint8)[ins])
     assert torch.equal(s[ins], rs[ins])
+    # the training variant: the same cast plus h itself
+    qk, sk, hk = ops.grouped_mm_swiglu_quant(xq, wq, offs, xs, ws, mode, return_h=True)
+    assert hk.shape == h.shape and hk.dtype == torch.bfloat16
+    assert torch.equal(hk.view(torch.int16)[ins], h.view(torch.int16)[ins])
+    assert torch.equal(qk.view(torch.uint8)[ins], rq.view(torch.uint8)[ins])
+    assert torch.equal(sk[ins], rs[ins])
+
+
+def test_fused_keep_h_strides_and_rows_past_the_end(gpu):
+    # through the C ABI: h with a padded row stride, rows past the last group
+    # end and the padding columns must keep their fill bytes
+    sizes, F, K = [70, 0, 121], 128, 256
+    xq, xs, wq, ws, offs = _operands(gpu, sizes, F, K, 135)
+    tail = 37
+    xq = torch.cat([xq, xq[:tail]])
+    xs = torch.cat([xs.contiguous(), xs[:tail].contiguous()])
+    M, E = xq.shape[0], wq.shape[0]
+    sa, ldas = ops._scales_2d(xs, M, K // 32, "xs")
+    sw, wsg, ldws = ops._scales_3d(ws, E, 2 * F, K // 32, "ws")
+    ldh, ldq = 2 * F + 24, F + 40
+    h = torch.full((M, ldh), 0x7FC1, dtype=torch.int16, device=gpu)
+    q = torch.full((M, ldq), 0xAB, dtype=torch.uint8, device=gpu)
+    s = torch.full((F // 32, (M + 15) // 16 * 16), 0xCD, dtype=torch.uint8, device=gpu)
+    lib = _lib.load()
+    st = lib.mxgg_grouped_fwd_swiglu_quant_keep_h(
+        xq.data_ptr(), K, sa.data_ptr(), ldas, wq.data_ptr(), 2 * F * K, K, sw.data_ptr(), wsg,
+        ldws, offs.data_ptr(), E, M, F, K, h.data_ptr(), ldh, q.data_ptr(), ldq, s.data_ptr(),
+        s.stride(0), _lib.SCALES_BLOCK_MAJOR, _lib.SCALE_RCEIL,
+        torch.cuda.current_stream(gpu).cuda_stream)
+    assert st == 0, lib.mxgg_last_error()
+    torch.cuda.synchronize(gpu)
+    inside = int(np.sum(sizes))
+    h_ref = ops.grouped_mm(xq[:inside], wq, offs, xs[:inside], ws)
+    rq, rs = ops.swiglu_quant(h_ref)
+    assert torch.equal(h[:inside, :2 * F], h_ref.view(torch.int16))
+    assert torch.equal(q[:inside, :F], rq.view(torch.uint8))
+    assert torch.equal(s[:, :inside], rs.t())
+    assert bool((h[inside:] == 0x7FC1).all()) and bool((h[:, 2 * F:] == 0x7FC1).all())
+    assert bool((q[inside:] == 0xAB).all()) and bool((q[:, F:] == 0xAB).all())
+    assert bool((s[:, inside:M] == 0xCD).all())
 
 
 def test_fused_row_major_scales_through_the_c_abi(gpu):
@@ -99,9 +142,15 @@ def test_fused_c5_shape(gpu):
     print(f"C5 gate+up fused: {int(sizes.sum())} tokens", flush=True)
     xq, xs, wq, ws, offs = _operands(gpu, sizes, F, H, 0)
     q, s = ops.grouped_mm_swiglu_quant(xq, wq, offs, xs, ws)
-    rq, rs = ops.swiglu_quant(ops.grouped_mm(xq, wq, offs, xs, ws))
+    h = ops.grouped_mm(xq, wq, offs, xs, ws)
+    rq, rs = ops.swiglu_quant(h)
     assert torch.equal(q.view(torch.uint8), rq.view(torch.uint8))
     assert torch.equal(s, rs)
+    del q, s
+    qk, sk, hk = ops.grouped_mm_swiglu_quant(xq, wq, offs, xs, ws, return_h=True)
+    assert torch.equal(hk.view(torch.int16), h.view(torch.int16))
+    assert torch.equal(qk.view(torch.uint8), rq.view(torch.uint8))
+    assert torch.equal(sk, rs)
 
 
 def test_forward_only_layers_equal_the_training_forward(gpu):
