@@ -428,10 +428,11 @@ def hbm_ceiling(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
 
 def gate_up_swiglu_c5(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
     """C5's gate+up projection (131072 tokens, Zipf(1.0) over 32 experts,
-    hidden 7168, intermediate 2048) three ways: the grouped GEMM alone (bf16
-    h [M, 4096]), GEMM + the standalone SwiGLU cast (the training forward),
-    and the fused kernel that writes only the MXFP8 cast of SiLU(gate) * up
-    (the forward-only pass)."""
+    hidden 7168, intermediate 2048) four ways: the grouped GEMM alone (bf16
+    h [M, 4096]), GEMM + the standalone SwiGLU cast (the unfused sequence),
+    the fused kernel that writes only the MXFP8 cast of SiLU(gate) * up (the
+    forward-only pass), and the fused kernel that also writes bf16 h (the
+    training forward)."""
     from mxfp8gg import ops
     sizes = workloads.c5_sizes()
     M, H, F, E = int(sizes.sum()), 7168, 2048, 32
@@ -447,10 +448,14 @@ def gate_up_swiglu_c5(torch, mxfp8gg, workloads, dev, steps=10, warmup=3):
                          steps, warmup, torch)
     ms_f = time_launches(lambda: ops.grouped_mm_swiglu_quant(xq, wq, offs, xs, ws), steps, warmup,
                          torch)
+    del h
+    ms_k = time_launches(lambda: ops.grouped_mm_swiglu_quant(xq, wq, offs, xs, ws, return_h=True),
+                         steps, warmup, torch)
     return {"tokens": M, "gemm_bf16_h_ms": round(ms_g, 4),
             "gemm_bf16_h_tflops": round(fl / ms_g / 1e9, 1),
             "gemm_then_swiglu_cast_ms": round(ms_u, 4),
-            "fused_ms": round(ms_f, 4), "fused_tflops": round(fl / ms_f / 1e9, 1)}
+            "fused_ms": round(ms_f, 4), "fused_tflops": round(fl / ms_f / 1e9, 1),
+            "fused_keep_h_ms": round(ms_k, 4), "fused_keep_h_tflops": round(fl / ms_k / 1e9, 1)}
 
 
 def routing_c5(torch, mxfp8gg, workloads, dev, steps=5, warmup=2):

@@ -223,8 +223,9 @@ class MXFP8RoutedExpertFFN(torch.autograd.Function):
     between the top-k dispatch and combine of a MoE layer on one GPU.
 
     forward : route plan (device) -> both casts of the routed x read straight
-              from token order -> gate+up GEMM -> SwiGLU + cast -> down GEMM ->
-              combine (score-weighted, fp32 sum over k)
+              from token order -> gate+up GEMM writing h (bf16, kept) and the
+              cast of SwiGLU(h) from its epilogue -> down GEMM -> combine
+              (score-weighted, fp32 sum over k)
     backward: the routed dY = bf16(dOut[t] * score[s]) is never written: its two
               casts are gathered from dOut; then as MXFP8ExpertFFN; the routed
               dX is summed back over k; d scores = dOut . routed output.
@@ -238,8 +239,7 @@ class MXFP8RoutedExpertFFN(torch.autograd.Function):
         wcast = weight_cache.get if weight_cache is not None else ops.quant_weight_dual
         xq, xs, xqt, xst, _ = routing.gather_to_mxfp8_dual(x, plan, scaling_mode)
         (wq, ws), (wgt, wgts) = wcast(w_gate_up, scaling_mode)
-        h = ops.grouped_mm(xq, wq, plan.offs, xs, ws, out_dtype=torch.bfloat16)
-        aq, as_ = ops.swiglu_quant(h, scaling_mode)
+        aq, as_, h = _gate_up_act(xq, xs, wq, ws, plan.offs, scaling_mode, keep_h=True)
         (dq, ds), (wdt, wdts) = wcast(w_down, scaling_mode)
         y = ops.grouped_mm(aq, dq, plan.offs, as_, ds, out_dtype=torch.bfloat16)
         sc = scores.to(torch.float32).contiguous() if scores is not None else None
