@@ -170,8 +170,10 @@ def _gate_up_act(xq, xs, wq, ws, ends, scaling_mode, keep_h=False):
     """MXFP8 cast of SiLU(gate) * up of the gate+up projection (and, with
     keep_h, the bf16 projection h itself as a third result): one fused kernel
     when the intermediate size allows (F % 128 == 0, activations under 2 GiB),
-    else the GEMM's bf16 output through the standalone SwiGLU cast (the same
-    bits either way, on the rows inside the groups)."""
+    else the GEMM's bf16 output through the standalone SwiGLU cast.  On the
+    rows inside the groups the fused kernel gives the bits of the unsplit GEMM
+    followed by that cast; the training and forward-only passes of one shape
+    take the same branch."""
     F2 = wq.shape[1]
     if F2 % 256 == 0 and (xq.shape[0] == 0 or
                           (xq.shape[0] - 1) * xq.stride(0) + xq.shape[1] <= ops._MAX_OPERAND_BYTES):

@@ -702,12 +702,15 @@ def grouped_mm_swiglu_quant(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor
     a: e4m3 [M, K]; w: e4m3 [E, 2F, K] with gate rows first (the fused gate+up
     weight); scales and offs as for grouped_mm.  F % 128 == 0.  Returns
     (q float8_e4m3fn [M, F], scales uint8 [M, F/32] view of block-major
-    storage), equal to swiglu_quant(grouped_mm(a, w, ...)) on the rows inside
-    the groups (rows past the last group end are not written).  Without
-    return_h the bf16 [M, 2F] projection is never materialised (forward-only
-    passes); with it (the training forward, mxgg_grouped_fwd_swiglu_quant_keep_h)
-    the kernel also writes h = grouped_mm(a, w, ...) for the backward and
-    returns (q, scales, h); rows of h past the last group end are zero.  The
+    storage), equal to swiglu_quant(grouped_mm(a, w, ..., split_tail=False))
+    on the rows inside the groups (rows past the last group end are not
+    written; the fused kernel never splits K, so a launch that grouped_mm
+    would split can differ from its default in the fp32 summation order).
+    Without return_h the bf16 [M, 2F] projection is never materialised
+    (forward-only passes); with it (the training forward,
+    mxgg_grouped_fwd_swiglu_quant_keep_h) the kernel also writes
+    h = grouped_mm(a, w, ..., split_tail=False) for the backward and returns
+    (q, scales, h); rows of h past the last group end are zero.  The
     reference runs the gate and up GEMMs, eager SiLU * up and the fp8 cast
     separately (e2e_bench.py:56-61)."""
     _need_gpu(a, "a")

@@ -54,7 +54,7 @@ def test_fused_gate_up_equals_unfused(gpu, sizes, F, K, scaled, mode):
     if not scaled:
         xs = ws = None
     q, s = ops.grouped_mm_swiglu_quant(xq, wq, offs, xs, ws, mode)
-    h = ops.grouped_mm(xq, wq, offs, xs, ws)
+    h = ops.grouped_mm(xq, wq, offs, xs, ws, split_tail=False)  # the fused kernel never splits
     rq, rs = ops.swiglu_quant(h, mode)
     ins = _inside(sizes, gpu)
     assert q.shape == rq.shape and s.shape == rs.shape
@@ -92,7 +92,7 @@ def test_fused_keep_h_strides_and_rows_past_the_end(gpu):
     assert st == 0, lib.mxgg_last_error()
     torch.cuda.synchronize(gpu)
     inside = int(np.sum(sizes))
-    h_ref = ops.grouped_mm(xq[:inside], wq, offs, xs[:inside], ws)
+    h_ref = ops.grouped_mm(xq[:inside], wq, offs, xs[:inside], ws, split_tail=False)
     rq, rs = ops.swiglu_quant(h_ref)
     assert torch.equal(h[:inside, :2 * F], h_ref.view(torch.int16))
     assert torch.equal(q[:inside, :F], rq.view(torch.uint8))
@@ -142,7 +142,7 @@ def test_fused_c5_shape(gpu):
     print(f"C5 gate+up fused: {int(sizes.sum())} tokens", flush=True)
     xq, xs, wq, ws, offs = _operands(gpu, sizes, F, H, 0)
     q, s = ops.grouped_mm_swiglu_quant(xq, wq, offs, xs, ws)
-    h = ops.grouped_mm(xq, wq, offs, xs, ws)
+    h = ops.grouped_mm(xq, wq, offs, xs, ws, split_tail=False)
     rq, rs = ops.swiglu_quant(h)
     assert torch.equal(q.view(torch.uint8), rq.view(torch.uint8))
     assert torch.equal(s, rs)

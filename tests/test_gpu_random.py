@@ -4,6 +4,9 @@ names and reproduces its case), checked against the CPU oracle with the same
 bars as the fixed-case tests:
 
   * casts, routing plans, gathers and combines: bit for bit;
+  * the gate+up GEMM with SwiGLU and the cast in its epilogue (with and
+    without the bf16 projection kept): bit for bit against the grouped GEMM
+    followed by the standalone SwiGLU cast;
   * grouped GEMMs: tests/_helpers.assert_close_to_oracle (every element within
     2^-7 |ref| + 2^-12 max|ref| of the float64 dequantise-then-matmul value);
     split forwards also within 2^-14 max|y| (fp32) or 2^-7 max|y| (bf16) of
@@ -162,6 +165,41 @@ def test_random_dual_cast(gpu, sizes, C, mode_name, seed):
     rqt, rst, rpad = O.quant_dim1(bits(x), ends, qt.shape[1], mode)
     assert np.array_equal(u8(qt), rqt) and np.array_equal(u8(st), rst)
     assert np.array_equal(pad.cpu().numpy(), rpad)
+
+
+def _swiglu_cases(n=10, seed=350):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        E = int(rng.integers(1, 9))
+        M = int(rng.integers(1, 700))
+        out.append((_sizes(rng, E, M), 128 * int(rng.integers(1, 4)), 32 * int(rng.integers(1, 13)),
+                    bool(rng.integers(0, 2)), ["rceil", "floor"][int(rng.integers(0, 2))],
+                    int(rng.integers(0, 2**31))))
+    return out
+
+
+@pytest.mark.parametrize("sizes,F,K,scaled,mode,seed", _swiglu_cases())
+def test_random_fused_swiglu_forward(gpu, sizes, F, K, scaled, mode, seed):
+    E, M = len(sizes), sum(sizes)
+    a_q, a_s = _rand_q((max(M, 1), K), gpu, seed)
+    w_q, w_s = _rand_q((E, 2 * F, K), gpu, seed + 1)
+    a_q, a_s = a_q[:M], a_s[:M]
+    if not scaled:
+        a_s = w_s = None
+    offs = torch.from_numpy(workloads.ends_of(sizes)).to(gpu)
+    f8 = torch.float8_e4m3fn
+    args = (a_q.view(f8), w_q.view(f8), offs, a_s, w_s, mode)
+    # the fused kernel never splits K: its h is the unsplit GEMM's, bit for bit
+    h = ops.grouped_mm(*args[:5], split_tail=False)
+    rq, rs = ops.swiglu_quant(h, mode)
+    q, s = ops.grouped_mm_swiglu_quant(*args)
+    qk, sk, hk = ops.grouped_mm_swiglu_quant(*args, return_h=True)
+    assert torch.equal(q.view(torch.uint8), rq.view(torch.uint8))
+    assert torch.equal(s, rs)
+    assert torch.equal(qk.view(torch.uint8), rq.view(torch.uint8))
+    assert torch.equal(sk, rs)
+    assert torch.equal(hk.view(torch.int16), h.view(torch.int16))
 
 
 def _route_cases(n=12, seed=400):
