@@ -132,12 +132,6 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 // with swz(s) = (s/2) mod 8 the 16 quads are each hit exactly twice.
 __device__ __forceinline__ uint32_t swz(uint32_t s) { return (s >> 1) & 7u; }
 
-// Tile row held by LDS slot s: slots [128w + 32i, +32) hold rows 128w + 4m + i
-// (m = 0..31), the rows of MFMA block i of wave row-half w.
-__device__ __forceinline__ uint32_t slot_row(uint32_t s) {
-  return (s & 128u) | ((s & 31u) << 2) | ((s >> 5) & 3u);
-}
-
 // Wait for this wave's DMA except the youngest `N` instructions and for all
 // of its LDS reads, then the workgroup barrier.  Written as assembly so the
 // compiler's waitcnt pass can neither relax nor move it (it does not see the
@@ -185,7 +179,8 @@ __device__ __forceinline__ void dma_x1(const desc_t& d, uint32_t lds_addr, uint3
 //  Data: wave w's i-th load (i = 0..7) fills LDS bytes [4096i + 1024w, +1024)
 //  of an operand, lane l writing 16 B at +16l: slot s = 32i + 8w + l/8 at
 //  physical chunk l%8, so the lane fetches logical chunk (l%8) ^ swz(s) of
-//  tile row slot_row(s) = 128(i/4) + 4(8w + l/8) + i%4.  Eight lanes cover one
+//  tile row 128(i/4) + 4(8w + l/8) + i%4 (slots 128a + 32b + c hold rows
+//  128a + 4c + b).  Eight lanes cover one
 //  128-byte line.  swz(s) = (4w + l/16) mod 8 does not depend on i, and the
 //  row moves by a lane-independent amount from load to load, so the lane keeps
 //  one base offset per operand and adds a uniform step.  Chunks outside
@@ -265,45 +260,48 @@ struct Stream {
   }
 };
 
-// Operands of one MFMA k-step in registers: 4 P fragments, 4 Q fragments, and
-// the scale bytes of the lane's block for fragments 0..3 (byte i for
-// fragment i).
+// Operands of one stage in registers: 8 P fragments and 8 Q fragments of 16
+// rows x 128 contraction bytes, and the scale dwords of the lane's 32-block
+// for the P rows of fragment halves G = 0, 1 (sa[G]) and the Q rows of
+// halves H = 0, 1 (sb[H]).
 struct Frags {
-  v8i a[4], b[4];
-  uint32_t sa, sb;
+  v8i a[8], b[8];
+  uint32_t sa[2], sb[2];
 };
 
-// Per-lane LDS byte offsets (relative to a stage) of fragment 0 for k-step
-// t = 0, 1; fragment i adds 32 slots = 4096 bytes.
-//   v_mfma_scale_f32_32x32x64_f8f6f4 (fp8) operand layout: lane l serves row
-//   l%32; its bytes 0..15 belong to scale block 0 and bytes 16..31 to block 1
-//   of the 64-deep step, both halves of the wave sharing each block, and the
-//   block-b scale of row r comes from lane r + 32b.  So in k-step t lane half h
-//   takes chunk 4t+h (of block 2t: chunks 4t, 4t+1) and chunk 4t+2+h (of block
-//   2t+1), and the scales of block 2t+h: lane m of fragment i serves tile row
-//   128w + 4m + i, so its four scale bytes are the dword at 128w + 4m.
+// Per-lane LDS byte offsets (relative to a stage).
+//   v_mfma_scale_f32_16x16x128_f8f6f4 (fp8) operand layout: lane m + 16g
+//   serves row m of a fragment with contraction chunks g (bytes 0..15) and
+//   g + 4 (bytes 16..31) of the 128-deep stage, the scale of 32-block b of
+//   row m comes from lane m + 16b, and D[4g + r][c] sits in register r of
+//   lane c + 16g.  Fragment f = 4G + i of wave row-half w holds tile rows
+//   128w + 64G + 4m + i (m = 0..15): LDS slots 128w + 32i + 16G + m of the
+//   DMA's slot layout.  Its scale byte is byte i of the dword of rows
+//   128w + 64G + 4m .. +3 of the lane's block.
 struct FragAddr {
-  uint32_t plo[2], phi[2], qlo[2], qhi[2], ps, qs;
+  uint32_t plo, phi, qlo, qhi, ps, qs;
 
   __device__ __forceinline__ void init() {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t wp = wave & 1u, wq = wave >> 1;
-    const uint32_t l32 = lane & 31u, h = lane >> 5;
-    // swz(128w + 32i + m) = swz(m) for every w, i
-    const uint32_t sw = swz(l32);
-    const uint32_t rp = (wp * 128u + l32) * kStageK, rq = kOpBytes + (wq * 128u + l32) * kStageK;
-#pragma unroll
-    for (uint32_t t = 0; t < 2; ++t) {
-      plo[t] = rp + (((4u * t + h) ^ sw) << 4);
-      phi[t] = rp + (((4u * t + 2u + h) ^ sw) << 4);
-      qlo[t] = rq + (((4u * t + h) ^ sw) << 4);
-      qhi[t] = rq + (((4u * t + 2u + h) ^ sw) << 4);
-    }
-    ps = kScaleOff + h * 512u + wp * 128u + 4u * l32;
-    qs = kScaleOff + 256u + h * 512u + wq * 128u + 4u * l32;
+    const uint32_t m = lane & 15u, g = lane >> 4;
+    // swz(128w + 32i + 16G + m) = swz(m) for every w, i, G
+    const uint32_t sw = swz(m);
+    const uint32_t rp = (wp * 128u + m) * kStageK, rq = kOpBytes + (wq * 128u + m) * kStageK;
+    plo = rp + ((g ^ sw) << 4);
+    phi = rp + (((g + 4u) ^ sw) << 4);
+    qlo = rq + ((g ^ sw) << 4);
+    qhi = rq + (((g + 4u) ^ sw) << 4);
+    ps = kScaleOff + g * 512u + wp * 128u + 4u * m;
+    qs = kScaleOff + 256u + g * 512u + wq * 128u + 4u * m;
   }
 };
+
+// Byte offset of fragment f = 4G + i from fragment 0: 16G + 32i slots.
+constexpr uint32_t frag_off(int f) {
+  return 2048u * (uint32_t)(f >> 2) + 4096u * (uint32_t)(f & 3);
+}
 
 __device__ __forceinline__ v8i lds_v8i(const uint8_t* lo, const uint8_t* hi) {
   const uint4 a = *reinterpret_cast<const uint4*>(lo);
@@ -314,50 +312,32 @@ __device__ __forceinline__ v8i lds_v8i(const uint8_t* lo, const uint8_t* hi) {
   return f;
 }
 
-// Fragment reads of k-step T are split so they spread over the MFMA stream:
-//   head : Q fragments 0..3, P fragments 0..1 and the scales
-//   tail : P fragments 2..3
+template <int F>
+__device__ __forceinline__ void read_a(const uint8_t* stage, const FragAddr& fa, Frags& f) {
+  f.a[F] = lds_v8i(stage + fa.plo + frag_off(F), stage + fa.phi + frag_off(F));
+}
+template <int F>
+__device__ __forceinline__ void read_b(const uint8_t* stage, const FragAddr& fa, Frags& f) {
+  f.b[F] = lds_v8i(stage + fa.qlo + frag_off(F), stage + fa.qhi + frag_off(F));
+}
 // Unscaled kernels use scale byte 127 (2^0) in every position.
-template <int T>
-__device__ __forceinline__ void read_q(const uint8_t* stage, const FragAddr& fa, Frags& f, int j) {
-  f.b[j] = lds_v8i(stage + fa.qlo[T] + 4096u * j, stage + fa.qhi[T] + 4096u * j);
+template <bool SCALED, int G>
+__device__ __forceinline__ void read_sa(const uint8_t* stage, const FragAddr& fa, Frags& f) {
+  f.sa[G] = SCALED ? *reinterpret_cast<const uint32_t*>(stage + fa.ps + 64u * G) : 0x7F7F7F7Fu;
 }
-template <int T>
-__device__ __forceinline__ void read_p(const uint8_t* stage, const FragAddr& fa, Frags& f, int i) {
-  f.a[i] = lds_v8i(stage + fa.plo[T] + 4096u * i, stage + fa.phi[T] + 4096u * i);
-}
-template <bool SCALED, int T>
-__device__ __forceinline__ void read_scales(const uint8_t* stage, const FragAddr& fa, Frags& f) {
-  f.sa = SCALED ? *reinterpret_cast<const uint32_t*>(stage + fa.ps + 1024u * T) : 0x7F7F7F7Fu;
-  f.sb = SCALED ? *reinterpret_cast<const uint32_t*>(stage + fa.qs + 1024u * T) : 0x7F7F7F7Fu;
-}
-template <bool SCALED, int T>
-__device__ __forceinline__ void read_head(const uint8_t* stage, const FragAddr& fa, Frags& f) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) read_q<T>(stage, fa, f, j);
-  read_p<T>(stage, fa, f, 0);
-  read_p<T>(stage, fa, f, 1);
-  read_scales<SCALED, T>(stage, fa, f);
-}
-template <int T>
-__device__ __forceinline__ void read_tail(const uint8_t* stage, const FragAddr& fa, Frags& f) {
-  read_p<T>(stage, fa, f, 2);
-  read_p<T>(stage, fa, f, 3);
+template <bool SCALED, int H>
+__device__ __forceinline__ void read_sb(const uint8_t* stage, const FragAddr& fa, Frags& f) {
+  f.sb[H] = SCALED ? *reinterpret_cast<const uint32_t*>(stage + fa.qs + 64u * H) : 0x7F7F7F7Fu;
 }
 
-// One MFMA: P fragment I against Q fragment J; op_sel picks scale byte I of
-// the P dword and byte J of the Q dword.
-template <int I, int J>
-__device__ __forceinline__ void mfma1(const Frags& f, v16f (&acc)[4][4]) {
-  acc[I][J] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.a[I], f.b[J], acc[I][J], 0, 0, I,
-                                                              (int)f.sa, J, (int)f.sb);
-}
-template <int I>
-__device__ __forceinline__ void mfma_row(const Frags& f, v16f (&acc)[4][4]) {
-  mfma1<I, 0>(f, acc);
-  mfma1<I, 1>(f, acc);
-  mfma1<I, 2>(f, acc);
-  mfma1<I, 3>(f, acc);
+// One MFMA: P fragment PI against Q fragment QJ into accumulator 8 PI + QJ;
+// op_sel picks byte PI % 4 of the P scale dword of half PI / 4 and byte
+// QJ % 4 of the Q dword of half QJ / 4.
+template <int PI, int QJ>
+__device__ __forceinline__ void mma(const Frags& f, v4f (&acc)[64]) {
+  acc[8 * PI + QJ] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+      f.a[PI], f.b[QJ], acc[8 * PI + QJ], 0, 0, PI & 3, (int)f.sa[PI >> 2], QJ & 3,
+      (int)f.sb[QJ >> 2]);
 }
 
 // Bytes of the 4-byte word at contraction position c that lie in [klo, kend),
@@ -369,27 +349,26 @@ __device__ __forceinline__ uint32_t word_window(uint32_t c, uint32_t klo, uint32
   return bytes_below((int)kend - (int)c) & ~bytes_below((int)klo - (int)c);
 }
 
-// Zero every fragment byte of k-step T of the stage starting at k0 whose
-// contraction index lies outside [klo, kend), in both operands (a zero on one
-// side alone would still turn a NaN code on the other into NaN).  Lane half h
-// holds chunk 4T+h in dwords 0..3 and chunk 4T+2+h in dwords 4..7 (FragAddr).
-template <int T>
-__device__ __forceinline__ void mask_frags(Frags& f, uint32_t k0, uint32_t klo, uint32_t kend) {
-  const uint32_t h = (threadIdx.x & 63u) >> 5;
-  const uint32_t clo = k0 + 16u * (4u * T + h), chi = clo + 32u;
+// Byte masks of the lane's eight fragment dwords for the stage starting at
+// k0: dwords 0..3 hold contraction chunk g (bytes k0 + 16g ..), dwords 4..7
+// chunk g + 4.  Every fragment of the stage shares them.
+struct KMask {
   uint32_t m[8];
+};
+__device__ __forceinline__ void k_mask(KMask& km, uint32_t k0, uint32_t klo, uint32_t kend) {
+  const uint32_t g = (threadIdx.x & 63u) >> 4;
+  const uint32_t clo = k0 + 16u * g, chi = clo + 64u;
 #pragma unroll
   for (uint32_t d = 0; d < 4; ++d) {
-    m[d] = word_window(clo + 4u * d, klo, kend);
-    m[4 + d] = word_window(chi + 4u * d, klo, kend);
+    km.m[d] = word_window(clo + 4u * d, klo, kend);
+    km.m[4 + d] = word_window(chi + 4u * d, klo, kend);
   }
+}
+// Zero the bytes of a fragment outside [klo, kend) (in both operands: a zero on
+// one side alone would still turn a NaN code on the other into NaN).
+__device__ __forceinline__ void apply_mask(v8i& x, const KMask& km) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      f.a[i][d] &= (int)m[d];
-      f.b[i][d] &= (int)m[d];
-    }
+  for (int d = 0; d < 8; ++d) x[d] &= (int)km.m[d];
 }
 
 #define MXGG_FENCE() __builtin_amdgcn_sched_barrier(0)
@@ -404,41 +383,34 @@ __device__ __forceinline__ void release_barrier() {
 // at klo rounded down to 128 so that every stage reads whole cache lines of
 // rows whose stride is a multiple of 128; chunks below klo load as zeros.
 //
-// Stage s lives in slot s%2; f0 holds k-step 0 and f1 k-step 1 of a stage.
-// A DMA instruction holds up its wave's issue until the address unit takes
-// it, so the 18 loads of a stage are spread three on every four MFMAs.  Per
-// stage, with the MFMA count reached at each point:
-//    0  MFMA rows 0-1 of f0 while the rest of k-step 1 (Q fragments, P
-//       fragments 2-3, scales) is read into f1
-//    8  release barrier: every wave has read all of slot s%2 -> MFMA rows 2-3
-//       of f0, with the first 6 loads of stage s+2 into that slot
-//   16  publish barrier: everything older than those 6 loads, i.e. all of
-//       stage s+1, has landed -> MFMA rows 0-3 of f1 with the other 12 loads
-//       of stage s+2 (the two scale loads last), while stage s+1's k-step 0
-//       is read into f0 and its P fragments 0-1 of k-step 1 into f1 once the
-//       MFMAs that used those registers have issued
-// A stage's fragment reads thus spread over the 24 MFMAs from one publish to
-// the next release.  With the publish at MFMA 24 they had 16, and the LDS,
-// which also takes the DMA's writes, had no slack left in them.  Every load
-// has at least 18 MFMAs to land in.  The wait counts do not depend on whether
-// scales are loaded: the scale loads of a stage come after its data loads, and
-// the publish wait leaves exactly the 6 newest (data) loads in flight.
+// Stage s lives in slot s%2.  Its 64 MFMAs run P fragments 0..7 against Q
+// fragments 0..3 (MFMA n = 4p + q), then against Q fragments 4..7 (n = 32 +
+// 4p + q - 4).  Fragment registers are refilled as they free up, so one set of
+// 128 VGPRs holds two stages at once and every read has MFMAs to land in:
+//    0-14  the rest of stage s from slot s%2: P 4..7 (first used at 16..28),
+//          Q 4..7 and the Q scales of half 1 (first used at 32)
+//      20  release barrier: every wave has read all of slot s%2 -> the 18
+//          loads of stage s+2 into that slot, from here to MFMA 61
+//      32  publish barrier: everything older than the 6 loads issued since
+//          the release, i.e. all of stage s+1, has landed
+//   33-58  the first part of stage s+1 from the other slot: Q 0..3 (free since
+//          MFMA 31) and P 0..3, each after its last use in stage s (MFMA
+//          35 + 4p), and the scales of halves 0
+// A load has at least 35 MFMAs (half the cycles of 18 of the 32x32x64
+// schedule's MFMAs, times two) to land before its publish.  The wait counts do
+// not depend on whether scales are loaded: the scale loads of a stage come
+// after its data loads, and the publish wait leaves exactly the 6 newest
+// (data) loads in flight.
 // MASK (unscaled only): [klo, kend) may have any bounds; chunks that straddle
-// them are loaded whole and the bytes outside are zeroed in registers before
-// they reach an MFMA.  Only experts whose token range is not a multiple of 16
-// take this path.  It keeps the publish barrier at MFMA 24 (12 loads of
-// stage s+2 before it, the fragment reads of stage s+1 after it), under which
-// its masking registers do not spill.
+// them are loaded whole and the bytes outside are zeroed in registers right
+// after each fragment read.  Only experts whose token range is not a multiple
+// of 16 take this path.
 template <bool SCALED, bool MASK = false>
 __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Operand& Q,
-                                         uint32_t klo, uint32_t kend, v16f (&acc)[4][4]) {
+                                         uint32_t klo, uint32_t kend, v4f (&acc)[64]) {
   static_assert(!(SCALED && MASK), "a scale block cannot be split by a token mask");
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  for (int i = 0; i < 64; ++i) acc[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
   if (kend <= klo) return;
   const uint32_t kbeg = klo & ~(uint32_t)(kStageK - 1);
   const uint32_t nst = (kend - kbeg + kStageK - 1) / kStageK;
@@ -447,7 +419,8 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
   FragAddr fa;
   fa.init();
   // Prologue: all of stage 0 and the data of stage 1 (its scales follow in
-  // the first stage), then publish stage 0.
+  // the first stage), then publish stage 0 and read the part of it that the
+  // loop reads one stage ahead.
   st.template load_scale<0>(sm.ring[0], P, kbeg);
   st.template load_scale<1>(sm.ring[0], Q, kbeg);
   st.issue_data(sm.ring[0], P, Q, kbeg);
@@ -456,128 +429,109 @@ __device__ __forceinline__ void mainloop(Smem& sm, const Operand& P, const Opera
   st.template load_scale<1>(sm.ring[1], Q, kbeg + kStageK);
   wait_barrier<SCALED ? 18 : 16>();
   MXGG_FENCE();
-  Frags f0, f1;
-  read_head<SCALED, 0>(sm.ring[0], fa, f0);
-  read_tail<0>(sm.ring[0], fa, f0);
-  if constexpr (!MASK) {
-    read_p<1>(sm.ring[0], fa, f1, 0);
-    read_p<1>(sm.ring[0], fa, f1, 1);
+  Frags f;
+  KMask km;
+  if constexpr (MASK) k_mask(km, kbeg, klo, kend);
+#define MASKA(F) \
+  if constexpr (MASK) apply_mask(f.a[F], km)
+#define MASKB(F) \
+  if constexpr (MASK) apply_mask(f.b[F], km)
+  {
+    const uint8_t* r0 = sm.ring[0];
+    read_b<0>(r0, fa, f); MASKB(0);
+    read_b<1>(r0, fa, f); MASKB(1);
+    read_b<2>(r0, fa, f); MASKB(2);
+    read_b<3>(r0, fa, f); MASKB(3);
+    read_a<0>(r0, fa, f); MASKA(0);
+    read_a<1>(r0, fa, f); MASKA(1);
+    read_a<2>(r0, fa, f); MASKA(2);
+    read_a<3>(r0, fa, f); MASKA(3);
+    read_sa<SCALED, 0>(r0, fa, f);
+    read_sb<SCALED, 0>(r0, fa, f);
   }
   // Past the last stage the loads fetch zeros into a slot nobody reads again,
-  // and the final head read fetches a stale slot that is never used, so the
-  // loop body has no branches.  nst >= 1 here (kend > klo); written as a
-  // do-while because a loop that may run zero times made the compiler zero
-  // the 256 accumulators twice per tile, once for the zero-trip path.
+  // and the final reads fetch a stale slot that is never used, so the loop
+  // body has no branches.  nst >= 1 here (kend > klo); written as a do-while
+  // because a loop that may run zero times made the compiler zero the
+  // accumulators twice per tile, once for the zero-trip path.
   uint32_t s = 0;
   do {
     uint8_t* cur = sm.ring[s & 1u];
     uint8_t* nxt = sm.ring[(s & 1u) ^ 1u];
     uint32_t bp, bq;
     st.stage_base(kbeg + (s + 2) * kStageK, bp, bq);
-    if constexpr (MASK) {
-      mask_frags<0>(f0, kbeg + s * kStageK, klo, kend);
-      MXGG_FENCE();
-    }
-    if constexpr (MASK) {
-      // the masked loop keeps the publish barrier at MFMA 24 (the schedule
-      // below makes its extra masking registers spill)
-      // MFMA 0-7: rows 0-1 of f0 while k-step 1 of stage s is read into f1
-      mfma1<0, 0>(f0, acc); read_q<1>(cur, fa, f1, 0); MXGG_FENCE();
-      mfma1<0, 1>(f0, acc); read_q<1>(cur, fa, f1, 1); MXGG_FENCE();
-      mfma1<0, 2>(f0, acc); read_q<1>(cur, fa, f1, 2); MXGG_FENCE();
-      mfma1<0, 3>(f0, acc); read_q<1>(cur, fa, f1, 3); MXGG_FENCE();
-      mfma1<1, 0>(f0, acc); read_p<1>(cur, fa, f1, 0); MXGG_FENCE();
-      mfma1<1, 1>(f0, acc); read_p<1>(cur, fa, f1, 1); MXGG_FENCE();
-      mfma1<1, 2>(f0, acc); read_p<1>(cur, fa, f1, 2); MXGG_FENCE();
-      mfma1<1, 3>(f0, acc); read_p<1>(cur, fa, f1, 3); read_scales<SCALED, 1>(cur, fa, f1); MXGG_FENCE();
+      mma<0, 0>(f, acc); read_a<4>(cur, fa, f); MASKA(4); MXGG_FENCE();
+      mma<0, 1>(f, acc); read_sa<SCALED, 1>(cur, fa, f); MXGG_FENCE();
+      mma<0, 2>(f, acc); read_a<5>(cur, fa, f); MASKA(5); MXGG_FENCE();
+      mma<0, 3>(f, acc); read_b<4>(cur, fa, f); MASKB(4); MXGG_FENCE();
+      mma<1, 0>(f, acc); read_a<6>(cur, fa, f); MASKA(6); MXGG_FENCE();
+      mma<1, 1>(f, acc); read_b<5>(cur, fa, f); MASKB(5); MXGG_FENCE();
+      mma<1, 2>(f, acc); read_a<7>(cur, fa, f); MASKA(7); MXGG_FENCE();
+      mma<1, 3>(f, acc); read_b<6>(cur, fa, f); MASKB(6); MXGG_FENCE();
+      mma<2, 0>(f, acc); read_sb<SCALED, 1>(cur, fa, f); read_b<7>(cur, fa, f); MASKB(7); MXGG_FENCE();
+      mma<2, 1>(f, acc); MXGG_FENCE();
+      mma<2, 2>(f, acc); MXGG_FENCE();
+      mma<2, 3>(f, acc); MXGG_FENCE();
       release_barrier();
       MXGG_FENCE();
-      if constexpr (MASK) {
-        mask_frags<1>(f1, kbeg + s * kStageK, klo, kend);
-        MXGG_FENCE();
-      }
-      // MFMA 8-31: the 18 loads of stage s+2, three on every four MFMAs
-      mfma1<2, 0>(f0, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
-      mfma1<2, 1>(f0, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
-      mfma1<2, 2>(f0, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
-      mfma1<2, 3>(f0, acc); MXGG_FENCE();
-      mfma1<3, 0>(f0, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
-      mfma1<3, 1>(f0, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
-      mfma1<3, 2>(f0, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
-      mfma1<3, 3>(f0, acc); MXGG_FENCE();
-      mfma1<0, 0>(f1, acc); st.load_p(cur, P, bp, 6); MXGG_FENCE();
-      mfma1<0, 1>(f1, acc); st.load_p(cur, P, bp, 7); MXGG_FENCE();
-      mfma1<0, 2>(f1, acc); st.load_q(cur, Q, bq, 0); MXGG_FENCE();
-      mfma1<0, 3>(f1, acc); MXGG_FENCE();
-      mfma1<1, 0>(f1, acc); st.load_q(cur, Q, bq, 1); MXGG_FENCE();
-      mfma1<1, 1>(f1, acc); st.load_q(cur, Q, bq, 2); MXGG_FENCE();
-      mfma1<1, 2>(f1, acc); st.load_q(cur, Q, bq, 3); MXGG_FENCE();
-      mfma1<1, 3>(f1, acc); MXGG_FENCE();
-      // MFMA 24-31: stage s+1 published (all but the 12 loads above have
-      // landed); the remaining 6 loads of stage s+2 and the head of stage s+1's
-      // k-step 0 into f0
-      wait_barrier<12>();
+      mma<3, 0>(f, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
+      mma<3, 1>(f, acc); MXGG_FENCE();
+      mma<3, 2>(f, acc); MXGG_FENCE();
+      mma<3, 3>(f, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
+      mma<4, 0>(f, acc); MXGG_FENCE();
+      mma<4, 1>(f, acc); MXGG_FENCE();
+      mma<4, 2>(f, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
+      mma<4, 3>(f, acc); MXGG_FENCE();
+      mma<5, 0>(f, acc); MXGG_FENCE();
+      mma<5, 1>(f, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
+      mma<5, 2>(f, acc); MXGG_FENCE();
+      mma<5, 3>(f, acc); MXGG_FENCE();
+      mma<6, 0>(f, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
+      mma<6, 1>(f, acc); MXGG_FENCE();
+      mma<6, 2>(f, acc); MXGG_FENCE();
+      mma<6, 3>(f, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
+      mma<7, 0>(f, acc); MXGG_FENCE();
+      mma<7, 1>(f, acc); MXGG_FENCE();
+      mma<7, 2>(f, acc); st.load_p(cur, P, bp, 6); MXGG_FENCE();
+      mma<7, 3>(f, acc); MXGG_FENCE();
+      wait_barrier<7>();
       MXGG_FENCE();
-      const uint32_t k2 = kbeg + (s + 2) * kStageK;
-      mfma1<2, 0>(f1, acc); st.load_q(cur, Q, bq, 4); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
-      mfma1<2, 1>(f1, acc); st.load_q(cur, Q, bq, 5); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
-      mfma1<2, 2>(f1, acc); st.load_q(cur, Q, bq, 6); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
-      mfma1<2, 3>(f1, acc); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
-      mfma1<3, 0>(f1, acc); st.load_q(cur, Q, bq, 7); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
-      mfma1<3, 1>(f1, acc); st.template load_scale<0>(cur, P, k2); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
-      mfma1<3, 2>(f1, acc); st.template load_scale<1>(cur, Q, k2); read_p<0>(nxt, fa, f0, 2); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
-      mfma1<3, 3>(f1, acc); read_p<0>(nxt, fa, f0, 3); MXGG_FENCE();
-    } else {
-      // MFMA 0-7: rows 0-1 of f0 while the rest of k-step 1 of stage s (Q
-      // fragments, P fragments 2-3, scales) is read into f1
-      mfma1<0, 0>(f0, acc); read_q<1>(cur, fa, f1, 0); MXGG_FENCE();
-      mfma1<0, 1>(f0, acc); read_q<1>(cur, fa, f1, 1); MXGG_FENCE();
-      mfma1<0, 2>(f0, acc); read_q<1>(cur, fa, f1, 2); MXGG_FENCE();
-      mfma1<0, 3>(f0, acc); read_q<1>(cur, fa, f1, 3); MXGG_FENCE();
-      mfma1<1, 0>(f0, acc); read_p<1>(cur, fa, f1, 2); MXGG_FENCE();
-      mfma1<1, 1>(f0, acc); read_p<1>(cur, fa, f1, 3); MXGG_FENCE();
-      mfma1<1, 2>(f0, acc); read_scales<SCALED, 1>(cur, fa, f1); MXGG_FENCE();
-      mfma1<1, 3>(f0, acc); MXGG_FENCE();
-      release_barrier();
-      MXGG_FENCE();
-      if constexpr (MASK) {
-        mask_frags<1>(f1, kbeg + s * kStageK, klo, kend);
-        MXGG_FENCE();
-      }
-      // MFMA 8-15: rows 2-3 of f0; the first 6 loads of stage s+2
-      mfma1<2, 0>(f0, acc); st.load_p(cur, P, bp, 0); MXGG_FENCE();
-      mfma1<2, 1>(f0, acc); st.load_p(cur, P, bp, 1); MXGG_FENCE();
-      mfma1<2, 2>(f0, acc); st.load_p(cur, P, bp, 2); MXGG_FENCE();
-      mfma1<2, 3>(f0, acc); MXGG_FENCE();
-      mfma1<3, 0>(f0, acc); st.load_p(cur, P, bp, 3); MXGG_FENCE();
-      mfma1<3, 1>(f0, acc); st.load_p(cur, P, bp, 4); MXGG_FENCE();
-      mfma1<3, 2>(f0, acc); st.load_p(cur, P, bp, 5); MXGG_FENCE();
-      mfma1<3, 3>(f0, acc); MXGG_FENCE();
-      // MFMA 16-31: stage s+1 published (all but the 6 loads above have
-      // landed); rows 0-3 of f1 with the other 12 loads of stage s+2, all of
-      // stage s+1's k-step 0 read into f0 and its P fragments 0-1 of k-step 1
-      // into f1 once rows 0 and 1 of f1 are done
-      wait_barrier<6>();
-      MXGG_FENCE();
-      const uint32_t k2 = kbeg + (s + 2) * kStageK;
-      mfma1<0, 0>(f1, acc); st.load_p(cur, P, bp, 6); read_q<0>(nxt, fa, f0, 0); MXGG_FENCE();
-      mfma1<0, 1>(f1, acc); st.load_p(cur, P, bp, 7); read_q<0>(nxt, fa, f0, 1); MXGG_FENCE();
-      mfma1<0, 2>(f1, acc); st.load_q(cur, Q, bq, 0); read_q<0>(nxt, fa, f0, 2); MXGG_FENCE();
-      mfma1<0, 3>(f1, acc); read_q<0>(nxt, fa, f0, 3); MXGG_FENCE();
-      mfma1<1, 0>(f1, acc); st.load_q(cur, Q, bq, 1); read_p<0>(nxt, fa, f0, 0); MXGG_FENCE();
-      mfma1<1, 1>(f1, acc); st.load_q(cur, Q, bq, 2); read_p<0>(nxt, fa, f0, 1); MXGG_FENCE();
-      mfma1<1, 2>(f1, acc); st.load_q(cur, Q, bq, 3); read_p<0>(nxt, fa, f0, 2); MXGG_FENCE();
-      mfma1<1, 3>(f1, acc); read_p<0>(nxt, fa, f0, 3); read_scales<SCALED, 0>(nxt, fa, f0); MXGG_FENCE();
-      mfma1<2, 0>(f1, acc); st.load_q(cur, Q, bq, 4); read_p<1>(nxt, fa, f1, 0); MXGG_FENCE();
-      mfma1<2, 1>(f1, acc); st.load_q(cur, Q, bq, 5); read_p<1>(nxt, fa, f1, 1); MXGG_FENCE();
-      mfma1<2, 2>(f1, acc); st.load_q(cur, Q, bq, 6); MXGG_FENCE();
-      mfma1<2, 3>(f1, acc); MXGG_FENCE();
-      mfma1<3, 0>(f1, acc); st.load_q(cur, Q, bq, 7); MXGG_FENCE();
-      mfma1<3, 1>(f1, acc); st.template load_scale<0>(cur, P, k2); MXGG_FENCE();
-      mfma1<3, 2>(f1, acc); st.template load_scale<1>(cur, Q, k2); MXGG_FENCE();
-      mfma1<3, 3>(f1, acc); MXGG_FENCE();
-    }
+      if constexpr (MASK) k_mask(km, kbeg + (s + 1) * kStageK, klo, kend);
+      mma<0, 4>(f, acc); MXGG_FENCE();
+      mma<0, 5>(f, acc); read_b<0>(nxt, fa, f); MASKB(0); MXGG_FENCE();
+      mma<0, 6>(f, acc); st.load_p(cur, P, bp, 7); MXGG_FENCE();
+      mma<0, 7>(f, acc); MXGG_FENCE();
+      mma<1, 4>(f, acc); read_a<0>(nxt, fa, f); MASKA(0); MXGG_FENCE();
+      mma<1, 5>(f, acc); st.load_q(cur, Q, bq, 0); MXGG_FENCE();
+      mma<1, 6>(f, acc); MXGG_FENCE();
+      mma<1, 7>(f, acc); read_b<1>(nxt, fa, f); MASKB(1); MXGG_FENCE();
+      mma<2, 4>(f, acc); st.load_q(cur, Q, bq, 1); MXGG_FENCE();
+      mma<2, 5>(f, acc); read_a<1>(nxt, fa, f); MASKA(1); MXGG_FENCE();
+      mma<2, 6>(f, acc); MXGG_FENCE();
+      mma<2, 7>(f, acc); st.load_q(cur, Q, bq, 2); MXGG_FENCE();
+      mma<3, 4>(f, acc); MXGG_FENCE();
+      mma<3, 5>(f, acc); read_b<2>(nxt, fa, f); MASKB(2); st.load_q(cur, Q, bq, 3); MXGG_FENCE();
+      mma<3, 6>(f, acc); read_a<2>(nxt, fa, f); MASKA(2); MXGG_FENCE();
+      mma<3, 7>(f, acc); MXGG_FENCE();
+      mma<4, 4>(f, acc); st.load_q(cur, Q, bq, 4); MXGG_FENCE();
+      mma<4, 5>(f, acc); MXGG_FENCE();
+      mma<4, 6>(f, acc); read_a<3>(nxt, fa, f); MASKA(3); MXGG_FENCE();
+      mma<4, 7>(f, acc); st.load_q(cur, Q, bq, 5); MXGG_FENCE();
+      mma<5, 4>(f, acc); read_b<3>(nxt, fa, f); MASKB(3); MXGG_FENCE();
+      mma<5, 5>(f, acc); MXGG_FENCE();
+      mma<5, 6>(f, acc); st.load_q(cur, Q, bq, 6); MXGG_FENCE();
+      mma<5, 7>(f, acc); read_sb<SCALED, 0>(nxt, fa, f); MXGG_FENCE();
+      mma<6, 4>(f, acc); st.load_q(cur, Q, bq, 7); MXGG_FENCE();
+      mma<6, 5>(f, acc); MXGG_FENCE();
+      mma<6, 6>(f, acc); read_sa<SCALED, 0>(nxt, fa, f); MXGG_FENCE();
+      mma<6, 7>(f, acc); st.template load_scale<0>(cur, P, kbeg + (s + 2) * kStageK); MXGG_FENCE();
+      mma<7, 4>(f, acc); MXGG_FENCE();
+      mma<7, 5>(f, acc); MXGG_FENCE();
+      mma<7, 6>(f, acc); st.template load_scale<1>(cur, Q, kbeg + (s + 2) * kStageK); MXGG_FENCE();
+      mma<7, 7>(f, acc); MXGG_FENCE();
   } while (++s < nst);
+#undef MASKA
+#undef MASKB
   // Drain the loads past the end before the next tile's prologue reuses the slots.
   wait_barrier<0>();
 }
@@ -591,22 +545,22 @@ __device__ __forceinline__ uint32_t swap_lane_pair(uint32_t x) {
 }
 
 // Write the tile: output row = Q index in [qbeg, qend), column = P index < pend.
-// Accumulator register r of block (i, j) in lane (l32, h) is D[8(r/4) + 4h +
-// r%4][l32] of the 32x32 MFMA, i.e. P index 128wp + 4c + i with
-// c = 8(r/4) + 4h + r%4, and Q index 128wq + 4*l32 + j: the four blocks
-// i = 0..3 hold one 4-value chunk of consecutive P indices.
+// Register r of accumulator 8(4G + i) + 4H + j in lane c + 16g is D[4g + r][c]
+// of the 16x16 MFMA of P fragment 4G + i and Q fragment 4H + j, i.e. P index
+// 128wp + 64G + 16g + 4r + i and Q index 128wq + 64H + 4c + j: the four
+// fragments i = 0..3 hold one 4-value chunk of consecutive P indices.
 // Stored directly, every store instruction would scatter 64 small pieces over
-// 32 rows.  Instead each wave stages its 128x128 fp32 sub-tile in its own
+// 16 rows.  Instead each wave stages its 128x128 fp32 sub-tile in its own
 // 32 KB of the idle LDS ring, in two passes of 64 rows (j = 0,1 then j = 2,3;
-// staged row s = 2*l32 + j%2, 512 B), and then stores whole rows: 32 lanes x
-// 4 values, converted to bf16 after the read for bf16 output.  The 16-byte
+// staged row s = 2(16H + c) + j%2, 512 B), and then stores whole rows: 32
+// lanes x 4 values, converted to bf16 after the read for bf16 output.  The 16-byte
 // chunk k of staged row s sits at k ^ ((s/2) mod 16), so a half-wave writing
 // one chunk column of 32 rows, and one reading a whole row, touches each LDS
 // bank exactly twice.  The staging writes take the accumulators straight from
 // AGPRs.  The output is written once and not read again by the kernel, so the
 // row stores are nontemporal (measured faster, most for fp32 output).
 template <bool F32>
-__device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char* out,
+__device__ __forceinline__ void epilogue(Smem& sm, const v4f (&acc)[64], char* out,
                                          int64_t ldo_bytes, uint32_t q0, uint32_t qbeg,
                                          uint32_t qend, uint32_t p0, uint32_t pend,
                                          bool accumulate = false) {
@@ -614,6 +568,7 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
   const uint32_t wave = wave_id();
   const uint32_t wp = wave & 1u, wq = wave >> 1;
   const uint32_t l32 = lane & 31u, h = lane >> 5;
+  const uint32_t c16 = lane & 15u, g = lane >> 4;
   uint8_t* stage = &sm.ring[0][0] + wave * 32768u;
   const uint32_t p = p0 + wp * 128u + 4u * l32;  // this lane's 4 columns on the way out
   // fp32 stores of a wave whose 128 rows and 128 columns all lie inside the
@@ -631,17 +586,21 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-      const int j = 2 * pass + jj;
-      uint8_t* row = stage + (2u * l32 + (uint32_t)jj) * 512u;
-      const uint32_t sw = l32 & 15u;
+    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t c = 8u * (r >> 2) + 4u * h + (r & 3);
-        *reinterpret_cast<float4*>(row + ((c ^ sw) << 4)) =
-            make_float4(acc[0][j][r], acc[1][j][r], acc[2][j][r], acc[3][j][r]);
+      for (int jj = 0; jj < 2; ++jj) {
+        const int qj = 4 * hh + 2 * pass + jj;
+        uint8_t* row = stage + (2u * (16u * (uint32_t)hh + c16) + (uint32_t)jj) * 512u;
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t c = 16u * (uint32_t)gg + 4u * g + (uint32_t)r;
+            *reinterpret_cast<float4*>(row + ((c ^ c16) << 4)) =
+                make_float4(acc[8 * (4 * gg) + qj][r], acc[8 * (4 * gg + 1) + qj][r],
+                            acc[8 * (4 * gg + 2) + qj][r], acc[8 * (4 * gg + 3) + qj][r]);
+          }
       }
-    }
     // This wave's LDS writes complete before its reads (in-order LDS queue).
     // Reads go out eight at a time, unconditionally (they are always in
     // bounds), so their latency overlaps; only the global stores of a
@@ -738,30 +697,32 @@ __device__ __forceinline__ void epilogue(Smem& sm, const v16f (&acc)[4][4], char
 // index) x 512 B (P index 0..255), 16-byte chunk k of row q at chunk
 // k ^ ((q / 4) mod 16): a half-wave writing one chunk column of 32 rows, or
 // reading one whole row, touches every bank at most twice.
-__device__ __forceinline__ void stage_bf16_tile(Smem& sm, const v16f (&acc)[4][4]) {
+__device__ __forceinline__ void stage_bf16_tile(Smem& sm, const v4f (&acc)[64]) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
   const uint32_t wp = wave & 1u, wq = wave >> 1;
-  const uint32_t l32 = lane & 31u, h = lane >> 5;
+  const uint32_t c16 = lane & 15u, g = lane >> 4;
   uint8_t* st = &sm.ring[0][0];
 #pragma unroll
-  for (uint32_t j = 0; j < 4; ++j) {
-    const uint32_t q = 128u * wq + 4u * l32 + j;
-    const uint32_t sw = (q >> 2) & 15u;
+  for (uint32_t qj = 0; qj < 8; ++qj) {
+    // Q row 128wq + 64H + 4c + j of fragment qj = 4H + j; its swizzle
+    // ((row / 4) mod 16) is c
+    const uint32_t q = 128u * wq + 64u * (qj >> 2) + 4u * c16 + (qj & 3u);
     uint8_t* row = st + q * 512u;
 #pragma unroll
-    for (uint32_t a = 0; a < 4; ++a)
+    for (uint32_t gg = 0; gg < 2; ++gg)
 #pragma unroll
       for (uint32_t b = 0; b < 2; ++b) {
-        // registers r and r + 1 hold P columns 4c .. 4c+7 of the wave's half,
-        // c = 8a + 4h + 2b
-        const int r = (int)(4u * a + 2u * b);
-        const uint32_t chunk = 16u * wp + 4u * a + 2u * h + b;
-        *reinterpret_cast<uint4*>(row + ((chunk ^ sw) << 4)) =
-            make_uint4(pack_bf16x2(acc[0][j][r], acc[1][j][r]),
-                       pack_bf16x2(acc[2][j][r], acc[3][j][r]),
-                       pack_bf16x2(acc[0][j][r + 1], acc[1][j][r + 1]),
-                       pack_bf16x2(acc[2][j][r + 1], acc[3][j][r + 1]));
+        // registers 2b and 2b + 1 of P fragments 4gg .. 4gg+3 hold P columns
+        // 64gg + 16g + 8b .. +7 of the wave's half
+        const uint32_t r = 2u * b;
+        const uint32_t chunk = 16u * wp + 8u * gg + 2u * g + b;
+        const uint32_t a0 = 8u * (4u * gg) + qj;
+        *reinterpret_cast<uint4*>(row + ((chunk ^ c16) << 4)) =
+            make_uint4(pack_bf16x2(acc[a0][r], acc[a0 + 8u][r]),
+                       pack_bf16x2(acc[a0 + 16u][r], acc[a0 + 24u][r]),
+                       pack_bf16x2(acc[a0][r + 1u], acc[a0 + 8u][r + 1u]),
+                       pack_bf16x2(acc[a0 + 16u][r + 1u], acc[a0 + 24u][r + 1u]));
       }
   }
   __syncthreads();
@@ -770,7 +731,7 @@ __device__ __forceinline__ void stage_bf16_tile(Smem& sm, const v16f (&acc)[4][4
 // bf16 output through the bf16 staging: wave w stores rows 64w .. 64w+63 of
 // the tile, two whole 512-byte rows per store instruction (lanes 0-31 one
 // row, 32-63 the next).
-__device__ __forceinline__ void epilogue_bf16(Smem& sm, const v16f (&acc)[4][4], char* out,
+__device__ __forceinline__ void epilogue_bf16(Smem& sm, const v4f (&acc)[64], char* out,
                                               int64_t ldo_bytes, uint32_t q0, uint32_t qbeg,
                                               uint32_t qend, uint32_t p0, uint32_t pend) {
   stage_bf16_tile(sm, acc);
@@ -829,7 +790,7 @@ __device__ __forceinline__ void epilogue_bf16(Smem& sm, const v16f (&acc)[4][4],
 // h[tok][F + pg + c] (ldh elements per row), for a backward that re-reads h:
 // the same bits epilogue_bf16 writes for the unfused projection.
 template <int MODE, bool KEEP>
-__device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v16f (&acc)[4][4], uint8_t* aq,
+__device__ __forceinline__ void epilogue_swiglu(Smem& sm, const v4f (&acc)[64], uint8_t* aq,
                                                 int64_t ldq, uint8_t* sc, int64_t s_row,
                                                 int64_t s_blk, uint32_t q0, uint32_t qbeg,
                                                 uint32_t qend, uint32_t pg, uint16_t* h,
@@ -1051,7 +1012,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_fwd(FwdArgs args, uint3
       Q.scale = make_desc(args.as, scale_extent(K / 32, args.ldas, M));
       Q.lds = (uint32_t)args.ldas;
     }
-    v16f acc[4][4];
+    v4f acc[64];
     if (part) {
       const uint32_t klo = split * chunk * kStageK;
       mainloop<SCALED>(sm, P, Q, klo, min(K, klo + chunk * kStageK), acc);
@@ -1246,36 +1207,44 @@ __global__ __launch_bounds__(kThreads, 1) void k_grouped_wgrad(WgradArgs args, u
       Q.scale = make_desc(args.gos, scale_extent(M / 32, args.ldgos, args.N));
       Q.lds = (uint32_t)args.ldgos;
     }
-    v16f acc[4][4];
+    // The dW tile: a partial of a split expert into the workspace, or the
+    // expert's slice of dW.
+    auto finish = [&](const v4f (&acc)[64]) {
+      if (staged && sm.chunks[rank] > 1) {
+        // one of several partials of this tile: the whole fp32 256x256 block
+        char* slot = reinterpret_cast<char*>(args.split_ws) + kWgHdrBytes +
+                     (int64_t)lid * kPartialBytes;
+        epilogue<true>(sm, acc, slot, 1024, 0u, 0u, 256u, 0u, 256u);
+        return;
+      }
+      char* out = reinterpret_cast<char*>(args.dw) + (int64_t)g * args.ldw_e * (F32 ? 4 : 2);
+      if constexpr (F32)
+        epilogue<true>(sm, acc, out, args.ldw_n * 4, q0, 0u, (uint32_t)args.N, p0,
+                       (uint32_t)args.K, split > 0 && !staged);
+      else
+        epilogue_bf16(sm, acc, out, args.ldw_n * 2, q0, 0u, (uint32_t)args.N, p0,
+                      (uint32_t)args.K);
+    };
+    // Each path keeps its own accumulators: shared ones made the register
+    // allocator copy accumulators inside the unmasked loop of the unscaled
+    // kernel.
     if (SCALED && ((tb | te) & 31) != 0) {
       // A group boundary inside a 32-token block breaks the block/scale
       // pairing: the whole expert is written as NaN rather than a wrong value.
+      v4f acc[64];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_nanf("");
+      for (int i = 0; i < 64; ++i) acc[i] = v4f{1.0f, 1.0f, 1.0f, 1.0f} * __builtin_nanf("");
+      finish(acc);
     } else if (!SCALED && ((cb | ce) & 15) != 0) {
       // unscaled, token range off the 16-byte load grid: masked to the token
+      v4f acc[64];
       mainloop<false, true>(sm, P, Q, (uint32_t)cb, (uint32_t)ce, acc);
+      finish(acc);
     } else {
+      v4f acc[64];
       mainloop<SCALED>(sm, P, Q, (uint32_t)cb, (uint32_t)ce, acc);
+      finish(acc);
     }
-    if (staged && sm.chunks[rank] > 1) {
-      // one of several partials of this tile: the whole fp32 256x256 block
-      char* slot = reinterpret_cast<char*>(args.split_ws) + kWgHdrBytes +
-                   (int64_t)lid * kPartialBytes;
-      epilogue<true>(sm, acc, slot, 1024, 0u, 0u, 256u, 0u, 256u);
-      continue;
-    }
-    char* out = reinterpret_cast<char*>(args.dw) + (int64_t)g * args.ldw_e * (F32 ? 4 : 2);
-    if constexpr (F32)
-      epilogue<true>(sm, acc, out, args.ldw_n * 4, q0, 0u, (uint32_t)args.N, p0,
-                     (uint32_t)args.K, split > 0 && !staged);
-    else
-      epilogue_bf16(sm, acc, out, args.ldw_n * 2, q0, 0u, (uint32_t)args.N, p0,
-                    (uint32_t)args.K);
   }
 }
 
