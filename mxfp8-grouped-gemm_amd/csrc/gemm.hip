@@ -46,7 +46,11 @@ constexpr int kStageK = 128;    // contraction elements (bytes) per stage
 constexpr int kThreads = 256;
 constexpr uint32_t kOpBytes = 256u * kStageK;          // one operand of one stage: 32 KB
 constexpr uint32_t kScaleOff = 2u * kOpBytes;          // scale rows after P and Q data
-constexpr uint32_t kStageBytes = kScaleOff + 4u * 512u;  // + [4 blocks][P, Q][256]
+// Scale block b of a stage at kScaleOff + b * kScaleBlk: [P, Q][256] bytes and
+// 64 bytes of padding, so that the lanes of blocks 0 and 1 (one half-wave of
+// a scale read) fall on different banks.
+constexpr uint32_t kScaleBlk = 576;
+constexpr uint32_t kStageBytes = kScaleOff + 4u * kScaleBlk;
 constexpr uint32_t kOobOffset = 0x80000000u;           // beyond every num_records we create
 // Split-K of the forward's last round: at most this many K-ranges per tile;
 // workspace = a header (tail tile count, split count, then q0, p0, group
@@ -244,7 +248,7 @@ struct Stream {
     const bool ok = blk >= (klo >> 5) && blk < (kend >> 5);
     // the block's row offset is wave-uniform: it rides in the scalar offset,
     // and an out-of-range block moves the whole load past num_records
-    dma_x1(X.scale, lds_offset(stage) + kScaleOff + 512u * wave + 256u * OP, OP ? sq : sp,
+    dma_x1(X.scale, lds_offset(stage) + kScaleOff + kScaleBlk * wave + 256u * OP, OP ? sq : sp,
            ok ? blk * X.lds : kOobOffset);
   }
 
@@ -293,8 +297,8 @@ struct FragAddr {
     phi = rp + (((g + 4u) ^ sw) << 4);
     qlo = rq + ((g ^ sw) << 4);
     qhi = rq + (((g + 4u) ^ sw) << 4);
-    ps = kScaleOff + g * 512u + wp * 128u + 4u * m;
-    qs = kScaleOff + 256u + g * 512u + wq * 128u + 4u * m;
+    ps = kScaleOff + g * kScaleBlk + wp * 128u + 4u * m;
+    qs = kScaleOff + 256u + g * kScaleBlk + wq * 128u + 4u * m;
   }
 };
 
