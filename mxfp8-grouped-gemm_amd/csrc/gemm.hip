@@ -391,20 +391,22 @@ __device__ __forceinline__ void release_barrier() {
 // fragments 0..3 (MFMA n = 4p + q), then against Q fragments 4..7 (n = 32 +
 // 4p + q - 4).  Fragment registers are refilled as they free up, so one set of
 // 128 VGPRs holds two stages at once and every read has MFMAs to land in:
-//    0-14  the rest of stage s from slot s%2: P 4..7 (first used at 16..28),
-//          Q 4..7 and the Q scales of half 1 (first used at 32)
-//      20  release barrier: every wave has read all of slot s%2 -> the 18
-//          loads of stage s+2 into that slot, from here to MFMA 61
-//      32  publish barrier: everything older than the 6 loads issued since
+//     0-8  the rest of stage s from slot s%2: P 4..7 (first used at 16..28),
+//          the P scales of half 1 (first used at 16), Q 4..7 and the Q
+//          scales of half 1 (first used at 32)
+//      12  release barrier: every wave has read all of slot s%2 -> the 18
+//          loads of stage s+2 into that slot, one per about three MFMAs up to
+//          MFMA 62
+//      32  publish barrier: everything older than the 7 loads issued since
 //          the release, i.e. all of stage s+1, has landed
 //   33-58  the first part of stage s+1 from the other slot: Q 0..3 (free since
 //          MFMA 31) and P 0..3, each after its last use in stage s (MFMA
 //          35 + 4p), and the scales of halves 0
-// A load has at least 35 MFMAs (half the cycles of 18 of the 32x32x64
-// schedule's MFMAs, times two) to land before its publish.  The wait counts do
-// not depend on whether scales are loaded: the scale loads of a stage come
-// after its data loads, and the publish wait leaves exactly the 6 newest
-// (data) loads in flight.
+// A load has at least 34 MFMAs (about 1100 cycles) to land before its
+// publish.  Releasing later (MFMA 16 to 24) or placing the loads and reads on
+// MFMA pairs measured slower.  The wait counts do not depend on whether
+// scales are loaded: the scale loads of a stage come after its data loads,
+// and the publish wait leaves exactly the 7 newest (data) loads in flight.
 // MASK (unscaled only): [klo, kend) may have any bounds; chunks that straddle
 // them are loaded whole and the bytes outside are zeroed in registers right
 // after each fragment read.  Only experts whose token range is not a multiple
