@@ -31,6 +31,33 @@ def test_header_lists_the_bound_functions():
     assert declared_functions() == sorted(_lib.SIGNATURES)
 
 
+def _ctype_of(decl: str):
+    """ctypes type of one C parameter or return type of the header (every
+    scalar there is int or int64_t, every pointer T*)."""
+    decl = decl.strip()
+    if decl == "const char*":
+        return ctypes.c_char_p
+    if "*" in decl:
+        return ctypes.c_void_p
+    kind = decl.split()[0]
+    return {"int64_t": ctypes.c_int64, "int": ctypes.c_int}[kind]
+
+
+def test_bound_signatures_match_the_header():
+    """Every argument of every binding has the width and kind the header
+    declares, so no call passes a 32-bit value where the library reads 64."""
+    text = re.sub(r"/\*.*?\*/|//[^\n]*", "", HEADER.read_text(), flags=re.S)
+    decls = re.findall(r"([A-Za-z_][\w ]*\*?)\s*\b(mxgg_\w+)\s*\(([^)]*)\)\s*;", text)
+    assert sorted(name for _, name, _ in decls) == sorted(_lib.SIGNATURES)
+    for ret, name, params in decls:
+        params = " ".join(params.split())
+        want = [] if params in ("", "void") else [_ctype_of(p.rsplit(" ", 1)[0])
+                                                  for p in params.split(",")]
+        res, args = _lib.SIGNATURES[name]
+        assert res is _ctype_of(ret.replace(" *", "*")), name
+        assert list(args) == want, name
+
+
 def test_library_exports_every_declared_symbol(lib):
     for name in declared_functions():
         assert hasattr(lib, name), name
