@@ -58,6 +58,46 @@ def test_bound_signatures_match_the_header():
         assert list(args) == want, name
 
 
+def test_integration_stubs_match_the_bindings():
+    """The ctypes stubs a maintainer would copy from INTEGRATION.md declare the
+    argument and return types mxfp8gg binds, and assert the header's ABI
+    version."""
+    import ast
+    text = (ROOT / "INTEGRATION.md").read_text()
+    blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
+    ns = {"ctypes": ctypes, "P": ctypes.c_void_p, "I64": ctypes.c_int64, "I": ctypes.c_int}
+
+    class Fn:
+        argtypes = None
+        restype = None
+
+    fns = {}
+
+    class Lib:
+        def __getattr__(self, name):
+            return fns.setdefault(name, Fn())
+
+    ns["_lib"] = Lib()
+    version = int(re.search(r"#define MXGG_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    checked = asserted = 0
+    for block in blocks:
+        for node in ast.walk(ast.parse(block)):
+            if isinstance(node, ast.Assign) and isinstance(node.targets[0], ast.Attribute):
+                tgt = node.targets[0]
+                if (tgt.attr in ("argtypes", "restype") and isinstance(tgt.value, ast.Attribute)
+                        and isinstance(tgt.value.value, ast.Name) and tgt.value.value.id == "_lib"):
+                    name = tgt.value.attr
+                    value = eval(compile(ast.Expression(node.value), "stub", "eval"), ns)
+                    setattr(fns.setdefault(name, Fn()), tgt.attr, value)
+                    res, args = _lib.SIGNATURES[name]
+                    assert value == (list(args) if tgt.attr == "argtypes" else res), name
+                    checked += 1
+            if isinstance(node, ast.Assert) and "mxgg_abi_version" in ast.unparse(node):
+                assert node.test.comparators[0].value == version
+                asserted += 1
+    assert checked >= 6 and asserted == 1
+
+
 def test_library_exports_every_declared_symbol(lib):
     for name in declared_functions():
         assert hasattr(lib, name), name
