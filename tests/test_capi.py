@@ -59,9 +59,9 @@ def test_bound_signatures_match_the_header():
 
 
 def test_integration_stubs_match_the_bindings():
-    """The ctypes stubs a maintainer would copy from INTEGRATION.md declare the
-    argument and return types mxfp8gg binds, and assert the header's ABI
-    version."""
+    """The ctypes stubs of the integration guide at the repository root (what a
+    maintainer would copy into the reference's code) declare the argument and
+    return types mxfp8gg binds, and assert the header's ABI version."""
     import ast
     text = (ROOT / "INTEGRATION.md").read_text()
     blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
