@@ -245,6 +245,26 @@ def test_output_inside_a_wider_buffer(gpu, out_dtype, col0, pad):
     assert torch.isnan(big[:, :col0]).all() and torch.isnan(big[:, col0 + N:]).all()
 
 
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("N", [4, 20, 100, 276])
+def test_forward_column_count_off_the_8_grid(gpu, N, out_dtype, split):
+    """N = 4 mod 8 (one or two column tiles): bf16 output rows start off
+    16-byte alignment and the last column tile ends inside a 16-byte chunk,
+    so those columns leave through the per-element stores, from the GEMM's
+    epilogue or from the split-K reduce."""
+    sizes = [40, 0, 300, 13]
+    M, K = sum(sizes), 512                  # 4 stages: the split entry cuts them
+    a_q, a_s = _rand_q((M, K), gpu, 61)
+    w_q, w_s = _rand_q((len(sizes), N, K), gpu, 62)
+    ends = workloads.ends_of(sizes)
+    y = ops.grouped_mm(a_q.view(torch.float8_e4m3fn), w_q.view(torch.float8_e4m3fn),
+                       torch.from_numpy(ends).to(gpu), a_s, w_s, out_dtype=out_dtype,
+                       split_tail=split)
+    ref = O.grouped_fwd(u8(a_q), u8(a_s), u8(w_q), u8(w_s), ends)
+    assert_close_to_oracle(y, ref)
+
+
 def test_scale_bump_doubles_output_exactly(gpu):
     x, w, sizes = workloads.c1(gpu)
     xq, xs = mxfp8gg.to_mxfp8_dim0(x)
@@ -478,6 +498,29 @@ def test_wgrad_c4_sampled(gpu):
     # linearity in the scales: one more on every dY scale doubles dW exactly
     dw2 = ops.grouped_wgrad(go, ia, pad, gos + 1, ias, out_dtype=torch.float32)
     assert torch.equal(dw2, 2 * dw)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("split", [0, 128])
+@pytest.mark.parametrize("N,K", [(36, 20), (260, 276)])
+def test_wgrad_feature_counts_off_the_8_grid(gpu, N, K, out_dtype, split):
+    """dW rows of K = 4 mod 8 elements (bf16 rows off 16-byte alignment, a
+    last column tile ending inside a 16-byte chunk) and N = 4 mod 8 rows,
+    unsplit and split along tokens (the staged partials' reduce writes them)."""
+    sizes = [64, 0, 160, 32]
+    M = sum(sizes)
+    go_q, go_s = _rand_q((N, M), gpu, 71)
+    ia_q, ia_s = _rand_q((K, M), gpu, 72)
+    ends = workloads.ends_of(sizes)
+    dw = ops.grouped_wgrad(go_q.view(torch.float8_e4m3fn), ia_q.view(torch.float8_e4m3fn),
+                           torch.from_numpy(ends).to(gpu), go_s, ia_s, out_dtype=out_dtype,
+                           split_tokens=split)
+    ref = O.grouped_wgrad(u8(go_q), u8(go_s), u8(ia_q), u8(ia_s), ends)
+    for g, s in enumerate(sizes):
+        if s == 0:
+            assert torch.all(dw[g] == 0)
+        else:
+            assert_close_to_oracle(dw[g], ref[g])
 
 
 @pytest.mark.parametrize("sizes,split", [([1024, 0, 2976, 96], 256), ([4096, 4096], 1024),
