@@ -252,7 +252,9 @@ int mxgg_zero_rows_past_groups(void* out, int64_t rows, int64_t row_bytes, int64
  *   of nblk block-rows holding `rows` rows must be readable for
  *   (nblk-1)*ld + round_up(rows, 4) bytes from its base (per expert for w).
  *   group_ends : int32 [num_groups] (device) or NULL for one group of M rows
- *   out      : [M, N] bf16 or f32 (out_dtype), row stride ldo
+ *   out      : [M, N] bf16 or f32 (out_dtype), row stride ldo; base aligned
+ *              to 4 elements and ldo a multiple of 4 (any N: columns past the
+ *              last whole 4-element group are stored one by one)
  * a_scales and w_scales are both given or both NULL (NULL = every scale 1.0,
  * E8M0 byte 0x7F).  K % 32 == 0.  Rows past the last group end are untouched.
  * a and w are 16-byte aligned, lda and ldw multiples of 16 and at most 2^23,
@@ -376,7 +378,9 @@ int mxgg_grouped_fwd_split_noalloc(const void* a, int64_t lda, const void* a_sca
  *                 written as NaN.  Without scales the bounds may be any token
  *                 index (ranges off the 16-token load grid are masked token by
  *                 token, at some speed cost for those experts only).
- *   dw          : [num_groups, N, K] bf16 or f32, contiguous; empty groups are
+ *   dw          : [num_groups, N, K] bf16 or f32, contiguous, aligned to 4
+ *                 elements, K a multiple of 4 (other K: mxgg_grouped_wgrad_strided
+ *                 with a row stride rounded up to 4); empty groups are
  *                 written with zeros
  * go_t and ia_t are 16-byte aligned, ldgo and ldia multiples of 16 and at most
  * 2^23, each operand spans less than 2 GiB; strides that are multiples of 128

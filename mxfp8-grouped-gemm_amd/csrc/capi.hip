@@ -704,8 +704,11 @@ static int grouped_wgrad(const void* go_t, int64_t ldgo, const void* go_scales_t
     return set_error(MXGG_ERR_ALIGNMENT,
                      "grouped_wgrad: operands must be 16-byte aligned with ld % 16 == 0");
   const int esz = out_dtype == MXGG_OUT_F32 ? 4 : 2;
-  if ((reinterpret_cast<uintptr_t>(dw) % (esz * 4)) != 0 || K % 4 != 0)
-    return set_error(MXGG_ERR_ALIGNMENT, "grouped_wgrad: dw must be vector aligned, K % 4 == 0");
+  // Rows of any K: the epilogues store whole 4-element vectors only inside a
+  // row and the rest element by element, so only the base and the strides
+  // (checked below) need vector alignment.
+  if ((reinterpret_cast<uintptr_t>(dw) % (esz * 4)) != 0)
+    return set_error(MXGG_ERR_ALIGNMENT, "grouped_wgrad: dw must be aligned to 4 elements");
   if (ldw_n < K || ldw_e < 0 || (num_groups > 1 && ldw_e < (N - 1) * ldw_n + K))
     return set_error(MXGG_ERR_SHAPE,
                      "grouped_wgrad: dW strides (expert %lld, row %lld) overlap an [N=%lld, "

@@ -656,7 +656,13 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
         ends = _group_ends(offs, E, a.device)
     elif E != 1:
         raise ValueError("offs is required when w holds more than one expert")
-    if out is None:
+    padded = out is None and N % 4 != 0
+    if padded:
+        # the library writes rows at a stride of whole 4-element groups: a
+        # column count off that grid runs into a wider buffer and is returned
+        # as a contiguous copy
+        out = torch.empty((M, (N + 3) // 4 * 4), dtype=out_dtype, device=a.device)[:, :N]
+    elif out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=a.device)
     elif out.shape != (M, N) or out.dtype != out_dtype or out.stride(-1) != 1:
         raise ValueError("out must be a row-major [M, N] tensor of out_dtype")
@@ -689,7 +695,7 @@ def grouped_mm(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
                        "grouped_fwd_split")
         else:
             _lib.check(lib.mxgg_grouped_fwd(*args, stream), "grouped_fwd")
-    return out
+    return out.contiguous() if padded else out
 
 
 def grouped_mm_swiglu_quant(a: torch.Tensor, w: torch.Tensor, offs: torch.Tensor | None,
@@ -866,18 +872,24 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
         si, ldis = _scales_2d(ia_scales, K, M // 32, "ia_scales")
     E = offs.numel()
     ends = _group_ends(offs, E, go.device)
-    if out is None:
+    padded = out is None and K % 4 != 0
+    if padded:
+        # dW rows at a stride of whole 4-element groups (the strided entry),
+        # returned as a contiguous copy
+        out = torch.empty((E, N, (K + 3) // 4 * 4), dtype=out_dtype, device=go.device)[:, :, :K]
+    elif out is None:
         out = torch.empty((E, N, K), dtype=out_dtype, device=go.device)
     elif out.shape != (E, N, K) or out.dtype != out_dtype or not out.is_contiguous():
         raise ValueError("out must be a contiguous [E, N, K] tensor of out_dtype")
     lib = _lib.load()
     nc = _feature_rows_per_launch(g8.stride(0), N, M)
     kc = _feature_rows_per_launch(i8.stride(0), K, M)
-    if nc < N or kc < K:
+    if nc < N or kc < K or padded:
         # An operand past the 32-bit buffer range: launches over chunks of its
         # feature rows (256-row multiples), each contracting every token and
         # writing its own slice of dW (mxgg_grouped_wgrad_strided), so the
-        # result is the one-launch result.
+        # result is the one-launch result.  A padded dW goes the same way
+        # (one chunk each way) for its row stride.
         esz = out.element_size()
         for n0 in range(0, N, nc):
             for k0 in range(0, K, kc):
@@ -896,10 +908,11 @@ def grouped_wgrad(go: torch.Tensor, ia: torch.Tensor, offs: torch.Tensor,
                     i8.data_ptr() + k0 * i8.stride(0), i8.stride(0),
                     si.data_ptr() + k0 if si is not None else None, ldis,
                     ends.data_ptr(), E, M, n, k,
-                    out.data_ptr() + (n0 * K + k0) * esz, N * K, K, _out_code(out_dtype), st,
+                    out.data_ptr() + (n0 * out.stride(1) + k0) * esz, out.stride(0),
+                    out.stride(1), _out_code(out_dtype), st,
                     ws.data_ptr() if ws is not None else None, nbytes, _stream_ptr(go)),
                     "grouped_wgrad_strided")
-        return out
+        return out.contiguous() if padded else out
     if split_tokens is None:
         split_tokens = wgrad_split_tokens(M, N, K, E, _cu_count(go.device))
     args = (g8.data_ptr(), g8.stride(0),

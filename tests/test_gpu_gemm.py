@@ -265,6 +265,31 @@ def test_forward_column_count_off_the_8_grid(gpu, N, out_dtype, split):
     assert_close_to_oracle(y, ref)
 
 
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("N", [1, 6, 17, 259])
+def test_forward_any_column_count(gpu, N, out_dtype, split):
+    """Column counts off the 4-element grid (the reference masks any N,
+    fused_fwd.py:163-164): the output runs at a padded row stride and comes
+    back contiguous, equal to the oracle, through grouped_mm and the drop-in
+    fused_grouped_fwd."""
+    sizes = [40, 0, 300, 13]
+    M, K = sum(sizes), 256
+    a_q, a_s = _rand_q((M, K), gpu, 63)
+    w_q, w_s = _rand_q((len(sizes), N, K), gpu, 64)
+    ends = workloads.ends_of(sizes)
+    args = (a_q.view(torch.float8_e4m3fn), w_q.view(torch.float8_e4m3fn),
+            torch.from_numpy(ends).to(gpu), a_s, w_s)
+    y = ops.grouped_mm(*args, out_dtype=out_dtype, split_tail=split)
+    assert y.shape == (M, N) and y.is_contiguous()
+    ref = O.grouped_fwd(u8(a_q), u8(a_s), u8(w_q), u8(w_s), ends)
+    assert_close_to_oracle(y, ref)
+    if out_dtype == torch.bfloat16 and not split:
+        y2 = fused_fwd.fused_grouped_fwd(*args)
+        assert y2.shape == (M, N) and y2.is_contiguous()
+        assert_close_to_oracle(y2, ref)
+
+
 def test_scale_bump_doubles_output_exactly(gpu):
     x, w, sizes = workloads.c1(gpu)
     xq, xs = mxfp8gg.to_mxfp8_dim0(x)
@@ -521,6 +546,36 @@ def test_wgrad_feature_counts_off_the_8_grid(gpu, N, K, out_dtype, split):
             assert torch.all(dw[g] == 0)
         else:
             assert_close_to_oracle(dw[g], ref[g])
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("split", [0, 128])
+@pytest.mark.parametrize("N,K", [(3, 1), (17, 18), (261, 259)])
+def test_wgrad_any_feature_count(gpu, N, K, out_dtype, split):
+    """dW rows of a K off the 4-element grid run at a padded row stride (the
+    strided entry) and come back contiguous, equal to the oracle; wgrad_fused
+    takes the same path."""
+    sizes = [64, 0, 160, 32]
+    M = sum(sizes)
+    go_q, go_s = _rand_q((N, M), gpu, 73)
+    ia_q, ia_s = _rand_q((K, M), gpu, 74)
+    ends = workloads.ends_of(sizes)
+    args = (go_q.view(torch.float8_e4m3fn), ia_q.view(torch.float8_e4m3fn),
+            torch.from_numpy(ends).to(gpu), go_s, ia_s)
+    dw = ops.grouped_wgrad(*args, out_dtype=out_dtype, split_tokens=split)
+    assert dw.shape == (len(sizes), N, K) and dw.is_contiguous()
+    ref = O.grouped_wgrad(u8(go_q), u8(go_s), u8(ia_q), u8(ia_s), ends)
+    for g, s in enumerate(sizes):
+        if s == 0:
+            assert torch.all(dw[g] == 0)
+        else:
+            assert_close_to_oracle(dw[g], ref[g])
+    if split == 0:
+        dw2 = wgrad_fused.wgrad_fused(*args, out_dtype=out_dtype, offs_kind="ends")
+        assert dw2.shape == dw.shape and dw2.is_contiguous()
+        for g, s in enumerate(sizes):
+            if s:
+                assert_close_to_oracle(dw2[g], ref[g])
 
 
 @pytest.mark.parametrize("sizes,split", [([1024, 0, 2976, 96], 256), ([4096, 4096], 1024),
