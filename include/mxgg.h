@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MXGG_ABI_VERSION 12
+#define MXGG_ABI_VERSION 13
 
 typedef enum mxgg_status {
   MXGG_OK = 0,
@@ -471,6 +471,23 @@ int mxgg_grouped_wgrad_strided(const void* go_t, int64_t ldgo, const void* go_sc
 int mxgg_route_plan(const int32_t* expert_idx, int64_t tokens, int64_t topk, int64_t num_experts,
                     int64_t pad_multiple, int64_t rows_cap, int32_t* perm, int32_t* src,
                     int32_t* group_ends, int32_t* counts, void* stream);
+
+/*
+ * The same plan over many workgroups (one per 4096 slots: a count kernel, one
+ * small offsets kernel, a rank kernel), with a caller-owned workspace of at
+ * least mxgg_route_plan_workspace_bytes(tokens, topk, num_experts) bytes
+ * (4-byte aligned, no initialisation; NULL when that is 0).  Same outputs, bit
+ * for bit, as mxgg_route_plan (the stable order is unique); spreading the
+ * scattered src stores over many compute units makes it the faster form past
+ * a few thousand slots.  Same reference interface as mxgg_route_plan
+ * (port_mxfp8.py:214, 240).  Calls that share a workspace must be ordered on
+ * one stream.  The size query returns -1 for invalid arguments.
+ */
+int64_t mxgg_route_plan_workspace_bytes(int64_t tokens, int64_t topk, int64_t num_experts);
+int mxgg_route_plan_ws(const int32_t* expert_idx, int64_t tokens, int64_t topk,
+                       int64_t num_experts, int64_t pad_multiple, int64_t rows_cap, int32_t* perm,
+                       int32_t* src, int32_t* group_ends, int32_t* counts, void* workspace,
+                       int64_t workspace_bytes, void* stream);
 
 /*
  * Routed rows in bf16: out[r] = x[src[r] / topk] for src[r] >= 0, times

@@ -817,9 +817,11 @@ int mxgg_grouped_wgrad_strided(const void* go_t, int64_t ldgo, const void* go_sc
 // ---------------------------------------------------------------------------
 // Token routing.
 // ---------------------------------------------------------------------------
-int mxgg_route_plan(const int32_t* expert_idx, int64_t tokens, int64_t topk, int64_t num_experts,
-                    int64_t pad_multiple, int64_t rows_cap, int32_t* perm, int32_t* src,
-                    int32_t* group_ends, int32_t* counts, void* stream) {
+// Argument checks shared by both route-plan entries (0 when valid).
+static int check_route_plan(const int32_t* expert_idx, int64_t tokens, int64_t topk,
+                            int64_t num_experts, int64_t pad_multiple, int64_t rows_cap,
+                            const int32_t* perm, const int32_t* src, const int32_t* group_ends,
+                            const int32_t* counts) {
   if (tokens < 0 || topk < 1 || rows_cap < 0)
     return set_error(MXGG_ERR_SHAPE, "route_plan: tokens=%lld, topk=%lld, rows_cap=%lld",
                      (long long)tokens, (long long)topk, (long long)rows_cap);
@@ -840,10 +842,47 @@ int mxgg_route_plan(const int32_t* expert_idx, int64_t tokens, int64_t topk, int
     return set_error(MXGG_ERR_UNSUPPORTED, "route_plan: rows_cap above 2^31");
   if (!group_ends || !counts || (n > 0 && (!expert_idx || !perm)) || (rows_cap > 0 && !src))
     return set_error(MXGG_ERR_INVALID_ARGUMENT, "route_plan: null pointer");
-  return check_launch(launch_route_plan(expert_idx, n, (int)num_experts, (int)pad_multiple,
-                                        rows_cap, perm, src, group_ends, counts,
+  return MXGG_OK;
+}
+
+int mxgg_route_plan(const int32_t* expert_idx, int64_t tokens, int64_t topk, int64_t num_experts,
+                    int64_t pad_multiple, int64_t rows_cap, int32_t* perm, int32_t* src,
+                    int32_t* group_ends, int32_t* counts, void* stream) {
+  const int rc = check_route_plan(expert_idx, tokens, topk, num_experts, pad_multiple, rows_cap,
+                                  perm, src, group_ends, counts);
+  if (rc != MXGG_OK) return rc;
+  return check_launch(launch_route_plan(expert_idx, tokens * topk, (int)num_experts,
+                                        (int)pad_multiple, rows_cap, perm, src, group_ends, counts,
                                         static_cast<hipStream_t>(stream)),
                       "route_plan");
+}
+
+int64_t mxgg_route_plan_workspace_bytes(int64_t tokens, int64_t topk, int64_t num_experts) {
+  if (tokens < 0 || topk < 1 || num_experts < 1 || num_experts > kMaxGroupsAbi ||
+      tokens > INT32_MAX / topk)
+    return -1;
+  return route_plan_blocks(tokens * topk) * num_experts * 4;
+}
+
+int mxgg_route_plan_ws(const int32_t* expert_idx, int64_t tokens, int64_t topk,
+                       int64_t num_experts, int64_t pad_multiple, int64_t rows_cap, int32_t* perm,
+                       int32_t* src, int32_t* group_ends, int32_t* counts, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+  const int rc = check_route_plan(expert_idx, tokens, topk, num_experts, pad_multiple, rows_cap,
+                                  perm, src, group_ends, counts);
+  if (rc != MXGG_OK) return rc;
+  const int64_t need = mxgg_route_plan_workspace_bytes(tokens, topk, num_experts);
+  if (workspace_bytes < need)
+    return set_error(MXGG_ERR_SHAPE, "route_plan_ws: workspace of %lld bytes, %lld needed",
+                     (long long)workspace_bytes, (long long)need);
+  if (need > 0 && (!workspace || reinterpret_cast<uintptr_t>(workspace) % 4 != 0))
+    return set_error(workspace ? MXGG_ERR_ALIGNMENT : MXGG_ERR_INVALID_ARGUMENT,
+                     "route_plan_ws: the workspace must be a 4-byte aligned device buffer");
+  return check_launch(launch_route_plan_blocks(expert_idx, tokens * topk, (int)num_experts,
+                                               (int)pad_multiple, rows_cap, perm, src, group_ends,
+                                               counts, static_cast<int32_t*>(workspace),
+                                               static_cast<hipStream_t>(stream)),
+                      "route_plan_ws");
 }
 
 // Rows of 16-byte bf16 chunks: cols % 8 == 0, 16-byte aligned bases and strides.

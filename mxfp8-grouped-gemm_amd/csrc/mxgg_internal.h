@@ -95,6 +95,12 @@ hipError_t launch_gather_quant_dim0(const uint16_t* x, int64_t xrows, int64_t ld
 hipError_t launch_route_plan(const int32_t* idx, int64_t n, int E, int pad, int64_t cap,
                              int32_t* perm, int32_t* src, int32_t* ends, int32_t* counts,
                              hipStream_t stream);
+// The same plan over route_plan_blocks(n) workgroups, with a workspace of
+// route_plan_blocks(n) * E int32 (no initialisation).
+int64_t route_plan_blocks(int64_t n);
+hipError_t launch_route_plan_blocks(const int32_t* idx, int64_t n, int E, int pad, int64_t cap,
+                                    int32_t* perm, int32_t* src, int32_t* ends, int32_t* counts,
+                                    int32_t* ws, hipStream_t stream);
 hipError_t launch_gather_rows(const uint16_t* x, int64_t ldx, int64_t xrows, const int32_t* src,
                               int topk, const float* row_scale, int64_t rows, int64_t cols,
                               uint16_t* out, int64_t ldo, hipStream_t stream);

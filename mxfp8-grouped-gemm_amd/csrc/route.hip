@@ -13,12 +13,14 @@
 // pad_multiple = 32 (port_mxfp8.py:214, 240), which sorts slots with a stable
 // argsort of the expert ids; this is the same order.
 //
-// The plan is one workgroup of 1024 threads (16 waves), so no grid-wide
-// synchronisation and no host round trip are needed: each wave counts the
-// experts of a contiguous slot range into its own LDS histogram, one thread
-// per expert turns the histograms into per-wave starting rows, and each wave
-// then walks its range again in 64-slot chunks, ranking equal experts inside
-// a chunk with one ballot per key bit.
+// One form of the plan is one workgroup of 1024 threads (16 waves), so no
+// grid-wide synchronisation and no host round trip are needed: each wave
+// counts the experts of a contiguous slot range into its own LDS histogram,
+// one thread per expert turns the histograms into per-wave starting rows, and
+// each wave then walks its range again in 64-slot chunks, ranking equal
+// experts inside a chunk with one ballot per key bit.  The other form runs the
+// same steps over one workgroup per 4096 slots, with the per-workgroup counts
+// in a caller's workspace and one small kernel between the two passes.
 //
 // Combine: out[t] = bf16(sum_k float(bf16(float(y[perm[s]]) * score[s]))),
 // summed in fp32 in k order (the routed output scaled by its score and rounded
@@ -47,25 +49,12 @@ __device__ __forceinline__ uint64_t match_key(uint32_t key, int nbits) {
   return m;
 }
 
-__global__ __launch_bounds__(kPlanThreads) void k_route_plan(
-    const int32_t* __restrict__ idx, int64_t n, int E, int pad, int64_t cap,
-    int32_t* __restrict__ perm, int32_t* __restrict__ src, int32_t* __restrict__ ends,
-    int32_t* __restrict__ counts) {
-  __shared__ int32_t hist[kPlanWaves * kMaxGroups];  // [wave][expert]
-  __shared__ int32_t scan[kPlanThreads];
-  __shared__ int32_t total_s;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = tid >> 6;
-  for (int i = tid; i < kPlanWaves * E; i += kPlanThreads) hist[i] = 0;
-  __syncthreads();
-
-  // Slot range of wave w: [beg, end), chunk-aligned.
-  const int64_t per = ((n + kPlanWaves - 1) / kPlanWaves + 63) / 64 * 64;
-  const int64_t beg = std::min<int64_t>((int64_t)w * per, n);
-  const int64_t end = std::min<int64_t>(beg + per, n);
-  int32_t* h = hist + w * E;
-  // the ids of 8 chunks are loaded together, so 8 loads are in flight
+// Counts the experts of slots [beg, end) of a wave into the LDS histogram h
+// (ids outside [0, E) are not counted); the ids of kPlanPrefetch 64-slot
+// chunks are loaded together, so that many loads are in flight.
+__device__ __forceinline__ void count_range(const int32_t* __restrict__ idx, int64_t beg,
+                                            int64_t end, int E, int32_t* h) {
+  const int lane = threadIdx.x & 63;
   for (int64_t b0 = beg; b0 < end; b0 += 64 * kPlanPrefetch) {
     int32_t ev[kPlanPrefetch];
 #pragma unroll
@@ -77,39 +66,18 @@ __global__ __launch_bounds__(kPlanThreads) void k_route_plan(
     for (int j = 0; j < kPlanPrefetch; ++j)
       if (ev[j] >= 0 && ev[j] < E) atomicAdd(&h[ev[j]], 1);
   }
-  __syncthreads();
+}
 
-  // Per expert: starting rank of each wave, the count, the padded size.
-  int32_t cnt = 0, padded = 0;
-  if (tid < E) {
-    for (int v = 0; v < kPlanWaves; ++v) {
-      const int32_t c = hist[v * E + tid];
-      hist[v * E + tid] = cnt;
-      cnt += c;
-    }
-    padded = (cnt + pad - 1) / pad * pad;
-  }
-  // exclusive scan of the padded sizes over experts
-  scan[tid] = padded;
-  __syncthreads();
-  for (int off = 1; off < kPlanThreads; off <<= 1) {
-    const int32_t add = tid >= off ? scan[tid - off] : 0;
-    __syncthreads();
-    scan[tid] += add;
-    __syncthreads();
-  }
-  const int32_t start = scan[tid] - padded;
-  if (tid < E) {
-    ends[tid] = scan[tid];
-    counts[tid] = cnt;
-    for (int v = 0; v < kPlanWaves; ++v) hist[v * E + tid] += start;
-    for (int32_t r = start + cnt; r < start + padded; ++r) src[r] = -1;
-  }
-  if (tid == E - 1) total_s = scan[tid];
-  __syncthreads();
-  for (int64_t r = (int64_t)total_s + tid; r < cap; r += kPlanThreads) src[r] = -1;
-
-  // Ranks: keys 0..E-1 are experts, E marks a dropped or absent slot.
+// Ranks slots [beg, end) of a wave in slot order, 64 at a time: h[e] holds
+// the next row of expert e for this wave and advances by the slots of e in
+// each chunk, which are ranked among themselves with one ballot per key bit.
+// Writes perm[s] (-1 for a dropped slot) and src[row].
+__device__ __forceinline__ void rank_range(const int32_t* __restrict__ idx, int64_t beg,
+                                           int64_t end, int E, int32_t* h, int64_t cap,
+                                           int32_t* __restrict__ perm,
+                                           int32_t* __restrict__ src) {
+  const int lane = threadIdx.x & 63;
+  // keys 0..E-1 are experts, E marks a dropped or absent slot
   const int nbits = 32 - __builtin_clz((unsigned)E);
   for (int64_t b0 = beg; b0 < end; b0 += 64 * kPlanPrefetch) {
     int32_t ev[kPlanPrefetch];
@@ -139,6 +107,131 @@ __global__ __launch_bounds__(kPlanThreads) void k_route_plan(
       }
     }
   }
+}
+
+// Per expert, from the slot counts of the nv consecutive histograms
+// hist[v * E + e]: each histogram's first row (exclusive prefix plus the
+// expert's padded start), the group ends, the counts, and -1 in src for the
+// padding rows and every row past the last group up to cap.  One workgroup of
+// kPlanThreads >= E threads; every thread calls it.
+__device__ void plan_offsets(int32_t* hist, int nv, int E, int pad, int64_t cap,
+                             int32_t* __restrict__ src, int32_t* __restrict__ ends,
+                             int32_t* __restrict__ counts, int32_t* scan, int32_t* total_s) {
+  const int tid = threadIdx.x;
+  int32_t cnt = 0, padded = 0;
+  if (tid < E) {
+    for (int v = 0; v < nv; ++v) {
+      const int32_t c = hist[(int64_t)v * E + tid];
+      hist[(int64_t)v * E + tid] = cnt;
+      cnt += c;
+    }
+    padded = (cnt + pad - 1) / pad * pad;
+  }
+  // exclusive scan of the padded sizes over experts
+  scan[tid] = padded;
+  __syncthreads();
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const int32_t add = tid >= off ? scan[tid - off] : 0;
+    __syncthreads();
+    scan[tid] += add;
+    __syncthreads();
+  }
+  const int32_t start = scan[tid] - padded;
+  if (tid < E) {
+    ends[tid] = scan[tid];
+    counts[tid] = cnt;
+    for (int v = 0; v < nv; ++v) hist[(int64_t)v * E + tid] += start;
+    for (int32_t r = start + cnt; r < start + padded; ++r) src[r] = -1;
+  }
+  if (tid == E - 1) *total_s = scan[tid];
+  __syncthreads();
+  for (int64_t r = (int64_t)*total_s + tid; r < cap; r += kPlanThreads) src[r] = -1;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void k_route_plan(
+    const int32_t* __restrict__ idx, int64_t n, int E, int pad, int64_t cap,
+    int32_t* __restrict__ perm, int32_t* __restrict__ src, int32_t* __restrict__ ends,
+    int32_t* __restrict__ counts) {
+  __shared__ int32_t hist[kPlanWaves * kMaxGroups];  // [wave][expert]
+  __shared__ int32_t scan[kPlanThreads];
+  __shared__ int32_t total_s;
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  for (int i = tid; i < kPlanWaves * E; i += kPlanThreads) hist[i] = 0;
+  __syncthreads();
+  // Slot range of wave w: [beg, end), chunk-aligned.
+  const int64_t per = ((n + kPlanWaves - 1) / kPlanWaves + 63) / 64 * 64;
+  const int64_t beg = std::min<int64_t>((int64_t)w * per, n);
+  const int64_t end = std::min<int64_t>(beg + per, n);
+  count_range(idx, beg, end, E, hist + w * E);
+  __syncthreads();
+  plan_offsets(hist, kPlanWaves, E, pad, cap, src, ends, counts, scan, &total_s);
+  rank_range(idx, beg, end, E, hist + w * E, cap, perm, src);
+}
+
+// The same plan over many workgroups, for the stores of routings past a few
+// thousand slots (one workgroup writes perm and src at one CU's store rate):
+// block b of the grid owns slots [b * kPlanBlockSlots, ...).
+//   k_plan_count : the block's expert counts into ws[b][e] (global memory);
+//   k_plan_offsets (one workgroup): ws[b][e] becomes the block's first row of
+//                  expert e; group ends, counts and the -1 rows of src;
+//   k_plan_rank  : the block's waves count their quarter-ranges again, take
+//                  their first rows from ws[b][*] plus the waves before them,
+//                  and rank as the one-workgroup plan does.
+// The result is the one-workgroup plan's, bit for bit: both are the stable
+// order by expert, which is unique.
+constexpr int kPlanBlockThreads = 512;
+constexpr int kPlanBlockWaves = kPlanBlockThreads / 64;
+constexpr int64_t kPlanBlockSlots = 4096;
+
+__global__ __launch_bounds__(kPlanBlockThreads) void k_plan_count(
+    const int32_t* __restrict__ idx, int64_t n, int E, int32_t* __restrict__ ws) {
+  __shared__ int32_t hist[kMaxGroups];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < E; i += kPlanBlockThreads) hist[i] = 0;
+  __syncthreads();
+  const int64_t lo = (int64_t)blockIdx.x * kPlanBlockSlots;
+  const int64_t hi = std::min<int64_t>(lo + kPlanBlockSlots, n);
+  const int64_t per = kPlanBlockSlots / kPlanBlockWaves;
+  const int64_t beg = std::min<int64_t>(lo + (int64_t)(tid >> 6) * per, hi);
+  count_range(idx, beg, std::min<int64_t>(beg + per, hi), E, hist);
+  __syncthreads();
+  for (int i = tid; i < E; i += kPlanBlockThreads) ws[(int64_t)blockIdx.x * E + i] = hist[i];
+}
+
+__global__ __launch_bounds__(kPlanThreads) void k_plan_offsets(
+    int32_t* __restrict__ ws, int nblocks, int E, int pad, int64_t cap,
+    int32_t* __restrict__ src, int32_t* __restrict__ ends, int32_t* __restrict__ counts) {
+  __shared__ int32_t scan[kPlanThreads];
+  __shared__ int32_t total_s;
+  plan_offsets(ws, nblocks, E, pad, cap, src, ends, counts, scan, &total_s);
+}
+
+__global__ __launch_bounds__(kPlanBlockThreads) void k_plan_rank(
+    const int32_t* __restrict__ idx, int64_t n, int E, int64_t cap,
+    const int32_t* __restrict__ ws, int32_t* __restrict__ perm, int32_t* __restrict__ src) {
+  __shared__ int32_t hist[kPlanBlockWaves * kMaxGroups];  // [wave][expert]
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  for (int i = tid; i < kPlanBlockWaves * E; i += kPlanBlockThreads) hist[i] = 0;
+  __syncthreads();
+  const int64_t lo = (int64_t)blockIdx.x * kPlanBlockSlots;
+  const int64_t hi = std::min<int64_t>(lo + kPlanBlockSlots, n);
+  const int64_t per = kPlanBlockSlots / kPlanBlockWaves;
+  const int64_t beg = std::min<int64_t>(lo + (int64_t)w * per, hi);
+  const int64_t end = std::min<int64_t>(beg + per, hi);
+  count_range(idx, beg, end, E, hist + w * E);
+  __syncthreads();
+  for (int e = tid; e < E; e += kPlanBlockThreads) {
+    int32_t row = ws[(int64_t)blockIdx.x * E + e];
+    for (int v = 0; v < kPlanBlockWaves; ++v) {
+      const int32_t c = hist[v * E + e];
+      hist[v * E + e] = row;
+      row += c;
+    }
+  }
+  __syncthreads();
+  rank_range(idx, beg, end, E, hist + w * E, cap, perm, src);
 }
 
 // One wave per output row; lane l handles the 16-byte chunks l, l + 64, ...
@@ -294,6 +387,27 @@ hipError_t launch_route_plan(const int32_t* idx, int64_t n, int E, int pad, int6
                              hipStream_t stream) {
   hipLaunchKernelGGL(k_route_plan, dim3(1), dim3(kPlanThreads), 0, stream, idx, n, E, pad, cap,
                      perm, src, ends, counts);
+  return hipGetLastError();
+}
+
+int64_t route_plan_blocks(int64_t n) { return (n + kPlanBlockSlots - 1) / kPlanBlockSlots; }
+
+hipError_t launch_route_plan_blocks(const int32_t* idx, int64_t n, int E, int pad, int64_t cap,
+                                    int32_t* perm, int32_t* src, int32_t* ends, int32_t* counts,
+                                    int32_t* ws, hipStream_t stream) {
+  const int64_t nb = route_plan_blocks(n);
+  if (nb > 0) {
+    hipLaunchKernelGGL(k_plan_count, dim3((unsigned)nb), dim3(kPlanBlockThreads), 0, stream, idx,
+                       n, E, ws);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  hipLaunchKernelGGL(k_plan_offsets, dim3(1), dim3(kPlanThreads), 0, stream, ws, (int)nb, E, pad,
+                     cap, src, ends, counts);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || nb == 0) return err;
+  hipLaunchKernelGGL(k_plan_rank, dim3((unsigned)nb), dim3(kPlanBlockThreads), 0, stream, idx, n,
+                     E, cap, ws, perm, src);
   return hipGetLastError();
 }
 

@@ -35,7 +35,7 @@ OFFS_ENDS = 0
 OFFS_SIZES = 1
 OFFS_AUTO = 2
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -111,6 +111,9 @@ SIGNATURES = {
          _I64, _P, _I64, _P],
     ),
     "mxgg_route_plan": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P]),
+    "mxgg_route_plan_workspace_bytes": (_I64, [_I64, _I64, _I64]),
+    "mxgg_route_plan_ws": (
+        _I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I64, _P]),
     "mxgg_gather_rows": (_I, [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P]),
     "mxgg_gather_quant_dual": (
         _I,

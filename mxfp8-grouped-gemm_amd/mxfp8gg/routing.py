@@ -5,8 +5,8 @@ dispatcher, swapped in with ``pad_multiple=32`` (port_mxfp8.py:214, 240):
 the (token, k) slots are sorted by expert with a stable argsort, the routed
 input is ``x[sorted_slots // topk]`` with every expert's rows padded to a
 multiple of 32, and the experts' output is scaled by the routing score and
-scattered back to token order.  Here the plan is computed on the device by one
-kernel (no host sync), the gather is fused into the MXFP8 casts of the expert
+scattered back to token order.  Here the plan is computed on the device by
+three small kernels (no host sync), the gather is fused into the MXFP8 casts of the expert
 input (the bf16 routed copy is never written), and the combine sums the top-k
 terms in fp32 and rounds once.
 
@@ -75,10 +75,16 @@ def route_plan(expert_idx: torch.Tensor, num_experts: int, pad_multiple: int = 3
     offs = torch.empty(num_experts, dtype=torch.int32, device=dev)
     counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
     lib = _lib.load()
+    # the many-workgroup form (one workgroup per 4096 slots); its workspace
+    # holds a count per (workgroup, expert)
+    nbytes = int(lib.mxgg_route_plan_workspace_bytes(T, K, num_experts))
+    if nbytes < 0:
+        raise ValueError(f"route_plan: invalid shape tokens={T}, topk={K}, experts={num_experts}")
+    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=dev)
     _lib.check(
-        lib.mxgg_route_plan(idx.data_ptr(), T, K, num_experts, pad_multiple, rows,
-                            perm.data_ptr(), src.data_ptr(), offs.data_ptr(), counts.data_ptr(),
-                            _stream_ptr(idx)),
+        lib.mxgg_route_plan_ws(idx.data_ptr(), T, K, num_experts, pad_multiple, rows,
+                               perm.data_ptr(), src.data_ptr(), offs.data_ptr(),
+                               counts.data_ptr(), ws.data_ptr(), nbytes, _stream_ptr(idx)),
         "route_plan",
     )
     return RoutePlan(perm, src, ops._mark_ends(offs), counts, T, K, num_experts, pad_multiple)

@@ -483,6 +483,30 @@ def test_route_plan_rejects(lib, kw, status):
     assert _route(lib, **kw) == status
 
 
+def test_route_plan_workspace_size(lib):
+    # one int32 count per (workgroup of 4096 slots, expert); -1 when invalid
+    assert lib.mxgg_route_plan_workspace_bytes(16384, 8, 32) == 32 * 32 * 4
+    assert lib.mxgg_route_plan_workspace_bytes(4097, 1, 3) == 2 * 3 * 4
+    assert lib.mxgg_route_plan_workspace_bytes(0, 2, 4) == 0
+    assert lib.mxgg_route_plan_workspace_bytes(64, 0, 4) == -1
+    assert lib.mxgg_route_plan_workspace_bytes(64, 2, 1025) == -1
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(E=0), _lib.ERR_UNSUPPORTED),                  # the shared checks come first
+    (dict(ws=None), _lib.ERR_INVALID_ARGUMENT),
+    (dict(ws=FAKE + 2), _lib.ERR_ALIGNMENT),
+    (dict(nbytes=4), _lib.ERR_SHAPE),                   # 64 * 2 slots, 4 experts: 16 bytes
+])
+def test_route_plan_ws_rejects(lib, kw, status):
+    a = dict(idx=FAKE, T=64, K=2, E=4, pad=32, cap=128 + 4 * 31, perm=FAKE, src=FAKE, ends=FAKE,
+             counts=FAKE, ws=FAKE, nbytes=16)
+    a.update(kw)
+    assert lib.mxgg_route_plan_ws(a["idx"], a["T"], a["K"], a["E"], a["pad"], a["cap"], a["perm"],
+                                  a["src"], a["ends"], a["counts"], a["ws"], a["nbytes"],
+                                  None) == status
+
+
 def _gather(lib, **kw):
     a = dict(x=FAKE, T=16, cols=64, ldx=64, src=FAKE, K=2, scale=None, rows=40, out=FAKE, ldo=64)
     a.update(kw)

@@ -61,6 +61,35 @@ def test_route_plan_c5_routing(gpu):
     assert torch.equal(s.long(), order)
 
 
+@pytest.mark.parametrize("T,K,E,pad,drop", [
+    (2500, 8, 32, 32, True),       # 20000 slots: five workgroups, the last partial
+    (1200, 7, 1024, 64, True),     # every expert id range across three workgroups
+    (4097, 1, 3, 1, False),        # one slot past the first workgroup
+    (6000, 2, 1, 32, False)])      # one expert
+def test_route_plan_forms_agree(gpu, T, K, E, pad, drop):
+    """The many-workgroup plan (what route_plan runs) and the one-workgroup
+    entry write the same perm, src, ends and counts, and both equal the oracle."""
+    idx = _idx(gpu, T, K, E, 11 + T, drop)
+    plan = mxfp8gg.route_plan(idx, E, pad)
+    n = T * K
+    rows = n + E * (pad - 1)
+    perm = torch.full((n,), 7, dtype=torch.int32, device=gpu)
+    src = torch.full((rows,), 7, dtype=torch.int32, device=gpu)
+    ends = torch.empty(E, dtype=torch.int32, device=gpu)
+    counts = torch.empty(E, dtype=torch.int32, device=gpu)
+    lib = _lib.load()
+    _lib.check(lib.mxgg_route_plan(idx.data_ptr(), T, K, E, pad, rows, perm.data_ptr(),
+                                   src.data_ptr(), ends.data_ptr(), counts.data_ptr(),
+                                   torch.cuda.current_stream().cuda_stream), "route_plan")
+    assert torch.equal(plan.perm, perm) and torch.equal(plan.src, src)
+    assert torch.equal(plan.offs, ends) and torch.equal(plan.counts, counts)
+    r_perm, r_src, r_ends, r_counts = _plan_ref(idx, E, pad)
+    assert np.array_equal(perm.cpu().numpy(), r_perm)
+    assert np.array_equal(src.cpu().numpy(), r_src)
+    assert np.array_equal(ends.cpu().numpy(), r_ends)
+    assert np.array_equal(counts.cpu().numpy(), r_counts)
+
+
 @pytest.mark.parametrize("scaled", [False, True])
 def test_gather_rows_matches_oracle(gpu, scaled):
     T, K, E, H = 301, 3, 5, 96
