@@ -120,10 +120,14 @@ __device__ void plan_offsets(int32_t* hist, int nv, int E, int pad, int64_t cap,
   const int tid = threadIdx.x;
   int32_t cnt = 0, padded = 0;
   if (tid < E) {
-    for (int v = 0; v < nv; ++v) {
-      const int32_t c = hist[(int64_t)v * E + tid];
-      hist[(int64_t)v * E + tid] = cnt;
-      cnt += c;
+    // the expert's total first: loads only, 8 in flight (the workspace form
+    // reads them from global memory)
+    for (int v0 = 0; v0 < nv; v0 += 8) {
+      int32_t c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = v0 + j < nv ? hist[(int64_t)(v0 + j) * E + tid] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cnt += c[j];
     }
     padded = (cnt + pad - 1) / pad * pad;
   }
@@ -140,7 +144,19 @@ __device__ void plan_offsets(int32_t* hist, int nv, int E, int pad, int64_t cap,
   if (tid < E) {
     ends[tid] = scan[tid];
     counts[tid] = cnt;
-    for (int v = 0; v < nv; ++v) hist[(int64_t)v * E + tid] += start;
+    // each histogram's first row: the expert's start plus the counts before
+    // it (8 loads issued before their 8 stores)
+    int32_t row = start;
+    for (int v0 = 0; v0 < nv; v0 += 8) {
+      int32_t c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = v0 + j < nv ? hist[(int64_t)(v0 + j) * E + tid] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (v0 + j < nv) hist[(int64_t)(v0 + j) * E + tid] = row;
+        row += c[j];
+      }
+    }
     for (int32_t r = start + cnt; r < start + padded; ++r) src[r] = -1;
   }
   if (tid == E - 1) *total_s = scan[tid];
