@@ -281,6 +281,7 @@ __global__ __launch_bounds__(256) void k_gather_rows(
 // are the same for the whole wave) and every chunk's 8 row loads go out
 // together; the sum stays in k order.  More slots take the general loop.
 constexpr int kCombineSlots = 8;
+constexpr int kCombineChunks = 4;
 
 template <bool SCORES>
 __global__ __launch_bounds__(256) void k_combine(
@@ -301,28 +302,41 @@ __global__ __launch_bounds__(256) void k_combine(
       r[k] = rk >= 0 && rk < yrows ? rk : -1;
       sc[k] = SCORES && k < topk ? scores[t * topk + k] : 1.0f;
     }
-    for (int c = lane; c < chunks; c += 64) {
-      uint4 v[kCombineSlots];
+    // kCombineChunks chunks of every slot row per trip: their 32 loads go out
+    // together (C5: 430 -> 416 us against one chunk per trip)
+    for (int c0 = lane; c0 < chunks; c0 += 64 * kCombineChunks) {
+      uint4 v[kCombineChunks][kCombineSlots];
 #pragma unroll
-      for (int k = 0; k < kCombineSlots; ++k)
-        v[k] = r[k] >= 0 ? *reinterpret_cast<const uint4*>(y + (int64_t)r[k] * ldy + 8 * c)
-                         : make_uint4(0, 0, 0, 0);
-      float acc[8];
+      for (int u = 0; u < kCombineChunks; ++u) {
+        const int c = c0 + 64 * u;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-#pragma unroll
-      for (int k = 0; k < kCombineSlots; ++k) {
-        if (r[k] < 0) continue;
-        const uint4 w = SCORES ? scale_chunk(v[k], sc[k]) : v[k];
-        acc[0] += bf16_lo(w.x); acc[1] += bf16_hi(w.x);
-        acc[2] += bf16_lo(w.y); acc[3] += bf16_hi(w.y);
-        acc[4] += bf16_lo(w.z); acc[5] += bf16_hi(w.z);
-        acc[6] += bf16_lo(w.w); acc[7] += bf16_hi(w.w);
+        for (int k = 0; k < kCombineSlots; ++k)
+          v[u][k] = r[k] >= 0 && c < chunks
+                        ? *reinterpret_cast<const uint4*>(y + (int64_t)r[k] * ldy + 8 * c)
+                        : make_uint4(0, 0, 0, 0);
       }
-      // the combined rows are not read again here: streaming store (+2%)
-      __builtin_nontemporal_store(u32x4{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
-                                        pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7])},
-                                  reinterpret_cast<u32x4*>(o + 8 * c));
+#pragma unroll
+      for (int u = 0; u < kCombineChunks; ++u) {
+        const int c = c0 + 64 * u;
+        float acc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kCombineSlots; ++k) {
+          if (r[k] < 0) continue;
+          const uint4 w = SCORES ? scale_chunk(v[u][k], sc[k]) : v[u][k];
+          acc[0] += bf16_lo(w.x); acc[1] += bf16_hi(w.x);
+          acc[2] += bf16_lo(w.y); acc[3] += bf16_hi(w.y);
+          acc[4] += bf16_lo(w.z); acc[5] += bf16_hi(w.z);
+          acc[6] += bf16_lo(w.w); acc[7] += bf16_hi(w.w);
+        }
+        // the combined rows are not read again here: streaming store (+2%)
+        if (c < chunks)
+          __builtin_nontemporal_store(
+              u32x4{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
+                    pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7])},
+              reinterpret_cast<u32x4*>(o + 8 * c));
+      }
     }
     return;
   }
