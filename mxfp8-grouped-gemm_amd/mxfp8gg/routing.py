@@ -55,6 +55,11 @@ class RoutePlan(NamedTuple):
         return self.src.numel()
 
 
+# Routings of at most this many slots take the one-workgroup plan (a single
+# launch); larger ones the plan over one workgroup per 4096 slots.
+_PLAN_ONE_WORKGROUP_SLOTS = 4096
+
+
 def route_plan(expert_idx: torch.Tensor, num_experts: int, pad_multiple: int = 32) -> RoutePlan:
     """Sort the slots of ``expert_idx`` ([tokens, topk] integer expert ids on the
     GPU) by expert, stably, each expert's rows padded to ``pad_multiple``.
@@ -75,18 +80,28 @@ def route_plan(expert_idx: torch.Tensor, num_experts: int, pad_multiple: int = 3
     offs = torch.empty(num_experts, dtype=torch.int32, device=dev)
     counts = torch.empty(num_experts, dtype=torch.int32, device=dev)
     lib = _lib.load()
-    # the many-workgroup form (one workgroup per 4096 slots); its workspace
-    # holds a count per (workgroup, expert)
-    nbytes = int(lib.mxgg_route_plan_workspace_bytes(T, K, num_experts))
-    if nbytes < 0:
-        raise ValueError(f"route_plan: invalid shape tokens={T}, topk={K}, experts={num_experts}")
-    ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=dev)
-    _lib.check(
-        lib.mxgg_route_plan_ws(idx.data_ptr(), T, K, num_experts, pad_multiple, rows,
-                               perm.data_ptr(), src.data_ptr(), offs.data_ptr(),
-                               counts.data_ptr(), ws.data_ptr(), nbytes, _stream_ptr(idx)),
-        "route_plan",
-    )
+    if T * K <= _PLAN_ONE_WORKGROUP_SLOTS:
+        # one workgroup's worth of slots: one launch, no workspace
+        _lib.check(
+            lib.mxgg_route_plan(idx.data_ptr(), T, K, num_experts, pad_multiple, rows,
+                                perm.data_ptr(), src.data_ptr(), offs.data_ptr(),
+                                counts.data_ptr(), _stream_ptr(idx)),
+            "route_plan",
+        )
+    else:
+        # the many-workgroup form (one workgroup per 4096 slots); its
+        # workspace holds a count per (workgroup, expert)
+        nbytes = int(lib.mxgg_route_plan_workspace_bytes(T, K, num_experts))
+        if nbytes < 0:
+            raise ValueError(f"route_plan: invalid shape tokens={T}, topk={K}, "
+                             f"experts={num_experts}")
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _lib.check(
+            lib.mxgg_route_plan_ws(idx.data_ptr(), T, K, num_experts, pad_multiple, rows,
+                                   perm.data_ptr(), src.data_ptr(), offs.data_ptr(),
+                                   counts.data_ptr(), ws.data_ptr(), nbytes, _stream_ptr(idx)),
+            "route_plan",
+        )
     return RoutePlan(perm, src, ops._mark_ends(offs), counts, T, K, num_experts, pad_multiple)
 
 
