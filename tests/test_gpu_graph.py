@@ -106,3 +106,35 @@ def test_graph_of_routed_forward_only(gpu):
         e_out = mxfp8gg.moe_routed_ffn(x, idx, sc, wgu, wd)
         torch.cuda.synchronize()
         assert torch.equal(g_out.view(torch.int16), e_out.view(torch.int16))
+
+
+def test_graph_replays_route_plan_over_workgroups(gpu):
+    """The routing plan past 4096 slots (count, offsets and rank kernels with a
+    workspace from the graph's pool) captured once and replayed with new
+    expert ids written in place: every replay equals the eager plan."""
+    T, K, E = 1536, 8, 32                        # 12288 slots: three workgroups
+    gen = torch.Generator(device=gpu).manual_seed(5)
+    idx = torch.empty((T, K), dtype=torch.int32, device=gpu)
+
+    def new_idx():
+        idx.copy_(torch.randint(0, E, (T, K), generator=gen, device=gpu, dtype=torch.int32))
+
+    new_idx()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mxfp8gg.route_plan(idx, E)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        g = mxfp8gg.route_plan(idx, E)
+    for _ in range(3):
+        new_idx()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        e = mxfp8gg.route_plan(idx, E)
+        torch.cuda.synchronize()
+        for a, b in zip((g.perm, g.src, g.offs, g.counts), (e.perm, e.src, e.offs, e.counts)):
+            assert torch.equal(a, b)
